@@ -1,0 +1,224 @@
+"""Benchmark of one F rank's MoE layer on one MI355X.
+
+Default workload: hidden 4096, moe_intermediate 2048, 256 experts of which this rank owns
+[0, 64), top-8 uniform routing, one 16384-token dispatch, MXFP4 expert weights, bf16
+activations at the boundary (MXFP8 inside). A "step" is one expert call over that job
+(activation quantization, routing, grouped gate_up + SwiGLU, grouped down, finalize), with
+inputs and packed weights resident in HBM.
+
+Prints one JSON line: value = algorithmic TFLOPS (6 * H * I * Np per step, Np counted from
+the generated ids), plus tokens/s, per-layer latency, per-stage times from HIP events on the
+launch stream, the roofline of the dominant kernel (the gate_up GEMM) and the CPU baseline
+(the fp32 CPU oracle on a bounded sample of the same workload).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "sgl-afd-plugin_amd")]
+
+PEAK_TFLOPS = {"fp4": 10100.0, "fp8": 5000.0, "bf16": 2500.0}
+PEAK_HBM_GBS = 8000.0
+STAGES = ("quant", "route", "gate_up", "down", "finalize")
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
+    ap.add_argument("--cpu-sample-experts", type=int, default=16)
+    return ap.parse_args()
+
+
+def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
+    """The fp32 CPU oracle on a bounded sample: the first ``sample_tokens`` tokens of the
+    same seeded job, with only experts [0, sample_experts) treated as local (so the sample
+    keeps the per-pair work of the full layer). 1 warm-up + 3 timed reps, median."""
+    import numpy as np
+    import torch
+
+    from oracle import experts as OX
+    from oracle import formats as F
+    from sgl_asap_amd import workloads as W
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    gen = W.generator("cpu", 1)
+    x, ids, w = W.job(shape, n=sample_tokens, seed=0, device="cpu")
+    w13, w2 = W.expert_weights(sample_experts, shape.hidden, shape.inter, gen, "cpu")
+    if shape.fmt == "mxfp4":
+        c13, s13 = F.mx_quantize(w13.numpy(), "e2m1")
+        c2, s2 = F.mx_quantize(w2.numpy(), "e2m1")
+        w13d, w2d = F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1")
+        act = "mxfp8"
+    else:
+        c13, s13 = F.fp8_block_quantize_2d(w13.numpy())
+        c2, s2 = F.fp8_block_quantize_2d(w2.numpy())
+        w13d, w2d = F.fp8_block_dequantize_2d(c13, s13), F.fp8_block_dequantize_2d(c2, s2)
+        act = "fp8_1x128"
+    ids_np, w_np = ids.numpy(), w.numpy()
+    np_pairs = int(((ids_np >= 0) & (ids_np < sample_experts)).sum())
+    times = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        OX.moe_ffn(x, ids_np, w_np, w13d, w2d, 0, act=act)
+        dt = time.perf_counter() - t0
+        if rep:
+            times.append(dt)
+    t = statistics.median(times)
+    tflops = 6.0 * shape.hidden * shape.inter * np_pairs / t / 1e12
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"{sample_tokens} tokens of the same seeded job, experts [0,{sample_experts}) local "
+            f"({np_pairs} pairs), fp32 torch CPU oracle incl. act quant/routing/finalize; "
+            f"median of 3 reps = {t * 1e3:.1f} ms"
+        ),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one F rank's share of the experts on one GPU; --gpus {args.gpus} "
+            "is not supported (the path shards by expert range, one F rank per GPU, with no "
+            "collectives: run one process per GPU)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+
+    import torch
+
+    from sgl_asap_amd import _lib
+    from sgl_asap_amd import workloads as W
+    from sgl_asap_amd.moe.experts import AfdExperts, pack_fp8_block_experts, pack_mxfp4_experts
+
+    shape = W.SHAPES[args.config]
+    n = args.tokens or shape.tokens
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    x, ids, w = W.job(shape, n=n, seed=0, device=dev)
+    gen = W.generator(dev, 1)
+    w13, w2 = W.expert_weights(shape.num_local, shape.hidden, shape.inter, gen, dev)
+    pack = pack_mxfp4_experts if shape.fmt == "mxfp4" else pack_fp8_block_experts
+    weights = pack(w13, w2, device=dev)
+    del w13, w2
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n)
+    np_pairs = W.pair_count(ids, shape.local)
+    flops = W.flops(shape.hidden, shape.inter, np_pairs)
+    gate_up_flops = 4 * shape.hidden * shape.inter * np_pairs
+
+    stream = torch.cuda.current_stream()
+    out = torch.empty(n, shape.hidden, dtype=torch.bfloat16, device=dev)
+    ws = experts.workspace()
+    cfg, wst = experts.cfg, experts._wstruct
+    ids32, w32 = ids.to(torch.int32).contiguous(), w.to(torch.float32).contiguous()
+
+    def step(evs=None):
+        arr = None
+        if evs is not None:
+            arr = (ctypes.c_void_p * 6)(*[e.cuda_event for e in evs])
+        _lib.call(
+            "afd_moe_ffn_profiled", ctypes.byref(cfg), ctypes.byref(wst), x.data_ptr(), ids32.data_ptr(),
+            w32.data_ptr(), n, ws.data_ptr(), ws.numel(), out.data_ptr(), stream.cuda_stream, arr,
+        )
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # per-step stage events (recorded once first so their HIP handles exist)
+    ev_sets = []
+    for _ in range(args.steps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
+        for e in evs:
+            e.record(stream)
+        ev_sets.append(evs)
+    torch.cuda.synchronize()
+
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for k in range(args.steps):
+        step(ev_sets[k])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms = t_start.elapsed_time(t_end) / args.steps
+
+    stage_ms = {s: [] for s in STAGES}
+    for evs in ev_sets:
+        for i, s in enumerate(STAGES):
+            stage_ms[s].append(evs[i].elapsed_time(evs[i + 1]))
+    stage_avg = {s: round(sum(v) / len(v), 5) for s, v in stage_ms.items()}
+
+    tflops = flops / (ms * 1e-3) / 1e12
+    gu_ms = stage_avg["gate_up"]
+    gu_tflops = gate_up_flops / (gu_ms * 1e-3) / 1e12
+    issued = "fp8" if shape.fmt in ("mxfp4", "fp8_block") else "bf16"
+    result = {
+        "metric": "MoE-layer TFLOPS + tokens/s at 16k-token dispatch, 1 MI355X; MFMA util %",
+        "value": round(tflops, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "mxfp4xmxfp8" if shape.fmt == "mxfp4" else "fp8xfp8(block)",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) expert weights, random-init)",
+        "config": {
+            "workload": f"{shape.name}: one F rank, H={shape.hidden} I={shape.inter}, "
+            f"{shape.num_local} local of {shape.num_experts} experts, top-{shape.top_k}, "
+            f"{'uniform' if shape.zipf is None else f'Zipf({shape.zipf})'} routing, {n} tokens, {shape.fmt} weights",
+            "tokens": n,
+            "local_pairs": np_pairs,
+            "algorithmic_tflop": round(flops / 1e12, 4),
+        },
+        "tokens_per_s": round(n / (ms * 1e-3), 1),
+        "layer_latency_ms": round(ms, 4),
+        "mfma_util_vs_fp4_peak": round(tflops / PEAK_TFLOPS["fp4"], 4),
+        "mfma_util_vs_issued_peak": round(tflops / PEAK_TFLOPS[issued], 4),
+        "stages_ms": stage_avg,
+        "roofline": {
+            "kernel": "grouped gate_up GEMM + SwiGLU (mx_gemm_kernel<gate_up>)"
+            if shape.fmt == "mxfp4" else "grouped gate_up GEMM + SwiGLU (fp8_gemm_kernel<gate_up>)",
+            "bound": "mfma",
+            "achieved": round(gu_tflops, 2),
+            "peak": PEAK_TFLOPS["fp4"] if shape.fmt == "mxfp4" else PEAK_TFLOPS["fp8"],
+            "unit": "TFLOP/s",
+            "frac": round(gu_tflops / (PEAK_TFLOPS["fp4"] if shape.fmt == "mxfp4" else PEAK_TFLOPS["fp8"]), 4),
+            "frac_vs_issued_format_peak": round(gu_tflops / PEAK_TFLOPS[issued], 4),
+            "traffic": None,
+        },
+    }
+    if args.cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(shape, min(args.cpu_sample_tokens, n), min(args.cpu_sample_experts, shape.num_local))
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,183 @@
+/*
+ * afd.h - C ABI of the MI355X (gfx950) F-side routed-expert path of an attention-FFN
+ * disaggregated MoE deployment.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (as void*), only
+ * enqueues work on that stream (no host synchronisation, no allocation, no global mutable
+ * state besides the thread-local last HIP error) and returns 0 or a negative afd_status.
+ *
+ * Reference interfaces each group replaces (paths relative to the reference repository,
+ * P = python/sgl_asap_plugin):
+ *   afd_moe_ffn ................ the expert call FusedMoE(x, StandardTopKOutput(w, ids))
+ *                                at P/srt/managers/scheduler.py:410-412 and its graph form
+ *                                P/srt/model_executor/runner/ffn_cuda_graph_runner.py:60,65
+ *   afd_route .................. the routing/permutation stage inside that call
+ *                                (local_expert_offset / local_num_experts routing,
+ *                                P/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:87-93)
+ *   afd_quant_mxfp8 / _fp8_1x128 the activation quantizer quantize_routed_input
+ *                                (mxfp4_flashinfer_trtllm_moe.py:59-61)
+ *   afd_finalize ............... the finalize (top-k weighted sum, do_finalize=True,
+ *                                mxfp4_flashinfer_trtllm_moe.py:97)
+ *   afd_combine ................ AsapBuffer.recv's sum of partial outputs
+ *                                (P/srt/layers/moe/token_dispatcher/asap.py:174-184) fused
+ *                                with the shared-expert add (P/srt/batch_overlap/
+ *                                operations_strategy.py:106-111)
+ *   afd_pack_mxfp4 / _fp8_block  the quant methods' weight repack at load time
+ *                                (FlashInfer layout, mxfp4_flashinfer_trtllm_moe.py:11-13)
+ *   afd_copy_async ............. cu.memcpy_async (P/transport/cuda_wrapper.py, used at
+ *                                P/transport/channel.py:345-349, P/transport/server.py:347)
+ *   afd_stream_write64 ......... cu.write64 / write32 (cuda_wrapper.py:258-270; doorbell at
+ *                                channel.py:351-355, done flag at server.py:350)
+ *   afd_stream_wait64 .......... cu.wait32 (cuda_wrapper.py:258-270; channel.py:339,370)
+ *   afd_host_alloc / _free ..... the doorbell page of P/transport/memory.py:48-116
+ *                                (pinned host memory on one GPU)
+ */
+#ifndef AFD_H_
+#define AFD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AFD_ABI_VERSION 1
+
+typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
+
+/* Status codes. The Python layer maps them to the reference's exceptions. */
+enum afd_status {
+  AFD_OK = 0,
+  AFD_ERR_ARG = -1,         /* null pointer or out-of-range argument (ValueError) */
+  AFD_ERR_SHAPE = -2,       /* unsupported shape or alignment (ValueError) */
+  AFD_ERR_UNSUPPORTED = -3, /* unsupported format or configuration (NotImplementedError) */
+  AFD_ERR_HIP = -4,         /* a HIP call failed; afd_last_hip_error() has its hipError_t */
+  AFD_ERR_WORKSPACE = -5    /* the workspace is smaller than afd_workspace_layout().total */
+};
+
+/* Expert weight formats (the activation format follows from it). */
+enum afd_weight_fmt {
+  AFD_W_MXFP4 = 1,    /* E2M1 + UE8M0 per 32 along K; activations MXFP8 (e4m3 + UE8M0/32) */
+  AFD_W_FP8_BLOCK = 2 /* e4m3 + fp32 per 128x128; activations e4m3 + fp32 per 1x128 */
+};
+
+/* Stream-wait conditions, as HIP's hipStreamWaitValue flags. */
+enum afd_wait_cond { AFD_WAIT_GEQ = 0, AFD_WAIT_EQ = 1, AFD_WAIT_AND = 2, AFD_WAIT_NOR = 3 };
+
+/* Shape of one MoE layer on one F rank. Experts [expert_lo, expert_lo + num_local) are
+ * local; top-k ids are global expert ids; pairs with other ids are skipped.
+ * Limits: hidden a multiple of 256, inter a multiple of 128, num_local <= 256,
+ * topk <= 32, n <= 131071. */
+typedef struct afd_moe_cfg {
+  int32_t hidden;
+  int32_t inter;
+  int32_t topk;
+  int32_t expert_lo;
+  int32_t num_local;
+  int32_t weight_fmt; /* enum afd_weight_fmt */
+} afd_moe_cfg;
+
+/* Packed expert weights of one layer (device pointers), as afd_pack_* writes them:
+ *  MXFP4:     w13 u8 [E][2I][H/2], s13 u8 [E][2I][H/32], w2 u8 [E][H][I/2], s2 u8 [E][H][I/32];
+ *             element 2i in the low nibble; w13 rows interleave gate and up in groups of 32
+ *             (physical row 64j+q is gate row 32j+q for q < 32, else up row 32j+q-32).
+ *  FP8_BLOCK: w13 u8 [E][2I][H], s13 f32 [E][2I/128][H/128], w2 u8 [E][H][I],
+ *             s2 f32 [E][H/128][I/128]; w13 rows interleave gate and up in groups of 32 as
+ *             above, while s13 keeps logical block order (gate blocks, then up blocks). */
+typedef struct afd_expert_weights {
+  const void* w13;
+  const void* s13;
+  const void* w2;
+  const void* s2;
+} afd_expert_weights;
+
+/* Byte offsets of the internal buffers of afd_moe_ffn's workspace for n tokens. */
+typedef struct afd_ws_layout {
+  uint64_t total;          /* bytes the workspace must have */
+  uint64_t xq, xs;         /* quantized activations [n][H] and their scales */
+  uint64_t counts;         /* i32 [E] pairs per local expert */
+  uint64_t offsets;        /* i32 [E+1] exclusive prefix of counts */
+  uint64_t padded_offsets; /* i32 [E+1] the same with every segment padded to block_m */
+  uint64_t sorted_pairs;   /* i32 [np_max] flat pair index t*k+kk per padded row, -1 = pad */
+  uint64_t pair_pos;       /* i32 [n*k] padded row of each pair, -1 = not local */
+  uint64_t tile_expert;    /* i32 [max_tiles] local expert of each block_m row tile */
+  uint64_t num_tiles;      /* i32 [1] row tiles in use */
+  uint64_t hist;           /* i32 router scratch */
+  uint64_t hq, hs;         /* intermediate activations [np_max][I] and their scales */
+  uint64_t y;              /* bf16 [np_max][H] per-pair down outputs */
+  int64_t np_max;          /* padded rows reserved: n*k + E*(block_m-1), rounded up */
+  int32_t block_m;         /* row tile of the grouped GEMMs */
+  int32_t max_tiles;
+} afd_ws_layout;
+
+int afd_abi_version(void);
+const char* afd_status_string(int status);
+int afd_last_hip_error(void); /* hipError_t of the last AFD_ERR_HIP on this thread */
+
+int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_layout* out);
+
+/* ---- weight packing (load time) -------------------------------------------------------
+ * w: fp32 [mats][rows][cols] logical weights (for gate_up = 1: rows = 2I = [gate; up]). */
+int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols, int32_t gate_up,
+                   uint8_t* q, uint8_t* s, afd_stream_t stream);
+int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
+                       int32_t gate_up, uint8_t* q, float* s, afd_stream_t stream);
+
+/* ---- activation quantizers -------------------------------------------------------------
+ * x: bf16 [rows][cols]. MXFP8: q e4m3 [rows][cols], s u8 [rows][cols/32].
+ * FP8 1x128: q e4m3 [rows][cols], s f32 [rows][cols/128]. */
+int afd_quant_mxfp8(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, uint8_t* s,
+                    afd_stream_t stream);
+int afd_quant_fp8_1x128(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q, float* s,
+                        afd_stream_t stream);
+
+/* ---- routing ----------------------------------------------------------------------------
+ * ids: i32 [n][k]. Writes counts, offsets, padded_offsets, sorted_pairs, pair_pos,
+ * tile_expert and num_tiles at the offsets of `layout` inside ws (the layout of
+ * afd_workspace_layout for this n). Pairs of one expert keep ascending flat index. */
+int afd_route(const int32_t* ids, int32_t n, const afd_moe_cfg* cfg, void* ws,
+              uint64_t ws_bytes, afd_stream_t stream);
+
+/* ---- the expert call ---------------------------------------------------------------------
+ * out[t] = bf16(sum over local pairs (t, kk), kk ascending, of w[t,kk] * y(t,kk)) with
+ * y = W2_e . silu(Wg_e . x_t) * (Wu_e . x_t) under the format's quantizers; 0 for tokens
+ * with no local pair. x bf16 [n][H], ids i32 [n][k], w f32 [n][k], out bf16 [n][H]. */
+int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint16_t* x,
+                const int32_t* ids, const float* w, int32_t n, void* ws, uint64_t ws_bytes,
+                uint16_t* out, afd_stream_t stream);
+
+/* afd_moe_ffn with hipEvent_t handles recorded on `stream` around its stages:
+ * stage_events[0] before the activation quantizer, [1] after it, [2] after routing,
+ * [3] after gate_up, [4] after down, [5] after finalize. NULL entries are skipped.
+ * Same replaced interface as afd_moe_ffn; for the per-stage timing of JobTimer
+ * (P/srt/managers/scheduler.py:109-159). */
+int afd_moe_ffn_profiled(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                         const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
+                         void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream,
+                         void* const* stage_events);
+
+/* out[t] = bf16(sum_kk fp32(w[t,kk]) * fp32(y[pair_pos[t*k+kk]])) over pair_pos >= 0, each
+ * product and each sum rounded to fp32 separately, kk ascending. */
+int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w, int32_t n,
+                 int32_t k, int32_t hidden, uint16_t* out, afd_stream_t stream);
+
+/* A-side combine over num_parts (1..16) bf16 partial sums of numel elements:
+ * routed = bf16(sum_f fp32(part_f)) (a copy for one part); out = shared ? bf16(fp32(routed)
+ * + fp32(shared)) : routed. `parts` is a host array of device pointers. */
+int afd_combine(const uint16_t* const* parts, int32_t num_parts, const uint16_t* shared,
+                uint16_t* out, int64_t numel, afd_stream_t stream);
+
+/* ---- transport primitives (one GPU: producer and consumer streams) -------------------- */
+int afd_host_alloc(void** ptr, uint64_t bytes); /* pinned, coherent, zero-filled */
+int afd_host_free(void* ptr);
+int afd_copy_async(void* dst, const void* src, uint64_t bytes, afd_stream_t stream);
+int afd_stream_write64(afd_stream_t stream, uint64_t* addr, uint64_t value);
+int afd_stream_wait64(afd_stream_t stream, uint64_t* addr, uint64_t value, uint64_t mask,
+                      int32_t cond);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AFD_H_ */

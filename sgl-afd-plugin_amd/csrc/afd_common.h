@@ -1,0 +1,110 @@
+// Shared device helpers of the gfx950 expert path: number-format codecs (bit-exact with
+// the build's CPU oracle), vector types and launch-check macros.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/afd.h"
+
+namespace afd {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr float kE4m3Max = 448.0f;
+constexpr float kFp8Eps = 1e-10f;
+constexpr int kMxBlock = 32;
+constexpr int kFp8Block = 128;
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN (the rounding of torch's .to(bfloat16)).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// ---------------------------------------------------------------- e4m3fn (OCP FP8)
+// |v| <= 448 (callers clamp). Normals keep 3 significand bits, ties to even; below 2^-6
+// the code is rint(|v| * 2^9) subnormal steps.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 31) << 7;
+  uint32_t mag = u & 0x7fffffffu;
+  int e = static_cast<int>(mag >> 23) - 127;
+  uint32_t code;
+  if (e >= -6) {
+    uint32_t man = mag & 0x7fffffu;
+    uint32_t keep = man >> 20, rem = man & 0xfffffu;
+    uint32_t up = (rem > 0x80000u) | ((rem == 0x80000u) & (keep & 1u));
+    uint32_t m = keep + up;
+    code = (static_cast<uint32_t>(e + 7 + static_cast<int>(m >> 3)) << 3) | (m & 7u);
+  } else {
+    code = static_cast<uint32_t>(__builtin_rintf(__uint_as_float(mag) * 512.0f));
+  }
+  return code | sign;
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  uint32_t s = (c >> 7) & 1u, e = (c >> 3) & 15u, m = c & 7u;
+  float mag = e == 0 ? static_cast<float>(m) * (1.0f / 512.0f)
+                     : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return s ? -mag : mag;
+}
+
+// ---------------------------------------------------------------- E2M1 (fp4)
+// Input already divided by the block scale. Ties (.25 .75 1.25 1.75 2.5 3.5 5) go to
+// the even code; saturates at 6.
+__device__ __forceinline__ uint32_t f32_to_e2m1(float v) {
+  float a = fabsf(v);
+  uint32_t code = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) +
+                  (a >= 3.5f) + (a > 5.0f);
+  return code | ((__float_as_uint(v) >> 31) << 3);
+}
+
+// ---------------------------------------------------------------- MX (UE8M0 per 32) scale
+// Shared exponent floor(log2(amax)) - emax, clamped to [-127, 127]; amax == 0 -> code 0.
+__device__ __forceinline__ uint32_t mx_scale_code(float amax, int emax) {
+  if (amax == 0.0f) return 0u;
+  int exp32 = static_cast<int>((__float_as_uint(amax) >> 23) & 0xffu);
+  int e = exp32 > 0 ? exp32 - 127 : -127;
+  int code = e - emax + 127;
+  code = code < 0 ? 0 : (code > 254 ? 254 : code);
+  return static_cast<uint32_t>(code);
+}
+
+// 2^(127 - code) as an exact fp32 power of two (code <= 253).
+__device__ __forceinline__ float mx_inv_scale(uint32_t code) {
+  return __uint_as_float((254u - code) << 23);
+}
+
+__device__ __forceinline__ float clamp_e4m3(float v) {
+  return fminf(fmaxf(v, -kE4m3Max), kE4m3Max);
+}
+
+}  // namespace afd
+
+// Host-side helpers shared by the translation units.
+namespace afd {
+int set_hip_error(hipError_t e);  // records e for afd_last_hip_error(); returns AFD_ERR_HIP
+}
+
+#define AFD_CHECK_LAUNCH()                                 \
+  do {                                                     \
+    hipError_t _e = hipGetLastError();                     \
+    if (_e != hipSuccess) return afd::set_hip_error(_e);   \
+  } while (0)
+
+#define AFD_CHECK_HIP(expr)                                \
+  do {                                                     \
+    hipError_t _e = (expr);                                \
+    if (_e != hipSuccess) return afd::set_hip_error(_e);   \
+  } while (0)

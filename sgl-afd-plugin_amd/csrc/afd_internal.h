@@ -1,0 +1,33 @@
+// Declarations shared by the translation units of libafd (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/afd.h"
+
+namespace afd {
+
+constexpr int kMaxLocalExperts = 256;
+constexpr int kMaxTopk = 32;
+constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
+
+int launch_route(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
+                 const afd_ws_layout& L, hipStream_t stream);
+
+// Grouped MXFP4 GEMMs (afd_gemm_mx.hip).
+int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                      const afd_ws_layout& L, int32_t n, hipStream_t stream);
+int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                   const afd_ws_layout& L, int32_t n, hipStream_t stream);
+
+// Grouped FP8 128x128-block GEMMs (afd_gemm_fp8.hip).
+int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                       const afd_ws_layout& L, int32_t n, hipStream_t stream);
+int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                    const afd_ws_layout& L, int32_t n, hipStream_t stream);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+}  // namespace afd

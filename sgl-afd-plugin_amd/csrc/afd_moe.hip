@@ -1,0 +1,297 @@
+// The expert call of one job on one F rank (afd_moe_ffn), its workspace layout, the
+// finalize (top-k weighted sum) and the A-side combine.
+//
+//   quant x -> route -> grouped gate_up (+SwiGLU, +h quant) -> grouped down -> finalize
+//
+// finalize and combine are HBM-bound gathers with fixed summation order, so their results
+// are reproducible bit for bit (no atomics).
+#include <mutex>
+#include <vector>
+
+#include "afd_common.h"
+#include "afd_internal.h"
+
+namespace afd {
+
+static thread_local int g_last_hip_error = 0;
+
+int set_hip_error(hipError_t e) {
+  g_last_hip_error = static_cast<int>(e);
+  return AFD_ERR_HIP;
+}
+
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= static_cast<int>(cache.size())) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
+
+// ---------------------------------------------------------------- finalize
+constexpr int kFinThreads = 256;
+constexpr int kFinElems = 8;  // bf16 per lane = one 16-byte vector
+
+__global__ __launch_bounds__(kFinThreads) void finalize_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos,
+    const float* __restrict__ w, int k, int hidden, int col_blocks, uint16_t* __restrict__ out) {
+  // products and sums round separately: no contraction of w * y + acc into an fma
+#pragma clang fp contract(off)
+  const int64_t tok = blockIdx.x / col_blocks;
+  const int col = ((blockIdx.x % col_blocks) * kFinThreads + threadIdx.x) * kFinElems;
+  if (col >= hidden) return;
+  float acc[kFinElems];
+#pragma unroll
+  for (int i = 0; i < kFinElems; ++i) acc[i] = 0.0f;
+  for (int kk = 0; kk < k; ++kk) {
+    const int pos = pair_pos[tok * k + kk];
+    if (pos < 0) continue;
+    const float wk = w[tok * k + kk];
+    v4i raw = *reinterpret_cast<const v4i*>(y + int64_t(pos) * hidden + col);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t u = static_cast<uint32_t>(raw[i]);
+      const float p0 = wk * __uint_as_float(u << 16);
+      const float p1 = wk * __uint_as_float(u & 0xffff0000u);
+      acc[2 * i] = acc[2 * i] + p0;
+      acc[2 * i + 1] = acc[2 * i + 1] + p1;
+    }
+  }
+  v4i o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = static_cast<int>(uint32_t(f32_to_bf16(acc[2 * i])) |
+                            (uint32_t(f32_to_bf16(acc[2 * i + 1])) << 16));
+  *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
+}
+
+static int launch_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w,
+                           int32_t n, int32_t k, int32_t hidden, uint16_t* out,
+                           hipStream_t stream) {
+  if (n == 0) return AFD_OK;
+  const int col_blocks = (hidden / kFinElems + kFinThreads - 1) / kFinThreads;
+  hipLaunchKernelGGL(finalize_kernel, dim3(col_blocks * n), dim3(kFinThreads), 0, stream, y,
+                     pair_pos, w, k, hidden, col_blocks, out);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+// ---------------------------------------------------------------- combine
+constexpr int kMaxParts = 16;
+struct PartList {
+  const uint16_t* p[kMaxParts];
+};
+
+__global__ __launch_bounds__(256) void combine_kernel(PartList parts, int num_parts,
+                                                      const uint16_t* __restrict__ shared,
+                                                      uint16_t* __restrict__ out,
+                                                      int64_t vecs) {
+  for (int64_t v = blockIdx.x * int64_t(256) + threadIdx.x; v < vecs;
+       v += int64_t(gridDim.x) * 256) {
+    v4i first = reinterpret_cast<const v4i*>(parts.p[0])[v];
+    v4i res;
+    if (num_parts == 1) {
+      res = first;
+    } else {
+      float acc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t u = static_cast<uint32_t>(first[i]);
+        acc[2 * i] = __uint_as_float(u << 16);
+        acc[2 * i + 1] = __uint_as_float(u & 0xffff0000u);
+      }
+      for (int f = 1; f < num_parts; ++f) {
+        v4i r = reinterpret_cast<const v4i*>(parts.p[f])[v];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t u = static_cast<uint32_t>(r[i]);
+          acc[2 * i] = __fadd_rn(acc[2 * i], __uint_as_float(u << 16));
+          acc[2 * i + 1] = __fadd_rn(acc[2 * i + 1], __uint_as_float(u & 0xffff0000u));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        res[i] = static_cast<int>(uint32_t(f32_to_bf16(acc[2 * i])) |
+                                  (uint32_t(f32_to_bf16(acc[2 * i + 1])) << 16));
+    }
+    if (shared) {
+      v4i s = reinterpret_cast<const v4i*>(shared)[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t a = static_cast<uint32_t>(res[i]), b = static_cast<uint32_t>(s[i]);
+        float lo = __fadd_rn(__uint_as_float(a << 16), __uint_as_float(b << 16));
+        float hi = __fadd_rn(__uint_as_float(a & 0xffff0000u), __uint_as_float(b & 0xffff0000u));
+        res[i] = static_cast<int>(uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16));
+      }
+    }
+    reinterpret_cast<v4i*>(out)[v] = res;
+  }
+}
+
+// ---------------------------------------------------------------- configuration checks
+static int check_cfg(const afd_moe_cfg* cfg) {
+  if (!cfg) return AFD_ERR_ARG;
+  if (cfg->topk < 1 || cfg->topk > kMaxTopk || cfg->num_local < 1 ||
+      cfg->num_local > kMaxLocalExperts || cfg->expert_lo < 0)
+    return AFD_ERR_ARG;
+  if (cfg->hidden <= 0 || cfg->inter <= 0 || cfg->hidden % 256 || cfg->inter % 128)
+    return AFD_ERR_SHAPE;
+  if (cfg->weight_fmt != AFD_W_MXFP4 && cfg->weight_fmt != AFD_W_FP8_BLOCK)
+    return AFD_ERR_UNSUPPORTED;
+  return AFD_OK;
+}
+
+}  // namespace afd
+
+using namespace afd;
+
+extern "C" int afd_abi_version(void) { return AFD_ABI_VERSION; }
+
+extern "C" const char* afd_status_string(int status) {
+  switch (status) {
+    case AFD_OK: return "ok";
+    case AFD_ERR_ARG: return "invalid argument";
+    case AFD_ERR_SHAPE: return "unsupported shape or alignment";
+    case AFD_ERR_UNSUPPORTED: return "unsupported format or configuration";
+    case AFD_ERR_HIP: return "HIP runtime error";
+    case AFD_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int afd_last_hip_error(void) { return g_last_hip_error; }
+
+extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_layout* out) {
+  int st = check_cfg(cfg);
+  if (st != AFD_OK) return st;
+  if (!out || n < 0 || n > 0x1ffff) return AFD_ERR_ARG;
+  const int64_t H = cfg->hidden, I = cfg->inter, E = cfg->num_local;
+  const int64_t pairs = int64_t(n) * cfg->topk;
+  const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
+  const int64_t np_max = (pairs + E * (kBlockM - 1) + kBlockM - 1) / kBlockM * kBlockM;
+  uint64_t o = 0;
+  auto take = [&](uint64_t bytes) {
+    uint64_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  afd_ws_layout L;
+  L.xq = take(uint64_t(n) * H);
+  L.xs = take(mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
+  L.counts = take(E * 4);
+  L.offsets = take((E + 1) * 4);
+  L.padded_offsets = take((E + 1) * 4);
+  L.sorted_pairs = take(uint64_t(np_max) * 4);
+  L.pair_pos = take(uint64_t(pairs) * 4);
+  L.tile_expert = take(uint64_t(np_max / kBlockM) * 4);
+  L.num_tiles = take(4);
+  L.hist = take(uint64_t(128) * E * 4);
+  L.hq = take(uint64_t(np_max) * I);
+  L.hs = take(mx ? uint64_t(np_max) * (I / 32) : uint64_t(np_max) * (I / 128) * 4);
+  L.y = take(uint64_t(np_max) * H * 2);
+  L.total = o;
+  L.np_max = np_max;
+  L.block_m = kBlockM;
+  L.max_tiles = static_cast<int32_t>(np_max / kBlockM);
+  *out = L;
+  return AFD_OK;
+}
+
+static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                        const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
+                        void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream,
+                        void* const* ev) {
+  afd_ws_layout L;
+  int st = afd_workspace_layout(cfg, n, &L);
+  if (st != AFD_OK) return st;
+  if (!weights || !weights->w13 || !weights->s13 || !weights->w2 || !weights->s2)
+    return AFD_ERR_ARG;
+  if (n > 0 && (!x || !ids || !w || !out)) return AFD_ERR_ARG;
+  if (!ws) return AFD_ERR_ARG;
+  if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto mark = [&](int i) -> int {
+    if (ev && ev[i]) AFD_CHECK_HIP(hipEventRecord(static_cast<hipEvent_t>(ev[i]), s));
+    return AFD_OK;
+  };
+  if ((st = mark(0)) != AFD_OK) return st;
+  if (n > 0) {
+    uint8_t* wsb = static_cast<uint8_t*>(ws);
+    const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
+    if (mx)
+      st = afd_quant_mxfp8(x, n, cfg->hidden, wsb + L.xq, wsb + L.xs, stream);
+    else
+      st = afd_quant_fp8_1x128(x, n, cfg->hidden, wsb + L.xq,
+                               reinterpret_cast<float*>(wsb + L.xs), stream);
+    if (st != AFD_OK || (st = mark(1)) != AFD_OK) return st;
+    if ((st = launch_route(ids, n, *cfg, wsb, L, s)) != AFD_OK) return st;
+    if ((st = mark(2)) != AFD_OK) return st;
+    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, n, s)
+            : launch_fp8_gate_up(*cfg, *weights, wsb, L, n, s);
+    if (st != AFD_OK || (st = mark(3)) != AFD_OK) return st;
+    st = mx ? launch_mx_down(*cfg, *weights, wsb, L, n, s)
+            : launch_fp8_down(*cfg, *weights, wsb, L, n, s);
+    if (st != AFD_OK || (st = mark(4)) != AFD_OK) return st;
+    st = launch_finalize(reinterpret_cast<const uint16_t*>(wsb + L.y),
+                         reinterpret_cast<const int32_t*>(wsb + L.pair_pos), w, n, cfg->topk,
+                         cfg->hidden, out, s);
+    if (st != AFD_OK) return st;
+  } else {
+    for (int i = 1; i < 5; ++i)
+      if ((st = mark(i)) != AFD_OK) return st;
+  }
+  return mark(5);
+}
+
+extern "C" int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                           const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
+                           void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream) {
+  return moe_ffn_impl(cfg, weights, x, ids, w, n, ws, ws_bytes, out, stream, nullptr);
+}
+
+extern "C" int afd_moe_ffn_profiled(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                                    const uint16_t* x, const int32_t* ids, const float* w,
+                                    int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
+                                    afd_stream_t stream, void* const* stage_events) {
+  return moe_ffn_impl(cfg, weights, x, ids, w, n, ws, ws_bytes, out, stream, stage_events);
+}
+
+extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w,
+                            int32_t n, int32_t k, int32_t hidden, uint16_t* out,
+                            afd_stream_t stream) {
+  if (n < 0 || k < 1 || k > kMaxTopk) return AFD_ERR_ARG;
+  if (n > 0 && (!y || !pair_pos || !w || !out)) return AFD_ERR_ARG;
+  if (hidden <= 0 || hidden % kFinElems) return AFD_ERR_SHAPE;
+  return launch_finalize(y, pair_pos, w, n, k, hidden, out, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int afd_combine(const uint16_t* const* parts, int32_t num_parts,
+                           const uint16_t* shared, uint16_t* out, int64_t numel,
+                           afd_stream_t stream) {
+  if (!parts || !out || num_parts < 1 || num_parts > kMaxParts || numel < 0) return AFD_ERR_ARG;
+  if (numel % 8) return AFD_ERR_SHAPE;
+  PartList pl = {};
+  for (int f = 0; f < num_parts; ++f) {
+    if (!parts[f]) return AFD_ERR_ARG;
+    pl.p[f] = parts[f];
+  }
+  if (numel == 0) return AFD_OK;
+  const int64_t vecs = numel / 8;
+  int64_t grid = (vecs + 255) / 256;
+  if (grid > 4 * 2048) grid = 4 * 2048;
+  hipLaunchKernelGGL(combine_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), pl, num_parts, shared, out, vecs);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}

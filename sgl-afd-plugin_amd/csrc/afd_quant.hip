@@ -1,0 +1,266 @@
+// Quantizers of the expert path on gfx950: MXFP8 / FP8-1x128 activations and the load-time
+// MXFP4 / FP8-128x128 weight packers. All are HBM-bound streaming kernels: one lane owns one
+// 32-element MX block (16 B fp4 or 32 B fp8 out, 1 scale byte), so every load is a 16-byte
+// vector and no cross-lane reduction is needed for MX; FP8 groups of 128 reduce over 4 lanes.
+#include "afd_common.h"
+
+namespace afd {
+
+constexpr int kQuantThreads = 256;
+
+// Logical source row of physical row r when gate and up rows are interleaved in groups of g
+// (rows = 2I = [gate; up]): physical 2g*j + q is gate row g*j + q for q < g, else up row.
+__device__ __forceinline__ int64_t gate_up_source_row(int64_t r, int64_t rows, int g) {
+  int64_t j = r / (2 * g), q = r % (2 * g);
+  return q < g ? j * g + q : rows / 2 + j * g + (q - g);
+}
+
+// ---------------------------------------------------------------- MXFP8 activations
+__global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
+    const uint16_t* __restrict__ x, int64_t blocks, int cols, uint8_t* __restrict__ q,
+    uint8_t* __restrict__ s) {
+  const int bpr = cols / kMxBlock;
+  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
+       b += int64_t(gridDim.x) * kQuantThreads) {
+    int64_t row = b / bpr, cb = b % bpr;
+    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cb * kMxBlock);
+    v4i raw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) raw[i] = src[i];
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w = static_cast<uint32_t>(raw[i][j]);
+        v[i * 8 + j * 2] = __uint_as_float(w << 16);
+        v[i * 8 + j * 2 + 1] = __uint_as_float(w & 0xffff0000u);
+      }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    uint32_t code = mx_scale_code(amax, 8);
+    float inv = mx_inv_scale(code);
+    v4i out[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] * inv)) << (8 * j);
+      out[i / 4][i % 4] = static_cast<int>(packed);
+    }
+    v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cb * kMxBlock);
+    dst[0] = out[0];
+    dst[1] = out[1];
+    s[row * bpr + cb] = static_cast<uint8_t>(code);
+  }
+}
+
+// ---------------------------------------------------------------- FP8 1x128 activations
+// 4 consecutive lanes own one group of 128 (32 elements each); amax via two xor shuffles.
+__global__ __launch_bounds__(kQuantThreads) void quant_fp8_1x128_kernel(
+    const uint16_t* __restrict__ x, int64_t quarters, int cols, uint8_t* __restrict__ q,
+    float* __restrict__ s) {
+  const int qpr = cols / kMxBlock;  // quarter-groups per row
+  const int64_t stride = int64_t(gridDim.x) * kQuantThreads;
+  // all lanes of a wave iterate together so the shuffles see live partners
+  int64_t total = (quarters + stride - 1) / stride * stride;
+  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < total; b += stride) {
+    bool live = b < quarters;
+    int64_t bb = live ? b : 0;
+    int64_t row = bb / qpr, cq = bb % qpr;
+    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cq * kMxBlock);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v4i r = src[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t w = static_cast<uint32_t>(r[j]);
+        v[i * 8 + j * 2] = __uint_as_float(w << 16);
+        v[i * 8 + j * 2 + 1] = __uint_as_float(w & 0xffff0000u);
+      }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
+    if (!live) continue;
+    v4i out[2];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] / sc)) << (8 * j);
+      out[i / 4][i % 4] = static_cast<int>(packed);
+    }
+    v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cq * kMxBlock);
+    dst[0] = out[0];
+    dst[1] = out[1];
+    if ((cq & 3) == 0) s[row * (cols / kFp8Block) + cq / 4] = sc;
+  }
+}
+
+// ---------------------------------------------------------------- MXFP4 weight packer
+__global__ __launch_bounds__(kQuantThreads) void pack_mxfp4_kernel(
+    const float* __restrict__ w, int64_t blocks, int rows, int cols, int gate_up,
+    uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
+  const int bpr = cols / kMxBlock;
+  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
+       b += int64_t(gridDim.x) * kQuantThreads) {
+    int64_t prow = b / bpr;  // physical row over all matrices
+    int cb = static_cast<int>(b % bpr);
+    int64_t mat = prow / rows, r = prow % rows;
+    int64_t lr = gate_up ? gate_up_source_row(r, rows, 32) : r;
+    const v4f* src = reinterpret_cast<const v4f*>(w + (mat * rows + lr) * cols + cb * kMxBlock);
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v4f t = src[i];
+      v[i * 4] = t[0];
+      v[i * 4 + 1] = t[1];
+      v[i * 4 + 2] = t[2];
+      v[i * 4 + 3] = t[3];
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    uint32_t code = mx_scale_code(amax, 2);
+    float inv = mx_inv_scale(code);
+    v4i out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) packed |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
+      out[i] = static_cast<int>(packed);
+    }
+    *reinterpret_cast<v4i*>(q + prow * (cols / 2) + cb * 16) = out;
+    s[prow * bpr + cb] = static_cast<uint8_t>(code);
+  }
+}
+
+// Physical row of logical row lr when gate and up rows are interleaved in groups of g
+// (the inverse of gate_up_source_row).
+__device__ __forceinline__ int64_t gate_up_dest_row(int64_t lr, int64_t rows, int g) {
+  int64_t half = rows / 2;
+  return lr < half ? (lr / g) * 2 * g + lr % g : ((lr - half) / g) * 2 * g + g + (lr - half) % g;
+}
+
+// ---------------------------------------------------------------- FP8 128x128 weight packer
+// One workgroup per logical 128x128 block: amax over the block, then each lane quantizes 64
+// values. Scales stay in logical block order; with gate_up the codes land on the physical
+// rows of the 32-row gate/up interleave.
+__global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
+    const float* __restrict__ w, int rows, int cols, int gate_up, uint8_t* __restrict__ q,
+    float* __restrict__ s) {
+  __shared__ float red[kQuantThreads / 64];
+  const int rbs = rows / kFp8Block, cbs = cols / kFp8Block;
+  const int64_t blk = blockIdx.x;
+  const int64_t mat = blk / (int64_t(rbs) * cbs);
+  const int rb = static_cast<int>((blk / cbs) % rbs), cb = static_cast<int>(blk % cbs);
+  const int t = threadIdx.x;
+  // lane t: row t/2 of the block, 64 columns starting at (t%2)*64
+  const int br = t / 2, bc = (t % 2) * 64;
+  const int64_t lrow = int64_t(rb) * kFp8Block + br;
+  const int64_t prow = gate_up ? gate_up_dest_row(lrow, rows, 32) : lrow;
+  const float* src = w + (mat * rows + lrow) * cols + int64_t(cb) * kFp8Block + bc;
+  float v[64];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v4f x4 = reinterpret_cast<const v4f*>(src)[i];
+    v[i * 4] = x4[0];
+    v[i * 4 + 1] = x4[1];
+    v[i * 4 + 2] = x4[2];
+    v[i * 4 + 3] = x4[3];
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((t & 63) == 0) red[t / 64] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
+  uint8_t* dst = q + (mat * rows + prow) * cols + int64_t(cb) * kFp8Block + bc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v4i out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        packed |= f32_to_e4m3(clamp_e4m3(v[i * 16 + j * 4 + b] / sc)) << (8 * b);
+      out[j] = static_cast<int>(packed);
+    }
+    reinterpret_cast<v4i*>(dst)[i] = out;
+  }
+  if (t == 0) s[(mat * rbs + rb) * cbs + cb] = sc;
+}
+
+static int grid_for(int64_t items) {
+  int64_t g = (items + kQuantThreads - 1) / kQuantThreads;
+  if (g > 8192) g = 8192;  // grid-stride beyond 32 workgroups per CU
+  return static_cast<int>(g < 1 ? 1 : g);
+}
+
+}  // namespace afd
+
+using namespace afd;
+
+extern "C" int afd_quant_mxfp8(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q,
+                               uint8_t* s, afd_stream_t stream) {
+  if (!x || !q || !s || rows < 0) return AFD_ERR_ARG;
+  if (cols <= 0 || cols % kMxBlock) return AFD_ERR_SHAPE;
+  if (rows == 0) return AFD_OK;
+  int64_t blocks = rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(quant_mxfp8_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+                     static_cast<hipStream_t>(stream), x, blocks, cols, q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+extern "C" int afd_quant_fp8_1x128(const uint16_t* x, int64_t rows, int32_t cols, uint8_t* q,
+                                   float* s, afd_stream_t stream) {
+  if (!x || !q || !s || rows < 0) return AFD_ERR_ARG;
+  if (cols <= 0 || cols % kFp8Block) return AFD_ERR_SHAPE;
+  if (rows == 0) return AFD_OK;
+  int64_t quarters = rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(quant_fp8_1x128_kernel, dim3(grid_for(quarters)), dim3(kQuantThreads), 0,
+                     static_cast<hipStream_t>(stream), x, quarters, cols, q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+extern "C" int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols,
+                              int32_t gate_up, uint8_t* q, uint8_t* s, afd_stream_t stream) {
+  if (!w || !q || !s || mats < 0) return AFD_ERR_ARG;
+  if (rows <= 0 || cols <= 0 || cols % kMxBlock) return AFD_ERR_SHAPE;
+  if (gate_up && rows % 64) return AFD_ERR_SHAPE;
+  if (mats == 0) return AFD_OK;
+  int64_t blocks = mats * rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(pack_mxfp4_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+                     static_cast<hipStream_t>(stream), w, blocks, rows, cols, gate_up ? 1 : 0,
+                     q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+extern "C" int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
+                                  int32_t gate_up, uint8_t* q, float* s, afd_stream_t stream) {
+  if (!w || !q || !s || mats < 0) return AFD_ERR_ARG;
+  if (rows <= 0 || cols <= 0 || rows % kFp8Block || cols % kFp8Block) return AFD_ERR_SHAPE;
+  if (gate_up && rows % 256) return AFD_ERR_SHAPE;
+  if (mats == 0) return AFD_OK;
+  int64_t blocks = mats * (rows / kFp8Block) * (cols / kFp8Block);
+  if (blocks > 0x7fffffff) return AFD_ERR_SHAPE;
+  hipLaunchKernelGGL(pack_fp8_block_kernel, dim3(static_cast<unsigned>(blocks)),
+                     dim3(kQuantThreads), 0, static_cast<hipStream_t>(stream), w, rows, cols,
+                     gate_up ? 1 : 0, q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}

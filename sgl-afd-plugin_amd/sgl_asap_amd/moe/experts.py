@@ -1,0 +1,209 @@
+"""The F-side per-layer expert runner: what ``FusedMoE`` is to the reference's FFN rank.
+
+The reference's FFN rank calls ``self.experts[layer_id](x, StandardTopKOutput(w, ids, None))``
+(``python/sgl_asap_plugin/srt/managers/scheduler.py:410-412``) on a FusedMoE whose local
+experts are ``range(ep_rank * per_rank, (ep_rank + 1) * per_rank)`` (``scheduler.py:206-218``)
+and gets a bf16 [n, hidden] partial sum over the local experts. ``AfdExperts`` keeps that
+call contract and runs it as one gfx950 call, ``afd_moe_ffn`` (include/afd.h):
+
+    quantize x -> route pairs to local experts -> grouped gate_up + SwiGLU -> grouped down
+    -> top-k weighted finalize
+
+Weights are packed once at load time on the GPU (``pack_mxfp4_experts`` /
+``pack_fp8_block_experts``) into the kernel's layout; a workspace sized for ``n_max`` tokens
+is allocated once per stream, so a call only enqueues kernels (the handler contract of
+``python/sgl_asap_plugin/transport/server.py:8-9``) and can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Dict, Optional
+
+import torch
+
+from .. import _lib
+from .topk import format_is_standard
+
+WEIGHT_FORMATS = {"mxfp4": _lib.AFD_W_MXFP4, "fp8_block": _lib.AFD_W_FP8_BLOCK}
+MX_BLOCK, FP8_BLOCK = 32, 128
+
+
+def _stream_handle(stream: Optional[torch.cuda.Stream] = None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return s.cuda_stream
+
+
+@dataclass
+class ExpertWeights:
+    """Packed weights of one layer's local experts (device tensors, kernel layout)."""
+
+    fmt: str  # "mxfp4" or "fp8_block"
+    num_local: int
+    hidden: int
+    inter: int
+    w13: torch.Tensor
+    s13: torch.Tensor
+    w2: torch.Tensor
+    s2: torch.Tensor
+
+    def as_struct(self) -> _lib.AfdExpertWeights:
+        return _lib.AfdExpertWeights(
+            self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr()
+        )
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.w13, self.s13, self.w2, self.s2))
+
+
+def _as_f32(w: torch.Tensor, device) -> torch.Tensor:
+    return w.to(device=device, dtype=torch.float32).contiguous()
+
+
+def pack_mxfp4_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> ExpertWeights:
+    """Quantize logical expert weights to MXFP4 in the kernel layout, on the GPU.
+
+    w13: [E, 2I, H] with rows [gate; up] (SGLang's w13 mapping, ``srt/models/deepseek_v4.py:132-137``);
+    w2: [E, H, I]. Any float dtype. The reference's checkpoints hold the same format
+    (int8-packed e2m1 + E8M0 per 32, ``srt/configs/model_config.py:3-7``).
+    """
+    device = torch.device(device or "cuda")
+    e, two_i, h = w13.shape
+    inter = two_i // 2
+    if w2.shape != (e, h, inter):
+        raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+    a = _as_f32(w13, device)
+    b = _as_f32(w2, device)
+    q13 = torch.empty(e, two_i, h // 2, dtype=torch.uint8, device=device)
+    s13 = torch.empty(e, two_i, h // MX_BLOCK, dtype=torch.uint8, device=device)
+    q2 = torch.empty(e, h, inter // 2, dtype=torch.uint8, device=device)
+    s2 = torch.empty(e, h, inter // MX_BLOCK, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        st = _stream_handle()
+        _lib.call("afd_pack_mxfp4", a.data_ptr(), e, two_i, h, 1, q13.data_ptr(), s13.data_ptr(), st)
+        _lib.call("afd_pack_mxfp4", b.data_ptr(), e, h, inter, 0, q2.data_ptr(), s2.data_ptr(), st)
+    return ExpertWeights("mxfp4", e, h, inter, q13, s13, q2, s2)
+
+
+def pack_fp8_block_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> ExpertWeights:
+    """Quantize logical expert weights to e4m3 with fp32 128x128 block scales, on the GPU
+    (the block-FP8 expert format of DeepGEMM / SGLang's Fp8MoEMethod)."""
+    device = torch.device(device or "cuda")
+    e, two_i, h = w13.shape
+    inter = two_i // 2
+    if w2.shape != (e, h, inter):
+        raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
+    a = _as_f32(w13, device)
+    b = _as_f32(w2, device)
+    q13 = torch.empty(e, two_i, h, dtype=torch.uint8, device=device)
+    s13 = torch.empty(e, two_i // FP8_BLOCK, h // FP8_BLOCK, dtype=torch.float32, device=device)
+    q2 = torch.empty(e, h, inter, dtype=torch.uint8, device=device)
+    s2 = torch.empty(e, h // FP8_BLOCK, inter // FP8_BLOCK, dtype=torch.float32, device=device)
+    with torch.cuda.device(device):
+        st = _stream_handle()
+        _lib.call("afd_pack_fp8_block", a.data_ptr(), e, two_i, h, 1, q13.data_ptr(), s13.data_ptr(), st)
+        _lib.call("afd_pack_fp8_block", b.data_ptr(), e, h, inter, 0, q2.data_ptr(), s2.data_ptr(), st)
+    return ExpertWeights("fp8_block", e, h, inter, q13, s13, q2, s2)
+
+
+def moe_cfg(weights: ExpertWeights, top_k: int, expert_lo: int) -> _lib.AfdMoeCfg:
+    return _lib.AfdMoeCfg(
+        weights.hidden, weights.inter, top_k, expert_lo, weights.num_local, WEIGHT_FORMATS[weights.fmt]
+    )
+
+
+def workspace_layout(cfg: _lib.AfdMoeCfg, n: int) -> dict:
+    """afd_workspace_layout as a dict of byte offsets (plus np_max, block_m, max_tiles)."""
+    out = _lib.AfdWsLayout()
+    _lib.call("afd_workspace_layout", ctypes.byref(cfg), n, ctypes.byref(out))
+    return {name: getattr(out, name) for name, _ in _lib.AfdWsLayout._fields_}
+
+
+class AfdExperts(torch.nn.Module):
+    """One MoE layer's local routed experts on one F rank.
+
+    ``forward(hidden_states, topk_output)`` is the FusedMoE call of the reference's FFN
+    rank: x bf16 [n, H], topk_output with ``topk_ids`` [n, k] (global ids) and
+    ``topk_weights`` [n, k]; returns bf16 [n, H], the top-k-weighted sum over the local
+    experts (rows with no local expert are 0). Enqueued on the current stream.
+    """
+
+    def __init__(
+        self,
+        num_experts: int,
+        top_k: int,
+        layer_id: int,
+        local: range,
+        weights: ExpertWeights,
+        n_max: int = 16384,
+    ):
+        super().__init__()
+        if len(local) != weights.num_local:
+            raise ValueError(f"{len(local)} local experts but weights for {weights.num_local}")
+        if not (0 <= local.start and local.stop <= num_experts):
+            raise ValueError(f"local experts {local} outside [0, {num_experts})")
+        self.num_experts, self.top_k, self.layer_id = num_experts, top_k, layer_id
+        self.local = local
+        self.hidden_size, self.intermediate_size = weights.hidden, weights.inter
+        self.weights = weights
+        self.n_max = n_max
+        self.cfg = moe_cfg(weights, top_k, local.start)
+        self.layout = workspace_layout(self.cfg, n_max)
+        self._ws: Dict[int, torch.Tensor] = {}
+        self._wstruct = weights.as_struct()
+
+    def workspace(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        """The workspace of ``stream`` (one per stream, so jobs on different streams can
+        overlap; calls on one stream are ordered and share it)."""
+        s = stream if stream is not None else torch.cuda.current_stream()
+        ws = self._ws.get(s.cuda_stream)
+        if ws is None:
+            ws = torch.empty(self.layout["total"], dtype=torch.uint8, device=self.weights.w13.device)
+            self._ws[s.cuda_stream] = ws
+        return ws
+
+    def forward(self, hidden_states: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):
+        if not format_is_standard(topk_output):
+            raise RuntimeError(f"expected explicit top-k ids and weights, got {type(topk_output).__name__}")
+        x = hidden_states
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"the expert path takes bf16 activations, got {x.dtype}")
+        n = x.shape[0]
+        if n > self.n_max:
+            raise ValueError(f"{n} tokens exceed n_max={self.n_max}")
+        ids = topk_output.topk_ids
+        w = topk_output.topk_weights
+        if ids.shape != (n, self.top_k) or w.shape != (n, self.top_k):
+            raise ValueError(f"top-k shapes {tuple(ids.shape)} / {tuple(w.shape)} for {n} tokens, k={self.top_k}")
+        x = x.contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        w = w.to(torch.float32).contiguous()
+        if out is None:
+            out = torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=x.device)
+        if n == 0:
+            return out
+        ws = self.workspace()
+        _lib.call(
+            "afd_moe_ffn",
+            ctypes.byref(self.cfg),
+            ctypes.byref(self._wstruct),
+            x.data_ptr(),
+            ids.data_ptr(),
+            w.data_ptr(),
+            n,
+            ws.data_ptr(),
+            ws.numel(),
+            out.data_ptr(),
+            _stream_handle(),
+        )
+        return out
+
+    def ws_view(self, name: str, dtype: torch.dtype, count: int, n: int, stream=None) -> torch.Tensor:
+        """A view of an intermediate buffer of the last call with ``n`` tokens (the
+        workspace layout depends on n); for parity tests and profiling."""
+        ws = self.workspace(stream)
+        off = workspace_layout(self.cfg, n)[name]
+        size = torch.tensor([], dtype=dtype).element_size()
+        return ws[off : off + count * size].view(dtype)

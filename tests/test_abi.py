@@ -1,0 +1,67 @@
+"""The C ABI library loads without a GPU, exports every declared entry point, and its
+host-only functions (status strings, workspace layout, argument checks) behave."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from sgl_asap_amd import _lib
+from sgl_asap_amd.moe.experts import workspace_layout
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "afd.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(afd_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert L.afd_abi_version() == 1
+
+
+def test_status_strings():
+    L = _lib.lib()
+    for st in (0, -1, -2, -3, -4, -5):
+        assert L.afd_status_string(st)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.AFD_ERR_ARG, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.AFD_ERR_UNSUPPORTED, "x")
+
+
+def test_workspace_layout_dsv4_rank():
+    cfg = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_MXFP4)
+    L = workspace_layout(cfg, 16384)
+    assert L["block_m"] == 128
+    assert L["np_max"] == (16384 * 8 + 64 * 127 + 127) // 128 * 128
+    assert L["xq"] == 0 and L["xs"] == 16384 * 4096
+    offs = [L[k] for k in ("xq", "xs", "counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos",
+                           "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert L["total"] >= L["y"] + L["np_max"] * 4096 * 2
+
+
+def test_bad_configs_rejected_on_host():
+    out = _lib.AfdWsLayout()
+    bad = [
+        _lib.AfdMoeCfg(4000, 2048, 8, 0, 64, 1),  # hidden not a multiple of 256
+        _lib.AfdMoeCfg(4096, 2000, 8, 0, 64, 1),  # inter not a multiple of 128
+        _lib.AfdMoeCfg(4096, 2048, 0, 0, 64, 1),  # topk 0
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 512, 1),  # too many local experts
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 7),  # unknown format
+    ]
+    for cfg in bad:
+        assert _lib.lib().afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) != 0
+    good = _lib.AfdMoeCfg(256, 128, 2, 0, 8, 1)
+    assert _lib.lib().afd_workspace_layout(ctypes.byref(good), 1 << 17, ctypes.byref(out)) != 0
+    assert _lib.lib().afd_workspace_layout(ctypes.byref(good), (1 << 17) - 1, ctypes.byref(out)) == 0

@@ -1,0 +1,56 @@
+"""GPU parity: finalize (top-k weighted sum) and the A-side combine are bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits16, dev, say
+from oracle import experts as OX
+from oracle import formats as F
+from sgl_asap_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("n,k,hidden,rows", [(1, 1, 256, 1), (97, 8, 4096, 300), (513, 2, 1024, 600)])
+def test_finalize_bitexact(n, k, hidden, rows):
+    say(f"finalize n={n} k={k} hidden={hidden}")
+    g = torch.Generator().manual_seed(n)
+    y = torch.randn(rows, hidden, generator=g).to(torch.bfloat16)
+    w = torch.rand(n, k, generator=g)
+    pos = torch.randint(-1, rows, (n * k,), generator=g, dtype=torch.int32)
+    out = torch.empty(n, hidden, dtype=torch.bfloat16, device=dev())
+    yd, wd, pd = y.to(dev()), w.to(dev()), pos.to(dev())
+    _lib.call("afd_finalize", yd.data_ptr(), pd.data_ptr(), wd.data_ptr(), n, k, hidden, out.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    ref = OX.finalize(bits16(y), pos.numpy(), w.numpy(), n, k)
+    assert np.array_equal(bits16(out), ref)
+
+
+@pytest.mark.parametrize("parts_n,with_shared", [(1, False), (1, True), (2, True), (4, False), (16, True)])
+def test_combine_bitexact(parts_n, with_shared):
+    say(f"combine parts={parts_n} shared={with_shared}")
+    g = torch.Generator().manual_seed(parts_n)
+    n, hidden = 333, 512
+    parts = [torch.randn(n, hidden, generator=g).to(torch.bfloat16) for _ in range(parts_n)]
+    shared = torch.randn(n, hidden, generator=g).to(torch.bfloat16) if with_shared else None
+    pd = [p.to(dev()) for p in parts]
+    sd = shared.to(dev()) if shared is not None else None
+    out = torch.empty(n, hidden, dtype=torch.bfloat16, device=dev())
+    import ctypes
+
+    arr = (ctypes.c_void_p * parts_n)(*[p.data_ptr() for p in pd])
+    _lib.call("afd_combine", arr, parts_n, sd.data_ptr() if sd is not None else None, out.data_ptr(), n * hidden, _stream())
+    torch.cuda.synchronize()
+    ref = OX.combine([bits16(p) for p in parts], bits16(shared) if shared is not None else None)
+    assert np.array_equal(bits16(out), ref)
+    # the reference's own formula on torch CPU, for the shared-free case
+    if not with_shared and parts_n > 1:
+        acc = parts[0].float()
+        for p in parts[1:]:
+            acc += p
+        assert np.array_equal(bits16(out), bits16(acc.to(torch.bfloat16)))

@@ -1,0 +1,107 @@
+"""GPU parity: the HIP quantizers and weight packers are bit-exact with the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import dev, say, u8
+from oracle import formats as F
+from sgl_asap_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bf16_input(rows, cols, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, cols, generator=g) * torch.logspace(-3, 3, cols)[None, :]
+    if rows >= 3:
+        x[0, :] = 0.0  # an all-zero row: scale code 0
+        x[1, :32] = 1e-30  # a tiny block
+        x[2, :64] = torch.tensor([0.25, -0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 448.0] * 8)
+    return x.to(torch.bfloat16)
+
+
+def _x_f32(x):
+    return F.bf16_to_f32(x.contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 32), (37, 512), (129, 4096)])
+def test_quant_mxfp8_bitexact(rows, cols):
+    say(f"quant_mxfp8 rows={rows} cols={cols}")
+    x = _bf16_input(rows, cols, seed=rows)
+    xd = x.to(dev())
+    q = torch.empty(rows, cols, dtype=torch.uint8, device=dev())
+    s = torch.empty(rows, cols // 32, dtype=torch.uint8, device=dev())
+    _lib.call("afd_quant_mxfp8", xd.data_ptr(), rows, cols, q.data_ptr(), s.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    q_ref, s_ref = F.mx_quantize(_x_f32(x), "e4m3")
+    assert np.array_equal(u8(s), s_ref)
+    assert np.array_equal(u8(q), q_ref)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (37, 512), (129, 4096)])
+def test_quant_fp8_1x128_bitexact(rows, cols):
+    say(f"quant_fp8_1x128 rows={rows} cols={cols}")
+    x = _bf16_input(rows, cols, seed=rows + 7)
+    xd = x.to(dev())
+    q = torch.empty(rows, cols, dtype=torch.uint8, device=dev())
+    s = torch.empty(rows, cols // 128, dtype=torch.float32, device=dev())
+    _lib.call("afd_quant_fp8_1x128", xd.data_ptr(), rows, cols, q.data_ptr(), s.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    q_ref, s_ref = F.fp8_group_quantize(_x_f32(x))
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(u8(q), q_ref)
+
+
+def _gate_up_rows(rows, g=32):
+    """Logical row of each physical row of the gate/up interleave."""
+    half = rows // 2
+    out = []
+    for r in range(rows):
+        j, q = divmod(r, 2 * g)
+        out.append(j * g + q if q < g else half + j * g + q - g)
+    return np.array(out)
+
+
+@pytest.mark.parametrize("gate_up", [0, 1])
+def test_pack_mxfp4_bitexact(gate_up):
+    say(f"pack_mxfp4 gate_up={gate_up}")
+    g = torch.Generator().manual_seed(3)
+    mats, rows, cols = 3, 128, 256
+    w = torch.randn(mats, rows, cols, generator=g) * 0.02
+    w[0, 0, :32] = 0.0
+    w[1, 5, :8] = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 6.0])
+    wd = w.to(dev())
+    q = torch.empty(mats, rows, cols // 2, dtype=torch.uint8, device=dev())
+    s = torch.empty(mats, rows, cols // 32, dtype=torch.uint8, device=dev())
+    _lib.call("afd_pack_mxfp4", wd.data_ptr(), mats, rows, cols, gate_up, q.data_ptr(), s.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    codes, scales = F.mx_quantize(w.numpy(), "e2m1")
+    packed = F.pack_fp4(codes)
+    if gate_up:
+        perm = _gate_up_rows(rows)
+        packed, scales = packed[:, perm], scales[:, perm]
+    assert np.array_equal(u8(s), scales)
+    assert np.array_equal(u8(q), packed)
+
+
+@pytest.mark.parametrize("gate_up", [0, 1])
+def test_pack_fp8_block_bitexact(gate_up):
+    say(f"pack_fp8_block gate_up={gate_up}")
+    g = torch.Generator().manual_seed(4)
+    mats, rows, cols = 2, 256, 384
+    w = torch.randn(mats, rows, cols, generator=g) * 0.02
+    wd = w.to(dev())
+    q = torch.empty(mats, rows, cols, dtype=torch.uint8, device=dev())
+    s = torch.empty(mats, rows // 128, cols // 128, dtype=torch.float32, device=dev())
+    _lib.call("afd_pack_fp8_block", wd.data_ptr(), mats, rows, cols, gate_up, q.data_ptr(), s.data_ptr(), _stream())
+    torch.cuda.synchronize()
+    codes, scales = F.fp8_block_quantize_2d(w.numpy())
+    if gate_up:
+        codes = codes[:, _gate_up_rows(rows)]
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), scales.view(np.uint32))
+    assert np.array_equal(u8(q), codes)
