@@ -90,6 +90,58 @@ __device__ __forceinline__ float clamp_e4m3(float v) {
   return fminf(fmaxf(v, -kE4m3Max), kE4m3Max);
 }
 
+// Two clamped fp32 -> e4m3fn bytes in the low 16 bits, by v_cvt_pk_fp8_f32 (round to nearest
+// even; bit-identical to f32_to_e4m3 on every fp32 input in [-448, 448]).
+__device__ __forceinline__ uint32_t pk_e4m3(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(lo), clamp_e4m3(hi), 0, false)) &
+         0xffffu;
+}
+
+// Four clamped fp32 -> four e4m3fn bytes (element i in byte i).
+__device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(a), clamp_e4m3(b), 0, false);
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(c), clamp_e4m3(d), lo, true));
+}
+
+// ---------------------------------------------------------------- direct global -> LDS copies
+// gfx950 global_load_lds: lane i of the wavefront writes its 16 (or 4) bytes to LDS at
+// M0 + 16*i (4*i); the global address is the uniform base plus the lane's 32-bit offset.
+// Issued through inline assembly so the compiler does not drain every outstanding copy
+// before each LDS read; callers wait with wait_vmcnt<N>() (vector-memory operations
+// complete in issue order for loads) and a barrier before reading what they copied.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)p));
+}
+
+// A pointer the caller knows is wavefront-uniform, moved into scalar registers.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ void lds_dma16(uint32_t m0, const void* base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff),
+               "s"(uniform_ptr(base))
+               : "memory");
+}
+
+__device__ __forceinline__ void lds_dma4(uint32_t m0, const void* base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff),
+               "s"(uniform_ptr(base))
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) leaving the other counters alone.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace afd
 
 // Host-side helpers shared by the translation units.

@@ -8,15 +8,20 @@
 // Tiling: a workgroup of 4 wavefronts owns a 128 x 256 output tile; wavefront (wm, wn) owns
 // 64 x 128 = 2 x 4 MFMA tiles of 32x32 (128 fp32 accumulators per lane). K advances 128 per
 // stage (two MFMA k-steps): A 128 rows x 128 B, B 256 rows x 64 B, plus one scale dword
-// (4 UE8M0 bytes) per row of each. Two LDS stages; the next stage's global loads are issued
-// before the current stage's MFMAs. LDS rows are XOR-swizzled by 16-byte chunk so the
-// ds_read_b128 of 8 consecutive rows hit 8 distinct bank groups.
+// (4 UE8M0 bytes) per row of each, 33.5 KiB per stage.
 //
-// The workgroups are persistent: grid = 2 per CU, tile index strides by the grid, and the
-// number of row tiles is read from device memory (the router wrote it), so no host round
-// trip is needed. Tile index order is (row tile, column tile) with column tiles fastest,
-// so consecutive workgroups (which the dispatcher spreads over the 8 XCDs) split a
-// weight tile's columns across XCDs and each expert's weights are fetched from HBM once.
+// Operands move HBM -> LDS with gfx950's direct global_load_lds (no register staging) into a
+// ring of 4 stages, three stages ahead of the MFMAs, so a stage has three stages of MFMA time
+// to arrive; one barrier per stage. Every wavefront issues the same 10 copies per stage, which
+// keeps the vmcnt arithmetic of the waits uniform. LDS rows are XOR-swizzled by 16-byte chunk
+// (the copies place each lane's chunk at its swizzled slot) so the ds_read_b128 of 8
+// consecutive rows hit 8 distinct bank groups.
+//
+// The workgroups are persistent: grid = resident workgroups, tile index strides by the grid,
+// and the number of row tiles is read from device memory (the router wrote it), so no host
+// round trip is needed. Tile index order is (row tile, column tile) with column tiles fastest,
+// so consecutive workgroups (which the dispatcher spreads over the 8 XCDs) split a weight
+// tile's columns across XCDs and each expert's weights are fetched from HBM once.
 #include "afd_common.h"
 #include "afd_internal.h"
 
@@ -31,7 +36,9 @@ constexpr int kBStage = kBN * kBK / 2;   // fp4 B bytes per stage
 constexpr int kSAStage = kBM * 4;
 constexpr int kSBStage = kBN * 4;
 constexpr int kStage = kAStage + kBStage + kSAStage + kSBStage;
-constexpr int kLdsBytes = 2 * kStage;
+constexpr int kStages = 4;
+constexpr int kCopiesPerStage = 10;  // per wavefront: 4 A + 4 B + 1 A-scale + 1 B-scale
+constexpr int kLdsBytes = kStages * kStage;
 constexpr int kHStride = 132;  // fp32 stride of the gate_up epilogue tile (128 + 4)
 constexpr int kYStride = 264;  // bf16 stride of the down epilogue tile (256 + 8)
 static_assert(kBM * kHStride * 4 <= kLdsBytes, "gate_up epilogue tile must fit the stages");
@@ -80,42 +87,36 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = p.tile_expert[mt];
 
-    const uint8_t* a_src[4];
-    const uint8_t* b_src[4];
+    // Per-lane 32-bit source offsets of this tile's copies (fixed over K; the K position
+    // goes into the uniform base). Copy q of wavefront w fills 1 KiB: A rows w*32+q*8+lane/8,
+    // B rows w*64+q*16+lane/4; each lane loads the logical chunk that belongs at its
+    // swizzled LDS slot.
+    uint32_t voff_a[4], voff_b[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int r = j * 32 + (t >> 3);
-      a_src[j] = p.a + a_row<MODE>(p, m0 + r) * a_ld + (t & 7) * 16;
-      int n = j * 64 + (t >> 2);
-      b_src[j] = p.b + (e * p.N + n0 + n) * b_ld + (t & 3) * 16;
+    for (int q = 0; q < 4; ++q) {
+      int r = wave * 32 + q * 8 + (lane >> 3);
+      voff_a[q] = static_cast<uint32_t>(a_row<MODE>(p, m0 + r) * a_ld) +
+                  (static_cast<uint32_t>((lane & 7) ^ (lane >> 3)) << 4);
+      int n = wave * 64 + q * 16 + (lane >> 2);
+      voff_b[q] = static_cast<uint32_t>((e * p.N + n0 + n) * b_ld) +
+                  (static_cast<uint32_t>((lane & 3) ^ ((lane >> 3) & 3)) << 4);
     }
-    const uint8_t* sa_src = p.as + a_row<MODE>(p, m0 + (t & (kBM - 1))) * s_ld;
-    const uint8_t* sb_src = p.bs + (e * p.N + n0 + t) * s_ld;
+    const uint32_t voff_sa = static_cast<uint32_t>(a_row<MODE>(p, m0 + wave * 32 + (lane & 31)) * s_ld);
+    const uint32_t voff_sb = static_cast<uint32_t>((e * p.N + n0 + wave * 64 + lane) * s_ld);
+    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+    const int w_u = __builtin_amdgcn_readfirstlane(wave);
 
-    v4i ra[4], rb[4];
-    uint32_t rsa = 0, rsb = 0;
-    auto load = [&](int kt) {
-      const int k0 = kt * kBK;
+    auto issue = [&](int kt) {
+      const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+      const uint8_t* abase = p.a + kt * kBK;
+      const uint8_t* bbase = p.b + kt * (kBK / 2);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ra[j] = *reinterpret_cast<const v4i*>(a_src[j] + k0);
-        rb[j] = *reinterpret_cast<const v4i*>(b_src[j] + k0 / 2);
-      }
-      if (t < kBM) rsa = *reinterpret_cast<const uint32_t*>(sa_src + k0 / 32);
-      rsb = *reinterpret_cast<const uint32_t*>(sb_src + k0 / 32);
-    };
-    auto store = [&](int s) {
-      uint8_t* base = lds + s * kStage;
+      for (int q = 0; q < 4; ++q) lds_dma16(st + (w_u * 32 + q * 8) * 128, abase, voff_a[q]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int r = j * 32 + (t >> 3);
-        *reinterpret_cast<v4i*>(base + a_off(r, t & 7)) = ra[j];
-        int n = j * 64 + (t >> 2);
-        *reinterpret_cast<v4i*>(base + kAStage + b_off(n, t & 3)) = rb[j];
-      }
-      uint32_t* sa = reinterpret_cast<uint32_t*>(base + kAStage + kBStage);
-      if (t < kBM) sa[t] = rsa;
-      sa[kBM + t] = rsb;
+      for (int q = 0; q < 4; ++q)
+        lds_dma16(st + kAStage + (w_u * 64 + q * 16) * 64, bbase, voff_b[q]);
+      if (lane < 32) lds_dma4(st + kAStage + kBStage + w_u * 32 * 4, p.as + kt * 4, voff_sa);
+      lds_dma4(st + kAStage + kBStage + kSAStage + w_u * 64 * 4, p.bs + kt * 4, voff_sb);
     };
 
     v16f acc[2][4];
@@ -126,12 +127,8 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      if (kt + 1 < KT) load(kt + 1);
-      const uint8_t* base = lds + (kt & 1) * kStage;
+    auto compute = [&](int s) {
+      const uint8_t* base = lds + s * kStage;
       const uint32_t* sa = reinterpret_cast<const uint32_t*>(base + kAStage + kBStage);
       const uint32_t* sb = sa + kBM;
       uint32_t sav[2], sbv[4];
@@ -170,9 +167,27 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
           }
         }
       }
-      if (kt + 1 < KT) store((kt + 1) & 1);
+    };
+
+    wait_vmcnt<0>();  // the previous tile's epilogue stores
+#pragma unroll
+    for (int s = 0; s < kStages - 1; ++s)
+      if (s < KT) issue(s);
+    for (int kt = 0; kt < KT; ++kt) {
+      // stage kt's copies are done when at most the later stages' copies are outstanding
+      if (kt + 2 < KT)
+        wait_vmcnt<2 * kCopiesPerStage>();
+      else if (kt + 1 < KT)
+        wait_vmcnt<kCopiesPerStage>();
+      else
+        wait_vmcnt<0>();
+      // every wavefront's copies of stage kt have landed, and every wavefront is done with
+      // stage kt-1, whose buffer the next copy overwrites
       __syncthreads();
+      if (kt + kStages - 1 < KT) issue(kt + kStages - 1);
+      compute(kt % kStages);
     }
+    __syncthreads();  // the epilogue reuses the stage buffers
 
     if (MODE == kGateUp) {
       // SwiGLU in registers: column subtiles (0,1) and (2,3) are the (gate, up) halves of
@@ -187,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
             int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
             int col = wn * 64 + jj * 32 + lr;
             float g = acc[i][2 * jj][q], u = acc[i][2 * jj + 1][q];
-            hl[row * kHStride + col] = g / (1.0f + expf(-g)) * u;
+            hl[row * kHStride + col] = __fdividef(g, 1.0f + __expf(-g)) * u;
           }
       __syncthreads();
       const int inter = p.N / 2;
@@ -213,13 +228,9 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
         float inv = mx_inv_scale(code);
         v4i out[2];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          uint32_t packed = 0;
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] * inv)) << (8 * j);
-          out[i / 4][i % 4] = static_cast<int>(packed);
-        }
+        for (int i = 0; i < 8; ++i)
+          out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv,
+                                                        v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
         if (p.sorted_pairs[grow] >= 0) {
           v4i* dst = reinterpret_cast<v4i*>(p.hq + int64_t(grow) * inter + n0 / 2 + cb * 32);
           dst[0] = out[0];
@@ -255,8 +266,18 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
   }
 }
 
+template <int MODE>
 static int persistent_grid(int max_tiles) {
-  int g = device_cu_count() * 2;
+  static int per_cu = 0;  // resident workgroups per CU (registers and LDS decide)
+  if (per_cu == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE>, kThreads, 0) !=
+            hipSuccess ||
+        b < 1)
+      b = 1;
+    per_cu = b;
+  }
+  int g = device_cu_count() * per_cu;
   return max_tiles < g ? (max_tiles < 1 ? 1 : max_tiles) : g;
 }
 
@@ -277,7 +298,7 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.hq = ws + L.hq;
   p.hs = ws + L.hs;
   p.y = nullptr;
-  int grid = persistent_grid(L.max_tiles * (p.N / kBN));
+  int grid = persistent_grid<kGateUp>(L.max_tiles * (p.N / kBN));
   hipLaunchKernelGGL(mx_gemm_kernel<kGateUp>, dim3(grid), dim3(kThreads), 0, stream, p);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
@@ -300,7 +321,7 @@ int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t
   p.hq = nullptr;
   p.hs = nullptr;
   p.y = reinterpret_cast<uint16_t*>(ws + L.y);
-  int grid = persistent_grid(L.max_tiles * (p.N / kBN));
+  int grid = persistent_grid<kDown>(L.max_tiles * (p.N / kBN));
   hipLaunchKernelGGL(mx_gemm_kernel<kDown>, dim3(grid), dim3(kThreads), 0, stream, p);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
