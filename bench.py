@@ -27,7 +27,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "sgl-afd-plugin_amd")]
 
 PEAK_TFLOPS = {"fp4": 10100.0, "fp8": 5000.0, "bf16": 2500.0}
 PEAK_HBM_GBS = 8000.0
-STAGES = ("quant", "route", "gate_up", "down", "finalize")
+STAGES = ("route", "quant", "gate_up", "down", "finalize")
 
 
 def parse():

@@ -78,13 +78,17 @@ typedef struct afd_moe_cfg {
   int32_t weight_fmt; /* enum afd_weight_fmt */
 } afd_moe_cfg;
 
-/* Packed expert weights of one layer (device pointers), as afd_pack_* writes them:
- *  MXFP4:     w13 u8 [E][2I][H/2], s13 u8 [E][2I][H/32], w2 u8 [E][H][I/2], s2 u8 [E][H][I/32];
- *             element 2i in the low nibble; w13 rows interleave gate and up in groups of 32
- *             (physical row 64j+q is gate row 32j+q for q < 32, else up row 32j+q-32).
+/* Packed expert weights of one layer (device pointers), as afd_pack_* writes them.
+ *  MXFP4: w13 / w2 are tile images, the LDS bytes of one 128-wide K stage of one 256-row
+ *    tile followed by that tile's UE8M0 scales: [E][N/256][K/128][256 x 64 B | 256 x 4 B]
+ *    (17408 bytes each; N = 2I, K = H for w13; N = H, K = I for w2). In a tile, 16-byte
+ *    chunk c (32 e2m1 values, element 2i in the low nibble) of row n sits at byte
+ *    n*64 + 16*(c ^ ((n >> 1) & 3)); scale j of row n at 16384 + 4n + j. w13 rows
+ *    interleave gate and up in groups of 32 (physical row 64j+q is gate row 32j+q for
+ *    q < 32, else up row 32j+q-32). s13 and s2 are not used (NULL).
  *  FP8_BLOCK: w13 u8 [E][2I][H], s13 f32 [E][2I/128][H/128], w2 u8 [E][H][I],
- *             s2 f32 [E][H/128][I/128]; w13 rows interleave gate and up in groups of 32 as
- *             above, while s13 keeps logical block order (gate blocks, then up blocks). */
+ *    s2 f32 [E][H/128][I/128]; w13 rows interleave gate and up in groups of 32 as above,
+ *    while s13 keeps logical block order (gate blocks, then up blocks). */
 typedef struct afd_expert_weights {
   const void* w13;
   const void* s13;
@@ -95,7 +99,8 @@ typedef struct afd_expert_weights {
 /* Byte offsets of the internal buffers of afd_moe_ffn's workspace for n tokens. */
 typedef struct afd_ws_layout {
   uint64_t total;          /* bytes the workspace must have */
-  uint64_t xq, xs;         /* quantized activations [n][H] and their scales */
+  uint64_t xq, xs;         /* quantized activations and their scales (MXFP4: gate_up A tile
+                              images of every padded row, scales inside, xs empty) */
   uint64_t counts;         /* i32 [E] pairs per local expert */
   uint64_t offsets;        /* i32 [E+1] exclusive prefix of counts */
   uint64_t padded_offsets; /* i32 [E+1] the same with every segment padded to block_m */
@@ -104,7 +109,8 @@ typedef struct afd_ws_layout {
   uint64_t tile_expert;    /* i32 [max_tiles] local expert of each block_m row tile */
   uint64_t num_tiles;      /* i32 [1] row tiles in use */
   uint64_t hist;           /* i32 router scratch */
-  uint64_t hq, hs;         /* intermediate activations [np_max][I] and their scales */
+  uint64_t hq, hs;         /* intermediate activations and their scales (MXFP4: down A tile
+                              images, scales inside, hs empty) */
   uint64_t y;              /* bf16 [np_max][H] per-pair down outputs */
   int64_t np_max;          /* padded rows reserved: n*k + E*(block_m-1), rounded up */
   int32_t block_m;         /* row tile of the grouped GEMMs */
@@ -118,9 +124,11 @@ int afd_last_hip_error(void); /* hipError_t of the last AFD_ERR_HIP on this thre
 int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_layout* out);
 
 /* ---- weight packing (load time) -------------------------------------------------------
- * w: fp32 [mats][rows][cols] logical weights (for gate_up = 1: rows = 2I = [gate; up]). */
+ * w: fp32 [mats][rows][cols] logical weights (for gate_up = 1: rows = 2I = [gate; up]).
+ * afd_pack_mxfp4 writes mats * rows * (cols/2 + cols/32) bytes of tile images to `out`
+ * (rows a multiple of 256, cols of 128). */
 int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols, int32_t gate_up,
-                   uint8_t* q, uint8_t* s, afd_stream_t stream);
+                   uint8_t* out, afd_stream_t stream);
 int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
                        int32_t gate_up, uint8_t* q, float* s, afd_stream_t stream);
 
@@ -148,7 +156,7 @@ int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const
                 uint16_t* out, afd_stream_t stream);
 
 /* afd_moe_ffn with hipEvent_t handles recorded on `stream` around its stages:
- * stage_events[0] before the activation quantizer, [1] after it, [2] after routing,
+ * stage_events[0] before routing, [1] after routing, [2] after the activation quantizer,
  * [3] after gate_up, [4] after down, [5] after finalize. NULL entries are skipped.
  * Same replaced interface as afd_moe_ffn; for the per-stage timing of JobTimer
  * (P/srt/managers/scheduler.py:109-159). */

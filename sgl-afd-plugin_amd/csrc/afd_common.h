@@ -104,6 +104,29 @@ __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d)
       __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(c), clamp_e4m3(d), lo, true));
 }
 
+// ---------------------------------------------------------------- MX GEMM operand tile images
+// The MX grouped GEMMs copy their operands HBM -> LDS as contiguous "tile images": the exact
+// LDS bytes of one K stage (128 K values) of one row tile, followed by the UE8M0 scales of
+// those rows (4 bytes = 4 blocks of 32 per row).
+//   A image (activations, 128 rows of e4m3): 128 x 128 B data, then 128 x 4 B scales.
+//   B image (weights, 256 rows of e2m1):     256 x  64 B data, then 256 x 4 B scales.
+// Rows are XOR-swizzled by 16-byte chunk so the MFMA operand reads (ds_read_b128 of 8
+// consecutive rows) hit 8 distinct bank groups.
+constexpr int kImgData = 16384;
+constexpr int kImgARows = 128, kImgBRows = 256;
+constexpr int kImgA = kImgData + kImgARows * 4;  // 16896
+constexpr int kImgB = kImgData + kImgBRows * 4;  // 17408
+constexpr int kImgK = 128;                        // K values per image
+
+// byte offset of logical 16-byte chunk c (0..7) of row r in an A image
+__host__ __device__ __forceinline__ int img_a_off(int r, int c) {
+  return r * 128 + ((c ^ (r & 7)) << 4);
+}
+// byte offset of logical 16-byte chunk c (0..3) of row n in a B image
+__host__ __device__ __forceinline__ int img_b_off(int n, int c) {
+  return n * 64 + ((c ^ ((n >> 1) & 3)) << 4);
+}
+
 // ---------------------------------------------------------------- direct global -> LDS copies
 // gfx950 global_load_lds: lane i of the wavefront writes its 16 (or 4) bytes to LDS at
 // M0 + 16*i (4*i); the global address is the uniform base plus the lane's 32-bit offset.

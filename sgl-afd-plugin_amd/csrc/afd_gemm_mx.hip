@@ -2,20 +2,18 @@
 // (v_mfma_scale_f32_32x32x64_f8f6f4: A e4m3, B e2m1, one UE8M0 scale per lane = per 32 K).
 //
 //   gate_up: h[p, :] = silu(x_t . Wg_e^T) * (x_t . Wu_e^T) for every padded row p of expert e
-//            (t = token of the pair at row p), quantized to MXFP8 in the epilogue.
+//            (t = token of the pair at row p), quantized to MXFP8 in the epilogue and written
+//            as the down GEMM's A operand images.
 //   down:    y[p, :] = bf16(h_p . W2_e^T).
 //
-// Tiling: a workgroup of 4 wavefronts owns a 128 x 256 output tile; wavefront (wm, wn) owns
-// 64 x 128 = 2 x 4 MFMA tiles of 32x32 (128 fp32 accumulators per lane). K advances 128 per
-// stage (two MFMA k-steps): A 128 rows x 128 B, B 256 rows x 64 B, plus one scale dword
-// (4 UE8M0 bytes) per row of each, 33.5 KiB per stage.
-//
-// Operands move HBM -> LDS with gfx950's direct global_load_lds (no register staging) into a
-// ring of 4 stages, three stages ahead of the MFMAs, so a stage has three stages of MFMA time
-// to arrive; one barrier per stage. Every wavefront issues the same 10 copies per stage, which
-// keeps the vmcnt arithmetic of the waits uniform. LDS rows are XOR-swizzled by 16-byte chunk
-// (the copies place each lane's chunk at its swizzled slot) so the ds_read_b128 of 8
-// consecutive rows hit 8 distinct bank groups.
+// Tiling: a workgroup of 2 x WN wavefronts owns a 128 x (128 WN) output tile; wavefront
+// (wm, wn) owns 64 x 128 = 2 x 4 MFMA tiles of 32x32 (128 fp32 accumulators per lane).
+// WN = 4 (8 wavefronts, two per SIMD, so one wavefront's LDS reads overlap the other's
+// MFMAs) is used whenever N is a multiple of 512; WN = 2 otherwise. K advances 128 per stage
+// (two MFMA k-steps). Both operands are stored as tile images (the LDS bytes of one stage,
+// scales included: afd_common.h), so a stage is one A block of 16.5 KiB and WN/2 B blocks of
+// 17 KiB that move HBM -> LDS with gfx950's direct global_load_lds in 1 KiB pieces, without
+// register staging, into a ring of 3 (WN = 4) or 4 (WN = 2) stages; one barrier per stage.
 //
 // The workgroups are persistent: grid = resident workgroups, tile index strides by the grid,
 // and the number of row tiles is read from device memory (the router wrote it), so no host
@@ -27,96 +25,97 @@
 
 namespace afd {
 
-constexpr int kBM = kBlockM;  // 128
-constexpr int kBN = 256;
-constexpr int kBK = 128;
-constexpr int kThreads = 256;
-constexpr int kAStage = kBM * kBK;       // fp8 A bytes per stage
-constexpr int kBStage = kBN * kBK / 2;   // fp4 B bytes per stage
-constexpr int kSAStage = kBM * 4;
-constexpr int kSBStage = kBN * 4;
-constexpr int kStage = kAStage + kBStage + kSAStage + kSBStage;
-constexpr int kStages = 4;
-constexpr int kCopiesPerStage = 10;  // per wavefront: 4 A + 4 B + 1 A-scale + 1 B-scale
-constexpr int kLdsBytes = kStages * kStage;
-constexpr int kHStride = 132;  // fp32 stride of the gate_up epilogue tile (128 + 4)
-constexpr int kYStride = 264;  // bf16 stride of the down epilogue tile (256 + 8)
-static_assert(kBM * kHStride * 4 <= kLdsBytes, "gate_up epilogue tile must fit the stages");
-static_assert(kBM * kYStride * 2 <= kLdsBytes, "down epilogue tile must fit the stages");
-
 enum { kGateUp = 0, kDown = 1 };
 
 struct MxGemmArgs {
-  const uint8_t* a;             // gate_up: xq [n][K]; down: hq [np][K]
-  const uint8_t* as;            // UE8M0 [rows][K/32]
+  const uint8_t* a_img;         // A images [row tiles][K/128]
+  const uint8_t* b_img;         // B images [E][N/256][K/128]
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
   const int32_t* num_tiles;     // [1]
-  const uint8_t* b;             // e2m1 [E][N][K/2]
-  const uint8_t* bs;            // UE8M0 [E][N][K/32]
-  int K, N, topk;
-  uint8_t* hq;   // gate_up out: e4m3 [np][N/2]
-  uint8_t* hs;   // gate_up out: UE8M0 [np][N/64]
-  uint16_t* y;   // down out: bf16 [np][N]
+  int K, N;
+  uint8_t* h_img;  // gate_up out: the down GEMM's A images [row tiles][N/256]
+  uint16_t* y;     // down out: bf16 [np][N]
 };
 
-__device__ __forceinline__ int a_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-__device__ __forceinline__ int b_off(int n, int c) { return n * 64 + ((c ^ ((n >> 1) & 3)) << 4); }
+// Shape of the workgroup tile for WN wavefronts along N.
+template <int WN>
+struct MxTile {
+  static_assert(WN == 2 || WN == 4, "tiles are 256 or 512 columns wide");
+  static constexpr int kWaves = 2 * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBM = kBlockM;  // 128 rows = one A image
+  static constexpr int kBN = 128 * WN;
+  static constexpr int kBImgs = WN / 2;  // 256-row B images per tile
+  static constexpr int kStage = kImgA + kBImgs * kImgB;
+  static constexpr int kStages = WN == 2 ? 4 : 3;
+  static constexpr int kLds = kStages * kStage;
+  static constexpr int kAChunks = 16 / kWaves;           // 1 KiB A pieces per wavefront
+  static constexpr int kBChunks = 16 * kBImgs / kWaves;  // 1 KiB B pieces per wavefront
+  // wavefronts [0, kBImgs) also copy one B image's scales, wavefront kBImgs the A scales
+  static constexpr int kCopiesLead = kAChunks + kBChunks + 1;
+  static constexpr int kCopiesRest = kAChunks + kBChunks;
+  static constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
+  static constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
+  static_assert(kBM * kHStride * 4 <= kLds, "gate_up epilogue tile must fit the stages");
+  static_assert(kBM * kYStride * 2 <= kLds, "down epilogue tile must fit the stages");
+  static_assert(kLds <= 160 * 1024, "LDS of one CU");
+};
 
-template <int MODE>
-__device__ __forceinline__ int64_t a_row(const MxGemmArgs& p, int m) {
-  if (MODE == kGateUp) {
-    int sp = p.sorted_pairs[m];
-    return sp >= 0 ? sp / p.topk : 0;
-  }
-  return m;
+// Wait until stage kt's copies (N per stage for this wavefront) have landed; up to S later
+// stages may still be in flight.
+template <int N, int S>
+__device__ __forceinline__ void wait_stage(int kt, int KT) {
+  if (S >= 2 && kt + 2 < KT)
+    wait_vmcnt<2 * N>();
+  else if (kt + 1 < KT)
+    wait_vmcnt<N>();
+  else
+    wait_vmcnt<0>();
 }
 
-template <int MODE>
-__global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+template <int MODE, int WN>
+__global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArgs p) {
+  using T = MxTile<WN>;
+  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[T::kLds];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
-  const int ntn = p.N / kBN;
+  const int wm = wave / WN, wn = wave % WN, lr = lane & 31, lk = lane >> 5;
+  const int ntn = p.N / kBN, nt256 = p.N / kImgBRows;
   const int tiles = p.num_tiles[0] * ntn;
-  const int KT = p.K / kBK;
-  const int64_t a_ld = p.K, s_ld = p.K / 32, b_ld = p.K / 2;
+  const int KT = p.K / kImgK;
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+  const int w_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t voff = static_cast<uint32_t>(lane) * 16;
+  // this wavefront's B operand: image wn/2 of the stage, rows (wn%2)*128 + j*32 + lr
+  const int bimg = wn / 2, brow = (wn % 2) * 128;
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int mt = tile / ntn, nt = tile % ntn;
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = p.tile_expert[mt];
-
-    // Per-lane 32-bit source offsets of this tile's copies (fixed over K; the K position
-    // goes into the uniform base). Copy q of wavefront w fills 1 KiB: A rows w*32+q*8+lane/8,
-    // B rows w*64+q*16+lane/4; each lane loads the logical chunk that belongs at its
-    // swizzled LDS slot.
-    uint32_t voff_a[4], voff_b[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      int r = wave * 32 + q * 8 + (lane >> 3);
-      voff_a[q] = static_cast<uint32_t>(a_row<MODE>(p, m0 + r) * a_ld) +
-                  (static_cast<uint32_t>((lane & 7) ^ (lane >> 3)) << 4);
-      int n = wave * 64 + q * 16 + (lane >> 2);
-      voff_b[q] = static_cast<uint32_t>((e * p.N + n0 + n) * b_ld) +
-                  (static_cast<uint32_t>((lane & 3) ^ ((lane >> 3) & 3)) << 4);
-    }
-    const uint32_t voff_sa = static_cast<uint32_t>(a_row<MODE>(p, m0 + wave * 32 + (lane & 31)) * s_ld);
-    const uint32_t voff_sb = static_cast<uint32_t>((e * p.N + n0 + wave * 64 + lane) * s_ld);
-    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-    const int w_u = __builtin_amdgcn_readfirstlane(wave);
+    const uint8_t* a_tile = p.a_img + int64_t(mt) * KT * kImgA;
+    const uint8_t* b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
 
     auto issue = [&](int kt) {
       const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
-      const uint8_t* abase = p.a + kt * kBK;
-      const uint8_t* bbase = p.b + kt * (kBK / 2);
+      const uint8_t* a = a_tile + int64_t(kt) * kImgA;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) lds_dma16(st + (w_u * 32 + q * 8) * 128, abase, voff_a[q]);
+      for (int q = 0; q < T::kAChunks; ++q) {
+        const int c = w_u * T::kAChunks + q;
+        lds_dma16(st + c * 1024, a + c * 1024, voff);
+      }
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        lds_dma16(st + kAStage + (w_u * 64 + q * 16) * 64, bbase, voff_b[q]);
-      if (lane < 32) lds_dma4(st + kAStage + kBStage + w_u * 32 * 4, p.as + kt * 4, voff_sa);
-      lds_dma4(st + kAStage + kBStage + kSAStage + w_u * 64 * 4, p.bs + kt * 4, voff_sb);
+      for (int q = 0; q < T::kBChunks; ++q) {
+        const int c = w_u * T::kBChunks + q, bi = c / 16, cc = c % 16;
+        const uint8_t* b = b_tile + (int64_t(bi) * KT + kt) * kImgB;
+        lds_dma16(st + kImgA + bi * kImgB + cc * 1024, b + cc * 1024, voff);
+      }
+      if (w_u < T::kBImgs) {
+        const uint8_t* b = b_tile + (int64_t(w_u) * KT + kt) * kImgB;
+        lds_dma16(st + kImgA + w_u * kImgB + kImgData, b + kImgData, voff);
+      }
+      if (w_u == T::kBImgs && lane < 32) lds_dma16(st + kImgData, a + kImgData, voff);
     };
 
     v16f acc[2][4];
@@ -128,14 +127,15 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
         for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
     auto compute = [&](int s) {
-      const uint8_t* base = lds + s * kStage;
-      const uint32_t* sa = reinterpret_cast<const uint32_t*>(base + kAStage + kBStage);
-      const uint32_t* sb = sa + kBM;
+      const uint8_t* abase = lds + s * kStage;
+      const uint8_t* bbase = abase + kImgA + bimg * kImgB;
+      const uint32_t* sa = reinterpret_cast<const uint32_t*>(abase + kImgData);
+      const uint32_t* sb = reinterpret_cast<const uint32_t*>(bbase + kImgData);
       uint32_t sav[2], sbv[4];
 #pragma unroll
       for (int i = 0; i < 2; ++i) sav[i] = sa[wm * 64 + i * 32 + lr];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sbv[j] = sb[wn * 128 + j * 32 + lr];
+      for (int j = 0; j < 4; ++j) sbv[j] = sb[brow + j * 32 + lr];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         v8i af[2], bf[4];
@@ -145,14 +145,14 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           int r = wm * 64 + i * 32 + lr;
-          v4i lo = *reinterpret_cast<const v4i*>(base + a_off(r, ks * 4 + lk));
-          v4i hi = *reinterpret_cast<const v4i*>(base + a_off(r, ks * 4 + 2 + lk));
+          v4i lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + lk));
+          v4i hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + 2 + lk));
           af[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          int n = wn * 128 + j * 32 + lr;
-          v4i v = *reinterpret_cast<const v4i*>(base + kAStage + b_off(n, ks * 2 + lk));
+          int n = brow + j * 32 + lr;
+          v4i v = *reinterpret_cast<const v4i*>(bbase + img_b_off(n, ks * 2 + lk));
           bf[j] = v8i{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
         }
         const int sh = 8 * (ks * 2 + lk);
@@ -174,13 +174,10 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
     for (int s = 0; s < kStages - 1; ++s)
       if (s < KT) issue(s);
     for (int kt = 0; kt < KT; ++kt) {
-      // stage kt's copies are done when at most the later stages' copies are outstanding
-      if (kt + 2 < KT)
-        wait_vmcnt<2 * kCopiesPerStage>();
-      else if (kt + 1 < KT)
-        wait_vmcnt<kCopiesPerStage>();
+      if (w_u <= T::kBImgs)
+        wait_stage<T::kCopiesLead, kStages - 2>(kt, KT);
       else
-        wait_vmcnt<0>();
+        wait_stage<T::kCopiesRest, kStages - 2>(kt, KT);
       // every wavefront's copies of stage kt have landed, and every wavefront is done with
       // stage kt-1, whose buffer the next copy overwrites
       __syncthreads();
@@ -202,16 +199,18 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
             int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
             int col = wn * 64 + jj * 32 + lr;
             float g = acc[i][2 * jj][q], u = acc[i][2 * jj + 1][q];
-            hl[row * kHStride + col] = __fdividef(g, 1.0f + __expf(-g)) * u;
+            hl[row * T::kHStride + col] = __fdividef(g, 1.0f + __expf(-g)) * u;
           }
       __syncthreads();
-      const int inter = p.N / 2;
+      // the 128 x (kBN/2) h tile is WN/2 K stages of the down GEMM's A operand, starting at
+      // stage n0/256 of row tile mt
+      constexpr int kBlocksPerRow = kBN / 64;  // MX blocks of 32 h columns
+      const int kt_down = p.N / kImgBRows;     // K stages of the down GEMM (I / 128)
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
-        int b = t + half * kThreads;  // 128 rows x 4 MX blocks
-        int row = b >> 2, cb = b & 3;
-        int grow = m0 + row;
-        const float* src = hl + row * kHStride + cb * 32;
+        int b = t + half * T::kThreads;
+        int row = b / kBlocksPerRow, cb = b % kBlocksPerRow;
+        const float* src = hl + row * T::kHStride + cb * 32;
         float v[32];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -231,12 +230,11 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
         for (int i = 0; i < 8; ++i)
           out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv,
                                                         v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
-        if (p.sorted_pairs[grow] >= 0) {
-          v4i* dst = reinterpret_cast<v4i*>(p.hq + int64_t(grow) * inter + n0 / 2 + cb * 32);
-          dst[0] = out[0];
-          dst[1] = out[1];
-          p.hs[int64_t(grow) * (inter / 32) + n0 / 64 + cb] = static_cast<uint8_t>(code);
-        }
+        const int j = cb % 4;
+        uint8_t* img = p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + cb / 4) * kImgA;
+        *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j)) = out[0];
+        *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j + 1)) = out[1];
+        img[kImgData + row * 4 + j] = static_cast<uint8_t>(code);
       }
       __syncthreads();
     } else {
@@ -249,82 +247,80 @@ __global__ __launch_bounds__(kThreads) void mx_gemm_kernel(MxGemmArgs p) {
           for (int q = 0; q < 16; ++q) {
             int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
             int col = wn * 128 + j * 32 + lr;
-            yl[row * kYStride + col] = f32_to_bf16(acc[i][j][q]);
+            yl[row * T::kYStride + col] = f32_to_bf16(acc[i][j][q]);
           }
       __syncthreads();
+      constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
 #pragma unroll 4
       for (int q = 0; q < 16; ++q) {
-        int idx = q * kThreads + t;  // 128 rows x 32 chunks of 8 bf16
-        int row = idx >> 5, c = idx & 31;
+        int idx = q * T::kThreads + t;
+        int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
         int grow = m0 + row;
         if (p.sorted_pairs[grow] >= 0)
           *reinterpret_cast<v4i*>(p.y + int64_t(grow) * p.N + n0 + c * 8) =
-              *reinterpret_cast<const v4i*>(yl + row * kYStride + c * 8);
+              *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8);
       }
       __syncthreads();
     }
   }
 }
 
-template <int MODE>
-static int persistent_grid(int max_tiles) {
+template <int MODE, int WN>
+static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream) {
+  using T = MxTile<WN>;
   static int per_cu = 0;  // resident workgroups per CU (registers and LDS decide)
   if (per_cu == 0) {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE>, kThreads, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE, WN>, T::kThreads,
+                                                     0) != hipSuccess ||
         b < 1)
       b = 1;
     per_cu = b;
   }
-  int g = device_cu_count() * per_cu;
-  return max_tiles < g ? (max_tiles < 1 ? 1 : max_tiles) : g;
+  const int max_tiles = max_row_tiles * (p.N / T::kBN);
+  int grid = device_cu_count() * per_cu;
+  if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
+  hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, p);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+template <int MODE>
+static int launch_mx_any(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream) {
+  if (p.N % MxTile<4>::kBN == 0) return launch_mx<MODE, 4>(p, max_row_tiles, stream);
+  return launch_mx<MODE, 2>(p, max_row_tiles, stream);
 }
 
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                       const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
   MxGemmArgs p;
-  p.a = ws + L.xq;
-  p.as = ws + L.xs;
+  p.a_img = ws + L.xq;
+  p.b_img = static_cast<const uint8_t*>(wt.w13);
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
-  p.b = static_cast<const uint8_t*>(wt.w13);
-  p.bs = static_cast<const uint8_t*>(wt.s13);
   p.K = cfg.hidden;
   p.N = 2 * cfg.inter;
-  p.topk = cfg.topk;
-  p.hq = ws + L.hq;
-  p.hs = ws + L.hs;
+  p.h_img = ws + L.hq;
   p.y = nullptr;
-  int grid = persistent_grid<kGateUp>(L.max_tiles * (p.N / kBN));
-  hipLaunchKernelGGL(mx_gemm_kernel<kGateUp>, dim3(grid), dim3(kThreads), 0, stream, p);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
+  return launch_mx_any<kGateUp>(p, L.max_tiles, stream);
 }
 
 int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                    const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
   MxGemmArgs p;
-  p.a = ws + L.hq;
-  p.as = ws + L.hs;
+  p.a_img = ws + L.hq;
+  p.b_img = static_cast<const uint8_t*>(wt.w2);
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
-  p.b = static_cast<const uint8_t*>(wt.w2);
-  p.bs = static_cast<const uint8_t*>(wt.s2);
   p.K = cfg.inter;
   p.N = cfg.hidden;
-  p.topk = cfg.topk;
-  p.hq = nullptr;
-  p.hs = nullptr;
+  p.h_img = nullptr;
   p.y = reinterpret_cast<uint16_t*>(ws + L.y);
-  int grid = persistent_grid<kDown>(L.max_tiles * (p.N / kBN));
-  hipLaunchKernelGGL(mx_gemm_kernel<kDown>, dim3(grid), dim3(kThreads), 0, stream, p);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
+  return launch_mx_any<kDown>(p, L.max_tiles, stream);
 }
 
 }  // namespace afd

@@ -187,8 +187,13 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
     return at;
   };
   afd_ws_layout L;
-  L.xq = take(uint64_t(n) * H);
-  L.xs = take(mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
+  const uint64_t max_tiles = uint64_t(np_max / kBlockM);
+  // MXFP4: xq holds the gate_up A images (every padded row, gathered and quantized) and hq
+  // the down A images; their scales live inside the images (xs, hs empty).
+  // FP8 block: xq / xs are the per-token e4m3 rows and fp32 1x128 scales, hq / hs the
+  // padded-row intermediate and its scales.
+  L.xq = take(mx ? max_tiles * (H / kImgK) * kImgA : uint64_t(n) * H);
+  L.xs = take(mx ? 0 : uint64_t(n) * (H / 128) * 4);
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
   L.padded_offsets = take((E + 1) * 4);
@@ -197,8 +202,8 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.tile_expert = take(uint64_t(np_max / kBlockM) * 4);
   L.num_tiles = take(4);
   L.hist = take(uint64_t(128) * E * 4);
-  L.hq = take(uint64_t(np_max) * I);
-  L.hs = take(mx ? uint64_t(np_max) * (I / 32) : uint64_t(np_max) * (I / 128) * 4);
+  L.hq = take(mx ? max_tiles * (I / kImgK) * kImgA : uint64_t(np_max) * I);
+  L.hs = take(mx ? 0 : uint64_t(np_max) * (I / 128) * 4);
   L.y = take(uint64_t(np_max) * H * 2);
   L.total = o;
   L.np_max = np_max;
@@ -215,8 +220,8 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   afd_ws_layout L;
   int st = afd_workspace_layout(cfg, n, &L);
   if (st != AFD_OK) return st;
-  if (!weights || !weights->w13 || !weights->s13 || !weights->w2 || !weights->s2)
-    return AFD_ERR_ARG;
+  if (!weights || !weights->w13 || !weights->w2) return AFD_ERR_ARG;
+  if (cfg->weight_fmt == AFD_W_FP8_BLOCK && (!weights->s13 || !weights->s2)) return AFD_ERR_ARG;
   if (n > 0 && (!x || !ids || !w || !out)) return AFD_ERR_ARG;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
@@ -229,14 +234,16 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   if (n > 0) {
     uint8_t* wsb = static_cast<uint8_t*>(ws);
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
+    if ((st = launch_route(ids, n, *cfg, wsb, L, s)) != AFD_OK) return st;
+    if ((st = mark(1)) != AFD_OK) return st;
     if (mx)
-      st = afd_quant_mxfp8(x, n, cfg->hidden, wsb + L.xq, wsb + L.xs, stream);
+      st = launch_gather_quant_mxfp8(x, reinterpret_cast<const int32_t*>(wsb + L.sorted_pairs),
+                                     reinterpret_cast<const int32_t*>(wsb + L.num_tiles),
+                                     cfg->topk, cfg->hidden, L.np_max, wsb + L.xq, s);
     else
       st = afd_quant_fp8_1x128(x, n, cfg->hidden, wsb + L.xq,
                                reinterpret_cast<float*>(wsb + L.xs), stream);
-    if (st != AFD_OK || (st = mark(1)) != AFD_OK) return st;
-    if ((st = launch_route(ids, n, *cfg, wsb, L, s)) != AFD_OK) return st;
-    if ((st = mark(2)) != AFD_OK) return st;
+    if (st != AFD_OK || (st = mark(2)) != AFD_OK) return st;
     st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, n, s)
             : launch_fp8_gate_up(*cfg, *weights, wsb, L, n, s);
     if (st != AFD_OK || (st = mark(3)) != AFD_OK) return st;

@@ -3,10 +3,18 @@
 // 32-element MX block (16 B fp4 or 32 B fp8 out, 1 scale byte), so every load is a 16-byte
 // vector and no cross-lane reduction is needed for MX; FP8 groups of 128 reduce over 4 lanes.
 #include "afd_common.h"
+#include "afd_internal.h"
 
 namespace afd {
 
 constexpr int kQuantThreads = 256;
+
+static int grid_for(int64_t items) {
+  int64_t g = (items + kQuantThreads - 1) / kQuantThreads;
+  if (g > 8192) g = 8192;  // grid-stride beyond 32 workgroups per CU
+  return static_cast<int>(g < 1 ? 1 : g);
+}
+
 
 // Logical source row of physical row r when gate and up rows are interleaved in groups of g
 // (rows = 2I = [gate; up]): physical 2g*j + q is gate row g*j + q for q < g, else up row.
@@ -104,15 +112,20 @@ __global__ __launch_bounds__(kQuantThreads) void quant_fp8_1x128_kernel(
 }
 
 // ---------------------------------------------------------------- MXFP4 weight packer
+// One lane per 32-element block of a physical row: 16 bytes of e2m1 codes (one logical
+// 16-byte chunk of a B image, since 32 fp4 values = 16 bytes) plus one UE8M0 scale, written
+// into the tile image of (matrix, 256-row tile, 128-wide K stage).
 __global__ __launch_bounds__(kQuantThreads) void pack_mxfp4_kernel(
     const float* __restrict__ w, int64_t blocks, int rows, int cols, int gate_up,
-    uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
+    uint8_t* __restrict__ out) {
   const int bpr = cols / kMxBlock;
+  const int kstages = cols / kImgK, ntiles = rows / kImgBRows;
   for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
        b += int64_t(gridDim.x) * kQuantThreads) {
     int64_t prow = b / bpr;  // physical row over all matrices
     int cb = static_cast<int>(b % bpr);
-    int64_t mat = prow / rows, r = prow % rows;
+    int64_t mat = prow / rows;
+    int r = static_cast<int>(prow % rows);
     int64_t lr = gate_up ? gate_up_source_row(r, rows, 32) : r;
     const v4f* src = reinterpret_cast<const v4f*>(w + (mat * rows + lr) * cols + cb * kMxBlock);
     float v[32];
@@ -129,17 +142,82 @@ __global__ __launch_bounds__(kQuantThreads) void pack_mxfp4_kernel(
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
     uint32_t code = mx_scale_code(amax, 2);
     float inv = mx_inv_scale(code);
-    v4i out;
+    v4i packed;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t packed = 0;
+      uint32_t word = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) packed |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
-      out[i] = static_cast<int>(packed);
+      for (int j = 0; j < 8; ++j) word |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
+      packed[i] = static_cast<int>(word);
     }
-    *reinterpret_cast<v4i*>(q + prow * (cols / 2) + cb * 16) = out;
-    s[prow * bpr + cb] = static_cast<uint8_t>(code);
+    const int nt = r / kImgBRows, n = r % kImgBRows;
+    const int ks = cb / 4, j = cb % 4;
+    uint8_t* img = out + ((mat * ntiles + nt) * kstages + ks) * int64_t(kImgB);
+    *reinterpret_cast<v4i*>(img + img_b_off(n, j)) = packed;
+    img[kImgData + n * 4 + j] = static_cast<uint8_t>(code);
   }
+}
+
+// ---------------------------------------------------------------- MXFP8 gather + quantize
+// The A operand of the grouped gate_up GEMM: for every padded row p (rows in expert order,
+// as the router laid them out), the token's activations quantized to MXFP8 and written into
+// the A tile images of row tile p/128. Padding rows get zero codes and zero scales.
+__global__ __launch_bounds__(kQuantThreads) void gather_quant_mxfp8_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ sorted_pairs,
+    const int32_t* __restrict__ num_tiles, int topk, int cols, uint8_t* __restrict__ out) {
+  const int bpr = cols / kMxBlock, kstages = cols / kImgK;
+  const int64_t blocks = int64_t(num_tiles[0]) * kImgARows * bpr;
+  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
+       b += int64_t(gridDim.x) * kQuantThreads) {
+    const int64_t p = b / bpr;
+    const int cb = static_cast<int>(b % bpr);
+    const int sp = sorted_pairs[p];
+    v4i out0 = {0, 0, 0, 0}, out1 = {0, 0, 0, 0};
+    uint32_t code = 0;
+    if (sp >= 0) {
+      const v4i* src = reinterpret_cast<const v4i*>(x + int64_t(sp / topk) * cols + cb * kMxBlock);
+      float v[32];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v4i raw = src[i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t u = static_cast<uint32_t>(raw[q]);
+          v[i * 8 + q * 2] = __uint_as_float(u << 16);
+          v[i * 8 + q * 2 + 1] = __uint_as_float(u & 0xffff0000u);
+        }
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+      code = mx_scale_code(amax, 8);
+      const float inv = mx_inv_scale(code);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        out0[i] = static_cast<int>(
+            pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv, v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
+        out1[i] = static_cast<int>(pk4_e4m3(v[16 + i * 4] * inv, v[17 + i * 4] * inv,
+                                            v[18 + i * 4] * inv, v[19 + i * 4] * inv));
+      }
+    }
+    const int64_t mt = p / kImgARows;
+    const int r = static_cast<int>(p % kImgARows);
+    const int ks = cb / 4, j = cb % 4;
+    uint8_t* img = out + (mt * kstages + ks) * int64_t(kImgA);
+    *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j)) = out0;
+    *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j + 1)) = out1;
+    img[kImgData + r * 4 + j] = static_cast<uint8_t>(code);
+  }
+}
+
+int launch_gather_quant_mxfp8(const uint16_t* x, const int32_t* sorted_pairs,
+                              const int32_t* num_tiles, int topk, int cols, int64_t max_rows,
+                              uint8_t* out, hipStream_t stream) {
+  const int64_t blocks = max_rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(gather_quant_mxfp8_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+                     stream, x, sorted_pairs, num_tiles, topk, cols, out);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
 }
 
 // Physical row of logical row lr when gate and up rows are interleaved in groups of g
@@ -202,12 +280,6 @@ __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
   if (t == 0) s[(mat * rbs + rb) * cbs + cb] = sc;
 }
 
-static int grid_for(int64_t items) {
-  int64_t g = (items + kQuantThreads - 1) / kQuantThreads;
-  if (g > 8192) g = 8192;  // grid-stride beyond 32 workgroups per CU
-  return static_cast<int>(g < 1 ? 1 : g);
-}
-
 }  // namespace afd
 
 using namespace afd;
@@ -237,15 +309,14 @@ extern "C" int afd_quant_fp8_1x128(const uint16_t* x, int64_t rows, int32_t cols
 }
 
 extern "C" int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols,
-                              int32_t gate_up, uint8_t* q, uint8_t* s, afd_stream_t stream) {
-  if (!w || !q || !s || mats < 0) return AFD_ERR_ARG;
-  if (rows <= 0 || cols <= 0 || cols % kMxBlock) return AFD_ERR_SHAPE;
-  if (gate_up && rows % 64) return AFD_ERR_SHAPE;
+                              int32_t gate_up, uint8_t* out, afd_stream_t stream) {
+  if (!w || !out || mats < 0) return AFD_ERR_ARG;
+  if (rows <= 0 || cols <= 0 || rows % kImgBRows || cols % kImgK) return AFD_ERR_SHAPE;
   if (mats == 0) return AFD_OK;
   int64_t blocks = mats * rows * (cols / kMxBlock);
   hipLaunchKernelGGL(pack_mxfp4_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
                      static_cast<hipStream_t>(stream), w, blocks, rows, cols, gate_up ? 1 : 0,
-                     q, s);
+                     out);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }

@@ -107,7 +107,7 @@ _SIGS = {
     "afd_status_string": ([_I32], ctypes.c_char_p),
     "afd_last_hip_error": ([], _I32),
     "afd_workspace_layout": ([ctypes.POINTER(AfdMoeCfg), _I32, ctypes.POINTER(AfdWsLayout)], _I32),
-    "afd_pack_mxfp4": ([_P, _I64, _I32, _I32, _I32, _P, _P, _P], _I32),
+    "afd_pack_mxfp4": ([_P, _I64, _I32, _I32, _I32, _P, _P], _I32),
     "afd_pack_fp8_block": ([_P, _I64, _I32, _I32, _I32, _P, _P, _P], _I32),
     "afd_quant_mxfp8": ([_P, _I64, _I32, _P, _P, _P], _I32),
     "afd_quant_fp8_1x128": ([_P, _I64, _I32, _P, _P, _P], _I32),

@@ -49,9 +49,10 @@ class ExpertWeights:
     s2: torch.Tensor
 
     def as_struct(self) -> _lib.AfdExpertWeights:
-        return _lib.AfdExpertWeights(
-            self.w13.data_ptr(), self.s13.data_ptr(), self.w2.data_ptr(), self.s2.data_ptr()
-        )
+        def ptr(t):
+            return t.data_ptr() if t.numel() else None
+
+        return _lib.AfdExpertWeights(ptr(self.w13), ptr(self.s13), ptr(self.w2), ptr(self.s2))
 
     @property
     def nbytes(self) -> int:
@@ -63,11 +64,12 @@ def _as_f32(w: torch.Tensor, device) -> torch.Tensor:
 
 
 def pack_mxfp4_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> ExpertWeights:
-    """Quantize logical expert weights to MXFP4 in the kernel layout, on the GPU.
+    """Quantize logical expert weights to MXFP4 in the kernel's tile-image layout, on the GPU.
 
     w13: [E, 2I, H] with rows [gate; up] (SGLang's w13 mapping, ``srt/models/deepseek_v4.py:132-137``);
-    w2: [E, H, I]. Any float dtype. The reference's checkpoints hold the same format
-    (int8-packed e2m1 + E8M0 per 32, ``srt/configs/model_config.py:3-7``).
+    w2: [E, H, I]. Any float dtype. The reference's checkpoints hold the same number format
+    (int8-packed e2m1 + E8M0 per 32, ``srt/configs/model_config.py:3-7``); the images carry
+    the codes and the scales together (include/afd.h describes the layout).
     """
     device = torch.device(device or "cuda")
     e, two_i, h = w13.shape
@@ -76,15 +78,14 @@ def pack_mxfp4_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> Expe
         raise ValueError(f"w2 shape {tuple(w2.shape)} does not match w13 {tuple(w13.shape)}")
     a = _as_f32(w13, device)
     b = _as_f32(w2, device)
-    q13 = torch.empty(e, two_i, h // 2, dtype=torch.uint8, device=device)
-    s13 = torch.empty(e, two_i, h // MX_BLOCK, dtype=torch.uint8, device=device)
-    q2 = torch.empty(e, h, inter // 2, dtype=torch.uint8, device=device)
-    s2 = torch.empty(e, h, inter // MX_BLOCK, dtype=torch.uint8, device=device)
+    img13 = torch.empty(e, two_i * (h // 2 + h // MX_BLOCK), dtype=torch.uint8, device=device)
+    img2 = torch.empty(e, h * (inter // 2 + inter // MX_BLOCK), dtype=torch.uint8, device=device)
+    none = torch.empty(0, dtype=torch.uint8, device=device)
     with torch.cuda.device(device):
         st = _stream_handle()
-        _lib.call("afd_pack_mxfp4", a.data_ptr(), e, two_i, h, 1, q13.data_ptr(), s13.data_ptr(), st)
-        _lib.call("afd_pack_mxfp4", b.data_ptr(), e, h, inter, 0, q2.data_ptr(), s2.data_ptr(), st)
-    return ExpertWeights("mxfp4", e, h, inter, q13, s13, q2, s2)
+        _lib.call("afd_pack_mxfp4", a.data_ptr(), e, two_i, h, 1, img13.data_ptr(), st)
+        _lib.call("afd_pack_mxfp4", b.data_ptr(), e, h, inter, 0, img2.data_ptr(), st)
+    return ExpertWeights("mxfp4", e, h, inter, img13, none, img2, none)
 
 
 def pack_fp8_block_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> ExpertWeights:

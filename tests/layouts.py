@@ -1,0 +1,42 @@
+"""numpy statement of the MX GEMM operand tile images (the layout include/afd.h documents),
+used by the tests to compare the GPU's packed bytes with the oracle's codes and scales."""
+
+import numpy as np
+
+IMG_DATA = 16384
+IMG_A = IMG_DATA + 128 * 4
+IMG_B = IMG_DATA + 256 * 4
+
+
+def b_images(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """packed e2m1 [E, N, K/2] + UE8M0 [E, N, K/32] -> images [E, N/256, K/128, IMG_B]."""
+    e, n, kb = packed.shape
+    k = kb * 2
+    nt, kt = n // 256, k // 128
+    data = packed.reshape(e, nt, 256, kt, 4, 16).transpose(0, 1, 3, 2, 4, 5)  # e nt kt row chunk byte
+    sc = scales.reshape(e, nt, 256, kt, 4).transpose(0, 1, 3, 2, 4)  # e nt kt row j
+    img = np.zeros((e, nt, kt, IMG_B), dtype=np.uint8)
+    body = np.zeros((e, nt, kt, 256, 4, 16), dtype=np.uint8)
+    rows = np.arange(256)
+    for c in range(4):
+        phys = c ^ ((rows >> 1) & 3)
+        body[:, :, :, rows, phys, :] = data[:, :, :, rows, c, :]
+    img[..., :IMG_DATA] = body.reshape(e, nt, kt, IMG_DATA)
+    img[..., IMG_DATA:] = sc.reshape(e, nt, kt, 256 * 4)
+    return img
+
+
+def a_rows(images: np.ndarray, k: int):
+    """A images [tiles * K/128 * IMG_A] bytes -> (codes [tiles*128, K], scales [tiles*128, K/32])."""
+    kt = k // 128
+    img = images.reshape(-1, kt, IMG_A)
+    tiles = img.shape[0]
+    body = img[..., :IMG_DATA].reshape(tiles, kt, 128, 8, 16)
+    rows = np.arange(128)
+    data = np.zeros((tiles, kt, 128, 8, 16), dtype=np.uint8)
+    for c in range(8):
+        phys = c ^ (rows & 7)
+        data[:, :, rows, c, :] = body[:, :, rows, phys, :]
+    codes = data.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, k)
+    sc = img[..., IMG_DATA:].reshape(tiles, kt, 128, 4).transpose(0, 2, 1, 3).reshape(tiles * 128, k // 32)
+    return codes, sc

@@ -44,7 +44,11 @@ def test_workspace_layout_dsv4_rank():
     L = workspace_layout(cfg, 16384)
     assert L["block_m"] == 128
     assert L["np_max"] == (16384 * 8 + 64 * 127 + 127) // 128 * 128
-    assert L["xq"] == 0 and L["xs"] == 16384 * 4096
+    tiles = L["np_max"] // 128
+    assert L["max_tiles"] == tiles
+    # MXFP4: xq holds one A tile image (16896 B) per row tile and 128-wide K stage
+    assert L["xq"] == 0 and L["xs"] == tiles * (4096 // 128) * 16896
+    assert L["hs"] - L["hq"] == tiles * (2048 // 128) * 16896
     offs = [L[k] for k in ("xq", "xs", "counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos",
                            "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)

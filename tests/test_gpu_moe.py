@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 import torch
 
+import layouts as L
 from gpu_util import bits16, dev, rel_l2, say, u8
 from oracle import experts as OX
 from oracle import formats as F
@@ -71,13 +72,19 @@ def test_tiny_layer_mxfp4():
     s = W.SHAPES["tiny"]
     experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k, s.tokens, "mxfp4", seed=0)
     assert_close(out, ref, ids.numpy(), s.local)
-    # intermediates: quantized x and the routing are bit-exact
+    # intermediates: the routing and the gathered, quantized activations are bit-exact
     n, k = ids.shape
-    xq = u8(experts.ws_view("xq", torch.uint8, n * s.hidden, n)).reshape(n, s.hidden)
-    q_ref, _ = F.mx_quantize(F.bf16_to_f32(bits16(x)), "e4m3")
-    assert np.array_equal(xq, q_ref)
     pos = experts.ws_view("pair_pos", torch.int32, n * k, n).cpu().numpy()
     assert np.array_equal(pos, parts["route"]["pair_pos"])
+    sp = parts["route"]["sorted_pairs"]
+    tiles = len(sp) // 128
+    img = u8(experts.ws_view("xq", torch.uint8, tiles * (s.hidden // 128) * L.IMG_A, n))
+    codes, scales = L.a_rows(img, s.hidden)
+    q_ref, s_ref = F.mx_quantize(F.bf16_to_f32(bits16(x)), "e4m3")
+    valid = sp >= 0
+    assert np.array_equal(codes[valid], q_ref[sp[valid] // k])
+    assert np.array_equal(scales[valid], s_ref[sp[valid] // k])
+    assert not codes[~valid].any() and not scales[~valid].any()
 
 
 @pytest.mark.parametrize(
