@@ -1,0 +1,61 @@
+"""One attention rank and one FFN rank on one MI355X: the AFD loop of a single GPU.
+
+Wires the pieces the reference runs in separate processes (``AsapBuffer.connect``,
+``python/sgl_asap_plugin/srt/layers/moe/token_dispatcher/asap.py:99-147``;
+``FfnScheduler.init_ffn_server``, ``srt/managers/scheduler.py:220-312``) into one process:
+
+    AsapMoE.forward -> AsapDispatcher.dispatch -> AttnChannel.send   (A send stream)
+        copies x / ids / w into the RecvArena, rings the doorbell
+    [shared experts on the compute stream]
+    AsapDispatcher.combine -> AsapBuffer.recv
+        pump: FfnServer.poll -> FfnScheduler.run_job                (F stream)
+            waits on the doorbell, runs the experts into A's result segment, rings done
+        AttnChannel.wait (compute stream) -> afd_combine (+ shared)
+
+Every wait is enqueued after the work that satisfies it (host order equals causal order),
+so the loop cannot deadlock even when streams share a hardware queue.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional
+
+import torch
+
+from .moe.dispatcher import AsapBuffer
+from .runner.scheduler import FfnScheduler
+from .transport.channel import AttnChannel
+from .transport.layout import Geometry
+from .transport.server import FfnServer
+
+
+class OneGpuAfd:
+    def __init__(self, experts: Dict[int, torch.nn.Module], *, n_max: int, slots: int = 2,
+                 seq_base: int = 0, graph_max_tokens: int = 0, timeout_s: float = 60.0,
+                 device: int = 0, reply_stream: bool = True, timing: bool = False,
+                 _backpressure: bool = True, _epoch_override: Optional[int] = None):
+        first = next(iter(experts.values()))
+        if first.n_max < n_max:
+            raise ValueError(f"experts hold workspaces for {first.n_max} tokens, the loop carries up to {n_max}")
+        self.geometry = Geometry(num_a=1, group=1, slots=slots, n_max=n_max, hidden=first.hidden_size,
+                                 topk=first.top_k, num_f=1)
+        self.server = FfnServer(0, self.geometry, device=device, seq_base=seq_base).start()
+        self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens,
+                                      reply_stream=reply_stream, timing=timing)
+        self.channel = AttnChannel(0, self.geometry, [self.server], device=device, seq_base=seq_base,
+                                   timeout_s=timeout_s, _backpressure=_backpressure,
+                                   _epoch_override=_epoch_override).connect()
+        self.buffer = AsapBuffer.install(self.channel, device, pump=self.scheduler.serve_pending)
+
+    def close(self) -> None:
+        torch.cuda.synchronize()
+        if AsapBuffer._buffer is self.buffer:
+            AsapBuffer.uninstall()
+        self.channel.close()
+        self.server.close()
+
+    def __enter__(self) -> "OneGpuAfd":
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self.close()

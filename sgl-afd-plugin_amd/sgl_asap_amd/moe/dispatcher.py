@@ -1,0 +1,143 @@
+"""Token dispatcher of an attention (A) rank whose routed experts run on the FFN (F) ranks.
+
+Same surface as ``python/sgl_asap_plugin/srt/layers/moe/token_dispatcher/asap.py``:
+``AsapDispatcher(layer_id).dispatch(hidden_states, topk_output, micro_batch)`` enqueues the
+send of one layer's tokens (empty batch -> empty output, non-standard top-k -> RuntimeError,
+n > n_max -> chunked ``exchange``; :48-73) and ``combine`` returns the sum of the F ranks'
+partial outputs (:75-78). ``AsapBuffer`` is the rank's connection (``send`` :149-172: bf16
+check -> TypeError, int32 ids, fp32 weights, the send stream waits on the compute stream;
+``recv`` :174-184: waits, then one part is cloned and several are summed in fp32, in F-rank
+order, into a new bf16 tensor; ``exchange`` :186-193).
+
+The sum is one gfx950 kernel (``afd_combine``) that can also add the shared experts' output
+(``combine(..., shared_output=)``): bf16(fp32(routed) + fp32(shared)), the same two
+roundings as the reference's recv followed by SGLang's plain shared add
+(``srt/layers/moe/ep_moe/layer.py:29-33``).
+
+On one GPU the F rank is in-process: ``AsapBuffer.pump`` (if set) is called before a wait
+is enqueued so the F side has enqueued its job first, which keeps host order equal to causal
+order on the device (no stream can ever wait on work that is enqueued after it).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Callable, NamedTuple, Optional
+
+import torch
+
+from .. import _lib
+from .topk import format_is_standard
+
+# The slot of a whole batch; micro-batch i of two-batch overlap uses slot i.
+SLOT = 0
+
+
+class AsapDispatchOutput(NamedTuple):
+    ticket: Optional[object]  # the pending send, None when ``hidden_states`` is final
+    hidden_states: Optional[torch.Tensor]
+    keepalive: tuple = ()  # the tensors the send's copies read, until the answer
+
+
+def combine_parts(parts, shared: Optional[torch.Tensor], n_tokens: int, hidden: int, device) -> torch.Tensor:
+    """bf16 [n, hidden] = bf16(sum_f fp32(part_f)) (+ shared) from device pointers ``parts``."""
+    out = torch.empty(n_tokens, hidden, dtype=torch.bfloat16, device=device)
+    if n_tokens == 0:
+        return out
+    arr = (ctypes.c_void_p * len(parts))(*parts)
+    shared_ptr = None
+    if shared is not None:
+        if shared.dtype != torch.bfloat16 or tuple(shared.shape) != (n_tokens, hidden):
+            raise ValueError(f"shared output must be bf16 [{n_tokens}, {hidden}], got {shared.dtype} {tuple(shared.shape)}")
+        shared = shared.contiguous()
+        shared_ptr = shared.data_ptr()
+    _lib.call("afd_combine", arr, len(parts), shared_ptr, out.data_ptr(), n_tokens * hidden,
+              torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+class AsapDispatcher:
+    def __init__(self, layer_id: int):
+        self.layer_id = layer_id
+
+    def dispatch(self, hidden_states: torch.Tensor, topk_output, micro_batch: Optional[int] = None) -> AsapDispatchOutput:
+        """``micro_batch``: index of a two-batch-overlap micro-batch, None for a whole batch."""
+        if hidden_states.shape[0] == 0:
+            return AsapDispatchOutput(None, hidden_states.new_empty(hidden_states.shape))
+        if not format_is_standard(topk_output):
+            raise RuntimeError(f"ASAP sends explicit top-k ids and weights, got {type(topk_output).__name__}")
+        buffer = AsapBuffer.get()
+        ids, weights = topk_output.topk_ids, topk_output.topk_weights
+        if hidden_states.shape[0] > buffer.n_max:
+            output = buffer.exchange(self.layer_id, hidden_states, ids, weights)
+            return AsapDispatchOutput(None, output)
+        ticket, keepalive = buffer.send(self.layer_id, hidden_states, ids, weights, micro_batch)
+        return AsapDispatchOutput(ticket, None, keepalive)
+
+    def combine(self, combine_input: AsapDispatchOutput, shared_output: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if combine_input.hidden_states is not None:
+            out = combine_input.hidden_states
+            if shared_output is not None and out.numel():
+                out = combine_parts([out.contiguous().data_ptr()], shared_output, out.shape[0], out.shape[1], out.device)
+            return out
+        return AsapBuffer.get().recv(combine_input.ticket, shared_output)
+
+
+class AsapBuffer:
+    """The attention rank's channel to the FFN ranks, with its send stream."""
+
+    _buffer: Optional["AsapBuffer"] = None
+
+    def __init__(self, channel, device: int, pump: Optional[Callable[[], object]] = None):
+        self.channel, self.device = channel, device
+        self.n_max = channel.g.n_max
+        self.hidden = channel.g.hidden
+        self.send_stream = torch.cuda.Stream(device)
+        self.pump = pump
+
+    @classmethod
+    def get(cls) -> "AsapBuffer":
+        if cls._buffer is None:
+            raise RuntimeError("This attention rank is not connected to the FFN ranks")
+        return cls._buffer
+
+    @classmethod
+    def install(cls, channel, device: int, pump: Optional[Callable[[], object]] = None) -> "AsapBuffer":
+        cls._buffer = cls(channel, device, pump)
+        return cls._buffer
+
+    @classmethod
+    def uninstall(cls) -> None:
+        cls._buffer = None
+
+    def send(self, layer_id: int, x, ids, weights, micro_batch=None):
+        """Enqueue one message -> (ticket, the tensors its copies read). The send stream waits
+        for the work that produced the inputs; the caller keeps them until the answer."""
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"ASAP carries bf16 activations, got {x.dtype}")
+        x = x.contiguous()
+        ids = ids.to(torch.int32).contiguous()
+        weights = weights.to(torch.float32).contiguous()
+        slot = SLOT if micro_batch is None else micro_batch
+        self.send_stream.wait_stream(torch.cuda.current_stream())
+        ticket = self.channel.send(layer_id, slot, x.data_ptr(), ids.data_ptr(), weights.data_ptr(), x.shape[0], self.send_stream)
+        for t in (x, ids, weights):  # the caching allocator must not hand them out before the copies ran
+            t.record_stream(self.send_stream)
+        return ticket, (x, ids, weights)
+
+    def recv(self, ticket, shared: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The sum of the FFN ranks' partial outputs (plus ``shared``), as a new tensor: the
+        next reply overwrites the result segments."""
+        if self.pump is not None:
+            self.pump()
+        ptrs = self.channel.wait(ticket, torch.cuda.current_stream())
+        return combine_parts(ptrs, shared, ticket.n_tokens, self.hidden, f"cuda:{self.device}")
+
+    def exchange(self, layer_id: int, x, ids, weights) -> torch.Tensor:
+        """send + recv in pieces of at most n_max tokens."""
+        pieces = []
+        for i in range(0, x.shape[0], self.n_max):
+            end = i + self.n_max
+            ticket, _ = self.send(layer_id, x[i:end], ids[i:end], weights[i:end])
+            pieces.append(self.recv(ticket))
+        return torch.cat(pieces)

@@ -1,0 +1,240 @@
+"""Transport host logic on the CPU: doorbell and geometry known answers, the F poller's
+rules (cyclic sequence compare, lost messages, stale epochs, unknown peers, bad sizes,
+round-robin order, T-row jobs) and the watchdog's timing, without a GPU."""
+
+import pytest
+
+from oracle import transport as OT
+from sgl_asap_amd.transport import layout as L
+from sgl_asap_amd.transport.server import FfnServer
+
+
+# ---- doorbell (known answers computed from python/sgl_asap_plugin/transport/layout.py:50-53,92-102)
+@pytest.mark.parametrize(
+    "fields,word",
+    [
+        ((1, 16384, 0, 1), 0x0800400000000001),
+        ((0xFFFFFFFF, 1, 60, 31), 0xF8780001FFFFFFFF),
+        ((2, 8192, 3, 2), 0x1006200000000002),
+        ((7, 131071, 1023, 31), 0xFFFFFFFF00000007),
+    ],
+)
+def test_doorbell_known_answers(fields, word):
+    assert L.pack_doorbell(*fields) == word
+    assert L.unpack_doorbell(word) == fields
+    assert OT.pack_doorbell(*fields) == word
+
+
+@pytest.mark.parametrize("bad", [(1, 0, 0, 1), (1, 131072, 0, 1), (1, 1, 1024, 1), (1, 1, 0, 0), (1, 1, 0, 32)])
+def test_doorbell_range_checks(bad):
+    with pytest.raises(ValueError):
+        L.pack_doorbell(*bad)
+
+
+def test_doorbell_seq_wraps_mod_2_32():
+    assert L.unpack_doorbell(L.pack_doorbell((1 << 32) + 5, 3, 0, 1))[0] == 5
+
+
+def test_doorbell_roundtrip_exhaustive_fields():
+    for n in (1, 2, 1000, L.MAX_TOKENS):
+        for layer in (0, 1, 511, L.MAX_LAYER):
+            for epoch in (1, 2, 30, L.MAX_EPOCH):
+                for seq in (0, 1, 0x7FFFFFFF, 0xFFFFFFFF):
+                    w = L.pack_doorbell(seq, n, layer, epoch)
+                    assert L.unpack_doorbell(w) == (seq, n, layer, epoch)
+                    assert w == OT.pack_doorbell(seq, n, layer, epoch)
+
+
+# ---- geometry (numbers computed from layout.py:116-198 for the DSV4 rank deployment)
+def test_geometry_dsv4_two_replicas_four_f():
+    g = L.Geometry(num_a=2, group=1, slots=2, n_max=16384, hidden=4096, topk=8, num_f=4)
+    assert g.ids_off == 134_217_728
+    assert g.w_off == 134_742_016
+    assert g.region_bytes == 135_266_304
+    assert g.recv_bytes == 541_065_216
+    assert g.flags_bytes == 2_097_152
+    assert g.seg_bytes == 134_217_728
+    assert g.result_bytes == 1_075_838_976
+    assert g.region_off(1, 1) == 3 * 135_266_304
+    assert g.bell_off(1, 0) == 128 and g.done_off(3, 1) == 7 * 64
+    assert g.seg_off(1, 0) == 2_097_152 + 2 * 134_217_728
+    assert g.host_bytes == 4096
+    assert L.Geometry.from_dict(g.as_dict()) == g
+
+
+def test_geometry_one_gpu_loop():
+    g = L.Geometry(num_a=1, group=1, slots=2, n_max=8192, hidden=4096, topk=8, num_f=1)
+    assert g.region_bytes == 67_633_152
+    assert g.recv_bytes == 135_266_304
+    assert g.result_bytes == 136_314_880
+
+
+@pytest.mark.parametrize(
+    "kw",
+    [
+        dict(num_a=0, group=1, slots=1, n_max=1, hidden=1, topk=1, num_f=1),
+        dict(num_a=3, group=2, slots=1, n_max=1, hidden=1, topk=1, num_f=1),
+        dict(num_a=1, group=1, slots=1, n_max=L.MAX_TOKENS + 1, hidden=1, topk=1, num_f=1),
+        dict(num_a=1, group=1, slots=1.0, n_max=1, hidden=1, topk=1, num_f=1),
+    ],
+)
+def test_geometry_rejects(kw):
+    with pytest.raises(ValueError):
+        L.Geometry(**kw)
+
+
+def test_geometry_matches_oracle_restatement():
+    for kw in (dict(num_a=3, group=3, slots=2, n_max=777, hidden=384, topk=6, num_f=2),
+               dict(num_a=1, group=1, slots=1, n_max=1, hidden=256, topk=1, num_f=1)):
+        g = L.Geometry(**kw)
+        o = OT.geometry(**kw)
+        for name in ("ids_off", "w_off", "region_bytes", "recv_bytes", "host_bytes", "flags_bytes", "seg_bytes", "result_bytes"):
+            assert getattr(g, name) == o[name], name
+
+
+def test_seq_ahead_cyclic():
+    assert L.seq_ahead(5, 0xFFFFFFFE) == 7
+    assert L.seq_ahead(0xFFFFFFFE, 5) == -7
+    assert L.seq_ahead(3, 3) == 0
+
+
+# ---- F poller (server.py:262-338)
+def server(num_a=2, group=1, slots=2, seq_base=0):
+    g = L.Geometry(num_a=num_a, group=group, slots=slots, n_max=64, hidden=256, topk=2, num_f=1)
+    s = FfnServer(0, g, memory="none", seq_base=seq_base).start()
+    return s, g
+
+
+def connect(s, g, a):
+    return s.hello(a, None, None, g)["epoch"]
+
+
+def test_poll_basic_and_empty():
+    s, g = server()
+    e = connect(s, g, 0)
+    assert s.poll() == []
+    s.announce(0, 1, L.pack_doorbell(1, 10, 3, e))
+    jobs = s.poll()
+    assert len(jobs) == 1 and jobs[0].layer_id == 3 and jobs[0].slot == 1
+    assert jobs[0].rows[0].n_tokens == 10 and jobs[0].rows[0].ids_ptr == g.region_off(0, 1) + g.ids_off
+    assert s.poll() == []  # already seen
+    assert s.stats["jobs"] == 1 and s.trace[-1] == (0, 1, 3)
+
+
+def test_poll_counts_lost_messages():
+    s, g = server()
+    e = connect(s, g, 0)
+    s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
+    s.announce(0, 0, L.pack_doorbell(3, 5, 0, e))  # 2 overwritten before the poll saw 1
+    jobs = s.poll()
+    assert len(jobs) == 1 and jobs[0].rows[0].seq == 3
+    assert s.stats["lost_messages"] == 2
+
+
+def test_poll_drops_stale_epoch_unknown_peer_bad_size():
+    s, g = server()
+    e = connect(s, g, 0)
+    s.announce(0, 0, L.pack_doorbell(1, 5, 0, (e % 31) + 1))
+    s.announce(1, 0, L.pack_doorbell(1, 5, 0, 1))  # rank 1 never connected
+    s.announce(0, 1, L.pack_doorbell(1, 64, 0, e))  # n == n_max is fine
+    assert len(s.poll()) == 1
+    assert s.stats["stale_epoch"] == 1 and s.stats["unknown_peer"] == 1
+    s2, g2 = server()
+    e2 = connect(s2, g2, 0)
+    s2.announce(0, 0, L.pack_doorbell(1, 65, 0, e2))  # n > n_max
+    assert s2.poll() == [] and s2.stats["bad_doorbell"] == 1
+
+
+def test_poll_round_robin_order():
+    s, g = server(num_a=2, slots=2)
+    e0, e1 = connect(s, g, 0), connect(s, g, 1)
+    for seq in (1, 2):
+        for a, e in ((0, e0), (1, e1)):
+            for slot in (0, 1):
+                s.announce(a, slot, L.pack_doorbell(seq, 4, seq, e))
+        jobs = s.poll()
+        order = [(j.replica, j.slot) for j in jobs]
+        if seq == 1:
+            assert order == [(0, 0), (0, 1), (1, 0), (1, 1)]
+        else:  # starts after the last served index, then wraps
+            assert order == [(0, 0), (0, 1), (1, 0), (1, 1)]
+    # one doorbell ahead of the round-robin pointer is served before the ones behind it
+    s.announce(0, 1, L.pack_doorbell(3, 4, 0, e0))
+    s.announce(1, 0, L.pack_doorbell(3, 4, 0, e1))
+    s._rr = 2
+    assert [(j.replica, j.slot) for j in s.poll()] == [(1, 0), (0, 1)]
+
+
+def test_poll_sequence_wrap():
+    s, g = server(seq_base=(1 << 32) - 2)
+    e = connect(s, g, 0)
+    for seq in ((1 << 32) - 1, 0, 1, 2):
+        s.announce(0, 0, L.pack_doorbell(seq, 4, 0, e))
+        jobs = s.poll()
+        assert len(jobs) == 1 and jobs[0].rows[0].seq == seq & L.SEQ_MASK
+    assert s.stats["lost_messages"] == 0
+
+
+def test_poll_groups_tp_rows_into_one_job():
+    s, g = server(num_a=4, group=2, slots=1)
+    eps = [connect(s, g, a) for a in range(4)]
+    s.announce(1, 0, L.pack_doorbell(1, 4, 7, eps[1]))
+    assert s.poll() == []  # half a job
+    s.announce(0, 0, L.pack_doorbell(1, 6, 7, eps[0]))
+    jobs = s.poll()
+    assert len(jobs) == 1 and [r.a for r in jobs[0].rows] == [0, 1] and jobs[0].replica == 0
+    s.announce(2, 0, L.pack_doorbell(1, 4, 7, eps[2]))
+    s.announce(3, 0, L.pack_doorbell(1, 4, 8, eps[3]))  # TP ranks disagree on the layer
+    assert s.poll() == [] and s.stats["group_mismatch"] == 1
+
+
+def test_hello_epochs_cycle_and_reconnect_resets():
+    s, g = server()
+    epochs = [connect(s, g, 0) for _ in range(33)]
+    assert epochs[:3] == [1, 2, 3] and epochs[30] == 31 and epochs[31] == 1
+    assert s.stats["reconnects"] == 32
+    e = epochs[-1]
+    s.announce(0, 0, L.pack_doorbell(9, 4, 0, e))
+    assert len(s.poll()) == 1
+    e2 = connect(s, g, 0)  # reconnect: last-seen back to seq_base
+    s.announce(0, 0, L.pack_doorbell(1, 4, 0, e2))
+    assert len(s.poll()) == 1
+
+
+def test_hello_rejects_geometry_mismatch():
+    s, g = server()
+    other = L.Geometry(num_a=2, group=1, slots=2, n_max=64, hidden=512, topk=2, num_f=1)
+    with pytest.raises(L.HandshakeError):
+        s.hello(0, None, None, other)
+    with pytest.raises(L.HandshakeError):
+        s.hello(5, None, None, g)
+
+
+def test_server_matches_oracle_poll_on_random_streams():
+    """The poller against the oracle's restatement on random doorbell streams."""
+    import random
+
+    rnd = random.Random(0)
+    for trial in range(20):
+        s, g = server(num_a=3, slots=2, seq_base=rnd.choice([0, (1 << 32) - 5]))
+        o = OT.Poller(num_a=3, group=1, slots=2, n_max=64, seq_base=s.seq_base)
+        eps = {}
+        for a in range(3):
+            if rnd.random() < 0.8:
+                eps[a] = connect(s, g, a)
+                o.hello(a)
+        seqs = {(a, sl): s.seq_base for a in range(3) for sl in range(2)}
+        for step in range(40):
+            a, sl = rnd.randrange(3), rnd.randrange(2)
+            seqs[(a, sl)] = (seqs[(a, sl)] + rnd.choice([1, 1, 1, 2])) & L.SEQ_MASK
+            epoch = eps.get(a, 1) if rnd.random() < 0.9 else 17
+            n = rnd.choice([1, 5, 64, 65])
+            word = L.pack_doorbell(seqs[(a, sl)], n, rnd.randrange(4), epoch)
+            s.announce(a, sl, word)
+            o.announce(a, sl, word)
+            if rnd.random() < 0.5:
+                got = [(j.replica, j.slot, j.layer_id, [r.seq for r in j.rows]) for j in s.poll()]
+                want = o.poll()
+                assert got == want
+        for k, v in o.stats.items():
+            assert s.stats[k] == v, (trial, k)
