@@ -11,11 +11,9 @@ Modules:
 * ``routing``   - the stable expert-contiguous permutation of local (token, k) pairs.
 * ``experts``   - fp32 expert FFN on dequantized operands (torch CPU), finalize
                   (top-k weighted sum) and the A-side combine.
-* ``transport`` - doorbell / geometry / poll rules.
-* ``c/``        - a C restatement of the quantizers and the routing, built by
-                  ``oracle/Makefile`` into ``oracle/_build/liboracle.so`` and checked
-                  against the numpy restatement.
+* ``transport`` - doorbell word, arena geometry and the F poller's rules, plain Python.
 
 Every function cites the reference file:line it restates. How each one is pinned (known
-answers, closed forms, library casts, brute force) is written in its docstring.
+answers, closed forms, library casts, brute force) is written in its docstring; the
+checks are tests/test_oracle_*.py, tests/test_transport.py and tests/test_golden.py.
 """

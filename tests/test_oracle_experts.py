@@ -1,0 +1,133 @@
+"""Pins the oracle's expert call, finalize and combine (CPU): a float64 per-token dense
+MLP written independently of the oracle's routed formulation, exact special cases (no
+local pair, zero weights, repeated tokens, power-of-two weight scaling), and the
+finalize / combine formulas against torch fp32 arithmetic, bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import experts as OX
+from oracle import formats as F
+
+H, I = 256, 128
+
+
+def bits(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def setup(n, k, num_experts, e_lo, num_local, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(num_experts, generator=g)[:k] for _ in range(n)]).to(torch.int32)
+    w = torch.rand(n, k, generator=g)
+    w13 = (torch.randn(num_local, 2 * I, H, generator=g) * 0.05).numpy()
+    w2 = (torch.randn(num_local, H, I, generator=g) * 0.05).numpy()
+    return x, ids.numpy(), w.numpy(), w13, w2
+
+
+def dense_reference(x, ids, w, w13, w2, e_lo):
+    """float64, token by token: sum over local picks of w * bf16(W2 . bf16(silu(Wg x) * (Wu x)))."""
+    xf = x.double().numpy()
+    n, k = ids.shape
+    out = np.zeros((n, H))
+    for t in range(n):
+        for kk in range(k):
+            e = int(ids[t, kk]) - e_lo
+            if not 0 <= e < w13.shape[0]:
+                continue
+            wg, wu = w13[e, :I].astype(np.float64), w13[e, I:].astype(np.float64)
+            g, u = wg @ xf[t], wu @ xf[t]
+            h = g / (1 + np.exp(-g)) * u
+            h = F.bf16_to_f32(F.f32_to_bf16(h.astype(np.float32))).astype(np.float64)
+            y = F.bf16_to_f32(F.f32_to_bf16((w2[e].astype(np.float64) @ h).astype(np.float32)))
+            out[t] += float(w[t, kk]) * y
+    return out
+
+
+def rel_l2(a, b):
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("n,k,ne,e_lo,nl", [(1, 1, 4, 0, 4), (5, 2, 12, 4, 4), (40, 3, 16, 8, 8)])
+def test_expert_call_matches_dense_float64(n, k, ne, e_lo, nl):
+    x, ids, w, w13, w2 = setup(n, k, ne, e_lo, nl, seed=n)
+    got = F.bf16_to_f32(OX.moe_ffn(x, ids, w, w13, w2, e_lo, act="bf16", block_m=4)).astype(np.float64)
+    want = dense_reference(x, ids, w, w13, w2, e_lo)
+    assert rel_l2(got, want) < 4e-3
+    # per element: within a few bf16 ulps plus the h rounding the two orders may take differently
+    assert np.all(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 1e-3 * np.abs(want).max())
+
+
+def test_gate_and_up_are_not_interchangeable():
+    """The check above is sensitive to the [gate; up] order: swapping them moves the result."""
+    x, ids, w, w13, w2 = setup(8, 2, 4, 0, 4, seed=3)
+    swapped = np.concatenate([w13[:, I:], w13[:, :I]], axis=1)
+    got = F.bf16_to_f32(OX.moe_ffn(x, ids, w, swapped, w2, 0, act="bf16")).astype(np.float64)
+    assert rel_l2(got, dense_reference(x, ids, w, w13, w2, 0)) > 0.3
+
+
+def test_no_local_pair_gives_exact_zeros():
+    x, ids, w, w13, w2 = setup(16, 2, 8, 0, 4, seed=4)
+    ids = ids % 4 + 4  # every pick on another rank
+    assert not OX.moe_ffn(x, ids, w, w13, w2, 0).any()
+
+
+def test_zero_weights_give_exact_zeros():
+    x, ids, w, w13, w2 = setup(16, 2, 4, 0, 4, seed=5)
+    out = OX.moe_ffn(x, ids, np.zeros_like(w), w13, w2, 0)
+    assert np.all((out & 0x7FFF) == 0)  # +0 or -0
+
+
+def test_repeated_tokens_give_identical_rows():
+    x, ids, w, w13, w2 = setup(12, 2, 4, 0, 4, seed=6)
+    x[5], ids[5], w[5] = x[2], ids[2], w[2]
+    out = OX.moe_ffn(x, ids, w, w13, w2, 0)
+    assert np.array_equal(out[5], out[2])
+
+
+def test_power_of_two_weight_scaling_is_exact():
+    x, ids, w, w13, w2 = setup(10, 1, 4, 0, 4, seed=7)
+    a = F.bf16_to_f32(OX.moe_ffn(x, ids, w, w13, w2, 0))
+    b = F.bf16_to_f32(OX.moe_ffn(x, ids, 4 * w, w13, w2, 0))
+    assert np.array_equal(4 * a, b)
+
+
+def test_mxfp8_activations_stay_close_to_bf16():
+    x, ids, w, w13, w2 = setup(32, 2, 4, 0, 4, seed=8)
+    a = F.bf16_to_f32(OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16"))
+    for act in ("mxfp8", "fp8_1x128"):
+        b = F.bf16_to_f32(OX.moe_ffn(x, ids, w, w13, w2, 0, act=act))
+        assert 1e-4 < rel_l2(b, a) < 0.08, act  # quantized (not a no-op) but close
+
+
+def test_finalize_matches_torch_fp32_ops():
+    g = torch.Generator().manual_seed(9)
+    n, k, rows = 24, 3, 80
+    y = torch.randn(rows, H, generator=g).to(torch.bfloat16)
+    w = torch.rand(n, k, generator=g)
+    pos = torch.randint(-1, rows, (n * k,), generator=g, dtype=torch.int32)
+    got = OX.finalize(bits(y), pos.numpy(), w.numpy(), n, k)
+    acc = torch.zeros(n, H)
+    for kk in range(k):
+        p = pos.view(n, k)[:, kk]
+        sel = p >= 0
+        term = torch.zeros(n, H)
+        term[sel] = w[sel, kk][:, None] * y[p[sel].long()].float()
+        acc = torch.where(sel[:, None], acc + term, acc)
+    assert np.array_equal(got, bits(acc.to(torch.bfloat16)))
+
+
+@pytest.mark.parametrize("num_parts", [1, 2, 4])
+def test_combine_matches_torch(num_parts):
+    g = torch.Generator().manual_seed(10 + num_parts)
+    parts = [torch.randn(7, H, generator=g).to(torch.bfloat16) for _ in range(num_parts)]
+    shared = torch.randn(7, H, generator=g).to(torch.bfloat16)
+    acc = parts[0].float()
+    for p in parts[1:]:
+        acc = acc + p.float()
+    routed = parts[0].clone() if num_parts == 1 else acc.to(torch.bfloat16)
+    assert np.array_equal(OX.combine([bits(p) for p in parts]), bits(routed))
+    want = (routed.float() + shared.float()).to(torch.bfloat16)
+    assert np.array_equal(OX.combine([bits(p) for p in parts], bits(shared)), bits(want))
