@@ -40,7 +40,90 @@ def parse():
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
     ap.add_argument("--cpu-sample-experts", type=int, default=16)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="after the timed steps, run a plain fp32 copy kernel (torch.neg) over MIB MiB "
+                    "three times: the known-size reference for rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no GPU: turn two rocprofv3 --pmc counter_collection.csv files (FETCH_SIZE, "
+                    "WRITE_SIZE) of a --copy-calibration run into per-launch HBM bytes; writes --traffic-out")
+    ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
+                    help="no GPU: print a rocprofv3 --stats kernel_stats.csv as a markdown table")
+    ap.add_argument("--traffic-out", default=None)
     return ap.parse_args()
+
+
+TRAFFIC_DIR = os.path.join(ROOT, "profiles")
+
+
+def _csv_rows(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _short(name: str) -> str:
+    n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    if n.endswith(")"):
+        n = n[: n.rfind("(")]
+    return n[:90]
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, copy_mib: int, out_path) -> dict:
+    """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled so that the
+    plain copy kernel of the same run reads and writes exactly ``copy_mib`` MiB."""
+    per = {}
+    for which, path in (("fetch", fetch_csv), ("write", write_csv)):
+        acc = {}
+        for r in _csv_rows(path):
+            acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        per[which] = {k: sum(v) / len(v) for k, v in acc.items()}
+    copy = [k for k in per["fetch"] if "neg_kernel" in k]
+    if len(copy) != 1:
+        raise SystemExit(f"expected exactly one copy kernel (torch neg) in {fetch_csv}, found {copy}")
+    known_kib = copy_mib * 1024.0
+    f_fetch = known_kib / per["fetch"][copy[0]]
+    f_write = known_kib / per["write"][copy[0]]
+    kernels = {}
+    for k in per["fetch"]:
+        if "afd::" not in k and k != copy[0]:
+            continue
+        fb = per["fetch"][k] * f_fetch * 1024
+        wb = per["write"].get(k, 0.0) * f_write * 1024
+        kernels[_short(k)] = {"fetch_bytes": round(fb), "write_bytes": round(wb), "bytes": round(fb + wb)}
+    out = {
+        "copy_kernel_mib": copy_mib,
+        "scale_fetch": round(f_fetch, 4),
+        "scale_write": round(f_write, 4),
+        "kernels": kernels,
+    }
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump(out, f, indent=1)
+    return out
+
+
+def stats_summary(path: str) -> str:
+    rows = _csv_rows(path)
+    lines = ["| kernel | calls | avg us | min us | max us | % |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        lines.append(
+            f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+            f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.2f} |"
+        )
+    return "\n".join(lines)
+
+
+def load_traffic(workload: str, kernel_key: str):
+    """Per-launch HBM bytes of the dominant kernel from the committed PMC summary of this
+    workload (profiles/traffic_<workload>.json), or None."""
+    path = os.path.join(TRAFFIC_DIR, f"traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        data = json.load(f)
+    hits = [v for k, v in data["kernels"].items() if kernel_key in k]
+    return hits[0]["bytes"] if len(hits) == 1 else None
 
 
 def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
@@ -95,6 +178,12 @@ def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
 
 def main():
     args = parse()
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary))
+        return
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(*args.pmc_summary, args.copy_calibration or 1024, args.traffic_out), indent=1))
+        return
     if args.gpus != 1:
         print(
             f"bench.py measures one F rank's share of the experts on one GPU; --gpus {args.gpus} "
@@ -173,6 +262,14 @@ def main():
             stage_ms[s].append(evs[i].elapsed_time(evs[i + 1]))
     stage_avg = {s: round(sum(v) / len(v), 5) for s, v in stage_ms.items()}
 
+    if args.copy_calibration:  # known-size reference kernel for the PMC byte counters
+        src = torch.ones(args.copy_calibration << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
+
     tflops = flops / (ms * 1e-3) / 1e12
     gu_ms = stage_avg["gate_up"]
     gu_tflops = gate_up_flops / (gu_ms * 1e-3) / 1e12
@@ -212,7 +309,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / (PEAK_TFLOPS["fp4"] if shape.fmt == "mxfp4" else PEAK_TFLOPS["fp8"]), 4),
             "frac_vs_issued_format_peak": round(gu_tflops / PEAK_TFLOPS[issued], 4),
-            "traffic": None,
+            "traffic": load_traffic(shape.name, "mx_gemm_kernel<0" if shape.fmt == "mxfp4" else "fp8_gemm_kernel<0"),
         },
     }
     if args.cpu_baseline:
