@@ -110,8 +110,10 @@ __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d)
 // those rows (4 bytes = 4 blocks of 32 per row).
 //   A image (activations, 128 rows of e4m3): 128 x 128 B data, then 128 x 4 B scales.
 //   B image (weights, 256 rows of e2m1):     256 x  64 B data, then 256 x 4 B scales.
-// Rows are XOR-swizzled by 16-byte chunk so the MFMA operand reads (ds_read_b128 of 8
-// consecutive rows) hit 8 distinct bank groups.
+// Rows are XOR-swizzled by 16-byte chunk. An MFMA operand read (ds_read_b128, one chunk of
+// 32 consecutive rows per half wavefront) is served 16 lanes = 256 bytes at a time by the
+// 64 banks of gfx950's LDS; the swizzle puts those 16 lanes on 16 distinct 16-byte bank
+// groups (and any 8 consecutive lanes on 8 distinct groups of a 128-byte line).
 constexpr int kImgData = 16384;
 constexpr int kImgARows = 128, kImgBRows = 256;
 constexpr int kImgA = kImgData + kImgARows * 4;  // 16896
@@ -120,11 +122,11 @@ constexpr int kImgK = 128;                        // K values per image
 
 // byte offset of logical 16-byte chunk c (0..7) of row r in an A image
 __host__ __device__ __forceinline__ int img_a_off(int r, int c) {
-  return r * 128 + ((c ^ (r & 7)) << 4);
+  return r * 128 + ((c ^ ((r ^ (r >> 3)) & 7)) << 4);
 }
 // byte offset of logical 16-byte chunk c (0..3) of row n in a B image
 __host__ __device__ __forceinline__ int img_b_off(int n, int c) {
-  return n * 64 + ((c ^ ((n >> 1) & 3)) << 4);
+  return n * 64 + ((c ^ (((n >> 1) ^ (n >> 2)) & 3)) << 4);
 }
 
 // ---------------------------------------------------------------- direct global -> LDS copies
@@ -163,6 +165,13 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// wait_vmcnt<N> plus every LDS read of this wavefront complete (lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lds() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
 }
 
 }  // namespace afd

@@ -15,17 +15,24 @@
 // 17 KiB that move HBM -> LDS with gfx950's direct global_load_lds in 1 KiB pieces, without
 // register staging, into a ring of 3 (WN = 4) or 4 (WN = 2) stages; one barrier per stage.
 //
-// The workgroups are persistent: grid = resident workgroups, tile index strides by the grid,
-// and the number of row tiles is read from device memory (the router wrote it), so no host
-// round trip is needed. Tile index order is (row tile, column tile) with column tiles fastest,
-// so consecutive workgroups (which the dispatcher spreads over the 8 XCDs) split a weight
-// tile's columns across XCDs and each expert's weights are fetched from HBM once.
+// The workgroups are persistent: grid = resident workgroups, and the number of row tiles is
+// read from device memory (the router wrote it), so no host round trip is needed. The
+// dispatcher deals workgroups to the 8 XCDs round robin (workgroup b runs on XCD b % 8), and
+// each XCD has its own L2. With enough row tiles, XCD x takes the contiguous row tiles
+// [R x / 8, R (x + 1) / 8) and its workgroups walk them row tile by row tile, column tiles
+// fastest: the 32 workgroups of an XCD then share each A image (the column tiles of a row
+// tile) and each weight slice (the ~4 row tiles of an expert) in their L2, so HBM sees every
+// A image and, but for the experts cut by an XCD boundary, every expert's weights once. Small
+// jobs use the same walk over all row tiles and the whole grid.
 #include "afd_common.h"
 #include "afd_internal.h"
 
 namespace afd {
 
 enum { kGateUp = 0, kDown = 1 };
+
+// Row tiles from which the grid is split by XCD (4 row tiles = one round of an XCD's 32 CUs).
+constexpr int kXcdSplitRows = 32;
 
 struct MxGemmArgs {
   const uint8_t* a_img;         // A images [row tiles][K/128]
@@ -82,7 +89,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int wm = wave / WN, wn = wave % WN, lr = lane & 31, lk = lane >> 5;
   const int ntn = p.N / kBN, nt256 = p.N / kImgBRows;
-  const int tiles = p.num_tiles[0] * ntn;
+  const int rows = p.num_tiles[0];
+  const int tiles = rows * ntn;
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   const int w_u = __builtin_amdgcn_readfirstlane(wave);
@@ -90,8 +98,17 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   // this wavefront's B operand: image wn/2 of the stage, rows (wn%2)*128 + j*32 + lr
   const int bimg = wn / 2, brow = (wn % 2) * 128;
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const int mt = tile / ntn, nt = tile % ntn;
+  // this workgroup's walk: tiles i = first, first + stride, ... < count of row tiles from mt0
+  int mt0 = 0, count = tiles, first = blockIdx.x, stride = gridDim.x;
+  if ((gridDim.x & 7) == 0 && rows >= kXcdSplitRows) {
+    const int xcd = blockIdx.x & 7;
+    mt0 = (rows * xcd) >> 3;
+    count = (((rows * (xcd + 1)) >> 3) - mt0) * ntn;
+    first = blockIdx.x >> 3;
+    stride = gridDim.x >> 3;
+  }
+  for (int i = first; i < count; i += stride) {
+    const int mt = mt0 + i / ntn, nt = i % ntn;
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = p.tile_expert[mt];
     const uint8_t* a_tile = p.a_img + int64_t(mt) * KT * kImgA;
@@ -199,17 +216,20 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
             int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
             int col = wn * 64 + jj * 32 + lr;
             float g = acc[i][2 * jj][q], u = acc[i][2 * jj + 1][q];
-            hl[row * T::kHStride + col] = __fdividef(g, 1.0f + __expf(-g)) * u;
+            hl[row * T::kHStride + col] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
           }
       __syncthreads();
       // the 128 x (kBN/2) h tile is WN/2 K stages of the down GEMM's A operand, starting at
       // stage n0/256 of row tile mt
       constexpr int kBlocksPerRow = kBN / 64;  // MX blocks of 32 h columns
       const int kt_down = p.N / kImgBRows;     // K stages of the down GEMM (I / 128)
+      // consecutive lanes take consecutive rows of one block column: a row is 4 * kHStride
+      // bytes = 16 (mod 256) apart, so 16 lanes read 16 distinct bank groups
+      static_assert(kBlocksPerRow * kBM == 2 * T::kThreads, "two h blocks per thread");
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         int b = t + half * T::kThreads;
-        int row = b / kBlocksPerRow, cb = b % kBlocksPerRow;
+        int row = b % kBM, cb = b / kBM;
         const float* src = hl + row * T::kHStride + cb * 32;
         float v[32];
 #pragma unroll

@@ -19,7 +19,7 @@ def b_images(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     body = np.zeros((e, nt, kt, 256, 4, 16), dtype=np.uint8)
     rows = np.arange(256)
     for c in range(4):
-        phys = c ^ ((rows >> 1) & 3)
+        phys = c ^ (((rows >> 1) ^ (rows >> 2)) & 3)
         body[:, :, :, rows, phys, :] = data[:, :, :, rows, c, :]
     img[..., :IMG_DATA] = body.reshape(e, nt, kt, IMG_DATA)
     img[..., IMG_DATA:] = sc.reshape(e, nt, kt, 256 * 4)
@@ -35,7 +35,7 @@ def a_rows(images: np.ndarray, k: int):
     rows = np.arange(128)
     data = np.zeros((tiles, kt, 128, 8, 16), dtype=np.uint8)
     for c in range(8):
-        phys = c ^ (rows & 7)
+        phys = c ^ ((rows ^ (rows >> 3)) & 7)
         data[:, :, rows, c, :] = body[:, :, rows, phys, :]
     codes = data.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, k)
     sc = img[..., IMG_DATA:].reshape(tiles, kt, 128, 4).transpose(0, 2, 1, 3).reshape(tiles * 128, k // 32)
