@@ -35,7 +35,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="layer", choices=["layer", "stream", "loop"],
+                    help="layer: one expert call per step (default); stream: the skewed job stream "
+                    "from 2 replicas x 2 micro-batches through the F scheduler; loop: the one-GPU "
+                    "A<->F loop with a shared expert, 2 micro-batches per layer")
     ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
+    ap.add_argument("--jobs", type=int, default=32, help="stream: jobs in the stream")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
@@ -176,6 +181,189 @@ def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
     }
 
 
+def _mxfp4_layer(W, shape, dev, n_max, seed=1):
+    """One layer of packed MXFP4 local experts of ``shape`` (weights ~ N(0, 0.02))."""
+    import torch
+
+    from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts
+
+    w13, w2 = W.expert_weights(shape.num_local, shape.hidden, shape.inter, W.generator(dev, seed), dev)
+    weights = pack_mxfp4_experts(w13, w2, device=dev)
+    del w13, w2
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n_max)
+
+
+def bench_stream(args) -> dict:
+    """The skewed job stream: Zipf(1.2) routing, job sizes log-uniform in [256, 16384], jobs
+    arriving from 2 A replicas x 2 micro-batches (round robin) through the one-GPU transport
+    into the F scheduler, with HIP graphs for every power-of-two bucket up to 16384 tokens and,
+    for comparison, eagerly. Timed: first send to the last reply landing, after one untimed
+    pass of the same stream."""
+    import torch
+
+    from sgl_asap_amd import workloads as W
+    from sgl_asap_amd.loop import OneGpuAfd
+
+    shape = W.SHAPES["dsv4_zipf"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n_max = 16384
+    sizes = W.job_sizes(args.jobs, 256, n_max, seed=0)
+    jobs = []
+    for j, n in enumerate(sizes):
+        x, ids, w = W.job(shape, n=n, seed=100 + j, device=dev)
+        jobs.append((x, ids.to(torch.int32).contiguous(), w.to(torch.float32).contiguous()))
+    pairs = sum(W.pair_count(ids, shape.local) for _, ids, _ in jobs)
+    flops = W.flops(shape.hidden, shape.inter, pairs)
+    tokens = sum(sizes)
+    order = [(r, mb) for r in range(2) for mb in range(2)]
+    out = {
+        "metric": "MoE-layer TFLOPS + tokens/s, skewed job stream (2 replicas x 2 micro-batches), 1 MI355X",
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "mxfp4xmxfp8",
+        "data": "synthetic (seeded N(0,1) tokens, Zipf(1.2) routing, N(0,0.02) expert weights, random-init)",
+        "config": {
+            "workload": f"dsv4_zipf job stream: one F rank, H={shape.hidden} I={shape.inter}, "
+            f"{shape.num_local} local of {shape.num_experts} experts, top-{shape.top_k}, {len(sizes)} jobs "
+            f"of logU[256,16384] tokens ({tokens} tokens, {pairs} local pairs)",
+            "job_tokens": sizes,
+        },
+    }
+    for mode, graph_max in (("graphs", n_max), ("eager", 0)):
+        experts = {0: _mxfp4_layer(W, shape, dev, n_max)}
+        t0 = time.perf_counter()
+        afd = OneGpuAfd(experts, n_max=n_max, slots=2, replicas=2, graph_max_tokens=graph_max, timing=True)
+        setup_s = time.perf_counter() - t0
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        main = torch.cuda.current_stream()
+
+        def run():
+            for s in sends:
+                s.wait_stream(main)
+            for base in range(0, len(jobs), len(order)):
+                tickets = []
+                for k, (r, mb) in enumerate(order):
+                    if base + k < len(jobs):
+                        x, ids, w = jobs[base + k]
+                        tickets.append((r, afd.channels[r].send(0, mb, x.data_ptr(), ids.data_ptr(),
+                                                                  w.data_ptr(), x.shape[0], sends[r])))
+                afd.scheduler.serve_pending()
+                for r, t in tickets:
+                    afd.channels[r].wait(t, main)
+
+        run()
+        torch.cuda.synchronize()
+        afd.scheduler.job_timer = type(afd.scheduler.job_timer)()  # time the measured pass only
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        h0 = time.perf_counter()
+        e0.record(main)
+        run()
+        e1.record(main)
+        host_ms = (time.perf_counter() - h0) * 1e3
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        out[mode] = {
+            "ms": round(ms, 3),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "host_enqueue_ms": round(host_ms, 3),
+            "setup_s": round(setup_s, 2),
+            "jobs_per_bucket": {str(b): v["jobs"] for b, v in afd.scheduler.job_timer.summary().items()},
+            "job_timer": afd.scheduler.job_timer.summary(),
+        }
+        afd.close()
+        del experts, afd
+        torch.cuda.empty_cache()
+    out["value"] = out["graphs"]["tflops"]
+    out["ms_per_step"] = out["graphs"]["ms"]
+    out["tokens_per_s"] = out["graphs"]["tokens_per_s"]
+    return out
+
+
+def bench_loop(args) -> dict:
+    """The one-GPU A<->F loop at W4A8 with a bf16 shared expert (intermediate 1536): per layer
+    two micro-batches of 8192 tokens (Zipf(1.2) routing) are dispatched on slots 0/1 (arena
+    copies + doorbells on the A send stream), the F scheduler parks its stream on the
+    doorbells and runs the experts (HIP graphs), the shared expert runs on the A compute
+    stream meanwhile, and the combine adds the routed partial sums and the shared output.
+    Per-layer latency: from before the first copy to the last combine's output."""
+    import torch
+
+    from sgl_asap_amd import workloads as W
+    from sgl_asap_amd.loop import OneGpuAfd
+    from sgl_asap_amd.moe.layer import AsapMoE
+    from sgl_asap_amd.moe.topk import StandardTopKOutput
+
+    shape = W.SHAPES["dsv4_zipf"]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n, shared_i = 8192, 1536
+    experts = {0: _mxfp4_layer(W, shape, dev, n)}
+    g = W.generator(dev, 2)
+    w_gu = (torch.randn(2 * shared_i, shape.hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    w_d = (torch.randn(shape.hidden, shared_i, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    def shared(x):
+        gate, up = (x @ w_gu.T).split(shared_i, dim=1)
+        return (torch.nn.functional.silu(gate) * up) @ w_d.T
+
+    mbs = []
+    for m in range(2):
+        x, ids, w = W.job(shape, n=n, seed=200 + m, device=dev)
+        mbs.append((x, StandardTopKOutput(w.to(torch.float32), ids.to(torch.int32))))
+    pairs = sum(W.pair_count(t.topk_ids, shape.local) for _, t in mbs)
+    routed_flops = W.flops(shape.hidden, shape.inter, pairs)
+    shared_flops = 2 * 6 * shape.hidden * shared_i * n
+    afd = OneGpuAfd(experts, n_max=n, slots=2, graph_max_tokens=n)
+    layer = AsapMoE(shape.num_experts, shape.hidden, shape.inter, 0, top_k=shape.top_k)
+    main = torch.cuda.current_stream()
+
+    def step():
+        d = [layer.dispatcher.dispatch(x, t, micro_batch=m) for m, (x, t) in enumerate(mbs)]
+        afd.scheduler.serve_pending()
+        s = [shared(x) for x, _ in mbs]
+        return [layer.dispatcher.combine(d[m], s[m]) for m in range(2)]
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    lat = []
+    for _ in range(args.steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(main)
+        step()
+        e1.record(main)
+        torch.cuda.synchronize()
+        lat.append(e0.elapsed_time(e1))
+    afd.close()
+    ms = statistics.median(lat)
+    return {
+        "metric": "per-layer latency of the one-GPU AFD loop (W4A8 + bf16 shared expert), 1 MI355X",
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "dtype": "mxfp4xmxfp8 routed, bf16 shared",
+        "data": "synthetic (seeded N(0,1) tokens, Zipf(1.2) routing, N(0,0.02) weights, random-init)",
+        "config": {
+            "workload": f"dsv4_zipf loop: 2 micro-batches x {n} tokens, H={shape.hidden} I={shape.inter}, "
+            f"{shape.num_local} local of {shape.num_experts} experts, top-{shape.top_k}, shared expert I={shared_i} bf16",
+            "local_pairs": pairs,
+        },
+        "layer_latency_ms": round(ms, 4),
+        "layer_latency_ms_min": round(min(lat), 4),
+        "tokens_per_s": round(2 * n / (ms * 1e-3), 1),
+        "tflops_routed_plus_shared": round((routed_flops + shared_flops) / (ms * 1e-3) / 1e12, 2),
+    }
+
+
 def main():
     args = parse()
     if args.stats_summary:
@@ -194,6 +382,13 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.workload == "stream":
+        print(json.dumps(bench_stream(args)), flush=True)
+        return
+    if args.workload == "loop":
+        print(json.dumps(bench_loop(args)), flush=True)
+        return
 
     from sgl_asap_amd import _lib
     from sgl_asap_amd import workloads as W

@@ -30,28 +30,38 @@ from .transport.server import FfnServer
 
 
 class OneGpuAfd:
+    """``replicas`` A ranks (one replica each, group 1) and one F rank on one GPU. A rank 0's
+    channel is installed as this process's ``AsapBuffer``; the others are driven through
+    ``channels[a]`` directly (``AttnChannel.send`` / ``wait``, pump with ``serve_pending``)."""
+
     def __init__(self, experts: Dict[int, torch.nn.Module], *, n_max: int, slots: int = 2,
-                 seq_base: int = 0, graph_max_tokens: int = 0, timeout_s: float = 60.0,
-                 device: int = 0, reply_stream: bool = True, timing: bool = False,
-                 _backpressure: bool = True, _epoch_override: Optional[int] = None):
+                 replicas: int = 1, seq_base: int = 0, graph_max_tokens: int = 0,
+                 timeout_s: float = 60.0, device: int = 0, reply_stream: bool = True,
+                 timing: bool = False, _backpressure: bool = True,
+                 _epoch_override: Optional[int] = None):
         first = next(iter(experts.values()))
         if first.n_max < n_max:
             raise ValueError(f"experts hold workspaces for {first.n_max} tokens, the loop carries up to {n_max}")
-        self.geometry = Geometry(num_a=1, group=1, slots=slots, n_max=n_max, hidden=first.hidden_size,
-                                 topk=first.top_k, num_f=1)
+        self.geometry = Geometry(num_a=replicas, group=1, slots=slots, n_max=n_max,
+                                 hidden=first.hidden_size, topk=first.top_k, num_f=1)
         self.server = FfnServer(0, self.geometry, device=device, seq_base=seq_base).start()
         self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens,
                                       reply_stream=reply_stream, timing=timing)
-        self.channel = AttnChannel(0, self.geometry, [self.server], device=device, seq_base=seq_base,
-                                   timeout_s=timeout_s, _backpressure=_backpressure,
-                                   _epoch_override=_epoch_override).connect()
+        self.channels = [
+            AttnChannel(a, self.geometry, [self.server], device=device, seq_base=seq_base,
+                        timeout_s=timeout_s, _backpressure=_backpressure,
+                        _epoch_override=_epoch_override).connect()
+            for a in range(replicas)
+        ]
+        self.channel = self.channels[0]
         self.buffer = AsapBuffer.install(self.channel, device, pump=self.scheduler.serve_pending)
 
     def close(self) -> None:
         torch.cuda.synchronize()
         if AsapBuffer._buffer is self.buffer:
             AsapBuffer.uninstall()
-        self.channel.close()
+        for channel in self.channels:
+            channel.close()
         self.server.close()
 
     def __enter__(self) -> "OneGpuAfd":

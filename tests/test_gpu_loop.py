@@ -135,3 +135,36 @@ def test_empty_batch():
         x, topk = job(0, 1)
         out = layer(x, topk)
         assert out.shape == (0, H) and afd.server.stats["jobs"] == 0
+
+
+def test_two_replicas_two_slots():
+    say("loop: 2 A replicas x 2 slots into one F server, 3 rounds")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, slots=2, replicas=2) as afd:
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        main = torch.cuda.current_stream()
+        for rnd in range(3):
+            jobs, tickets = [], []
+            for r in range(2):
+                for mb in range(2):
+                    x, topk = job(10 + 7 * r + 3 * mb + rnd, 300 + 10 * rnd + 2 * r + mb)
+                    ids = topk.topk_ids.to(torch.int32).contiguous()
+                    w = topk.topk_weights.to(torch.float32).contiguous()
+                    sends[r].wait_stream(main)
+                    t = afd.channels[r].send(0, mb, x.data_ptr(), ids.data_ptr(), w.data_ptr(), x.shape[0], sends[r])
+                    jobs.append((r, x, topk, ids, w))
+                    tickets.append((r, t))
+            assert afd.scheduler.serve_pending() == 4
+            for (r, t), (_, x, topk, _, _) in zip(tickets, jobs):
+                ptr = afd.channels[r].wait(t, main)[0]
+                got = torch.empty(x.shape[0], H, dtype=torch.bfloat16, device=dev())
+                _lib_copy(got, ptr)
+                torch.cuda.synchronize()
+                assert np.array_equal(bits16(got), direct(experts, 0, x, topk)), (rnd, r)
+        assert afd.server.stats["jobs"] == 12 and afd.server.stats["lost_messages"] == 0
+
+
+def _lib_copy(dst, src_ptr):
+    from sgl_asap_amd.transport import hip
+
+    hip.copy_async(dst.data_ptr(), src_ptr, dst.numel() * 2, torch.cuda.current_stream().cuda_stream)
