@@ -119,6 +119,9 @@ constexpr int kImgARows = 128, kImgBRows = 256;
 constexpr int kImgA = kImgData + kImgARows * 4;  // 16896
 constexpr int kImgB = kImgData + kImgBRows * 4;  // 17408
 constexpr int kImgK = 128;                        // K values per image
+// The MX GEMM copies an A image's 512 B of scales as a 1 KiB piece, reading the 512 B that
+// follow; buffers of A images keep that much readable memory after their last image.
+constexpr int kImgReadSlack = 512;
 
 // byte offset of logical 16-byte chunk c (0..7) of row r in an A image
 __host__ __device__ __forceinline__ int img_a_off(int r, int c) {

@@ -45,7 +45,8 @@ struct MxGemmArgs {
   uint16_t* y;     // down out: bf16 [np][N]
 };
 
-// Shape of the workgroup tile for WN wavefronts along N.
+// Shape of the workgroup tile: 2 x WN wavefronts in two groups of WN (group g = rows
+// [64 g, 64 g + 64)), BN = 128 WN columns.
 template <int WN>
 struct MxTile {
   static_assert(WN == 2 || WN == 4, "tiles are 256 or 512 columns wide");
@@ -54,46 +55,43 @@ struct MxTile {
   static constexpr int kBM = kBlockM;  // 128 rows = one A image
   static constexpr int kBN = 128 * WN;
   static constexpr int kBImgs = WN / 2;  // 256-row B images per tile
-  static constexpr int kStage = kImgA + kBImgs * kImgB;
-  static constexpr int kStages = WN == 2 ? 4 : 3;
+  // LDS stage: the A image (its 512 B of scales padded to a 1 KiB piece), then the B images
+  static constexpr int kLdsA = kImgData + 1024;
+  static constexpr int kStage = kLdsA + kBImgs * kImgB;
+  static constexpr int kStages = 3;
   static constexpr int kLds = kStages * kStage;
-  static constexpr int kAChunks = 16 / kWaves;           // 1 KiB A pieces per wavefront
-  static constexpr int kBChunks = 16 * kBImgs / kWaves;  // 1 KiB B pieces per wavefront
-  // wavefronts [0, kBImgs) also copy one B image's scales, wavefront kBImgs the A scales
-  static constexpr int kCopiesLead = kAChunks + kBChunks + 1;
-  static constexpr int kCopiesRest = kAChunks + kBChunks;
+  // a stage is 17 pieces of 1 KiB per image; every wavefront copies kPieces of them (pieces
+  // past the last repeat earlier ones: the same bytes to the same place)
+  static constexpr int kStagePieces = 17 * (1 + kBImgs);
+  static constexpr int kPieces = (kStagePieces + kWaves - 1) / kWaves;
   static constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
   static constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
+  static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
   static_assert(kBM * kHStride * 4 <= kLds, "gate_up epilogue tile must fit the stages");
   static_assert(kBM * kYStride * 2 <= kLds, "down epilogue tile must fit the stages");
   static_assert(kLds <= 160 * 1024, "LDS of one CU");
+  static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
 };
 
-// Wait until stage kt's copies (N per stage for this wavefront) have landed; up to S later
-// stages may still be in flight.
-template <int N, int S>
-__device__ __forceinline__ void wait_stage(int kt, int KT) {
-  if (S >= 2 && kt + 2 < KT)
-    wait_vmcnt<2 * N>();
-  else if (kt + 1 < KT)
-    wait_vmcnt<N>();
-  else
-    wait_vmcnt<0>();
-}
+// The scaled MFMA with a 4-dword (e2m1) B operand. The clang builtin takes 8 dwords for every
+// operand format; the intrinsic's B operand type follows the format, and e2m1 needs only 4.
+extern "C" __device__ v16f mfma_scale_f8_f4(v8i a, v4i b, v16f c, int cbsz, int blgp,
+                                            int opsel_a, int scale_a, int opsel_b, int scale_b)
+    __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v8i32.v4i32");
 
 template <int MODE, int WN>
 __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArgs p) {
   using T = MxTile<WN>;
   constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t lds[T::kLds];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave / WN, wn = wave % WN, lr = lane & 31, lk = lane >> 5;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
+  const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
   const int ntn = p.N / kBN, nt256 = p.N / kImgBRows;
   const int rows = p.num_tiles[0];
   const int tiles = rows * ntn;
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-  const int w_u = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t voff = static_cast<uint32_t>(lane) * 16;
   // this wavefront's B operand: image wn/2 of the stage, rows (wn%2)*128 + j*32 + lr
   const int bimg = wn / 2, brow = (wn % 2) * 128;
@@ -114,93 +112,130 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     const uint8_t* a_tile = p.a_img + int64_t(mt) * KT * kImgA;
     const uint8_t* b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
 
+    // this wavefront's copies of stage kt into ring slot kt % 3: piece c of image c / 17 (0 = A,
+    // its 17th piece being the scales plus the 512 B that follow them in memory). Scalar
+    // address arithmetic only, so the issuing code has no branches.
     auto issue = [&](int kt) {
       const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
       const uint8_t* a = a_tile + int64_t(kt) * kImgA;
 #pragma unroll
-      for (int q = 0; q < T::kAChunks; ++q) {
-        const int c = w_u * T::kAChunks + q;
-        lds_dma16(st + c * 1024, a + c * 1024, voff);
+      for (int q = 0; q < T::kPieces; ++q) {
+        int c = w_u * T::kPieces + q;
+        c = c < T::kStagePieces ? c : c - T::kStagePieces;
+        const int img = c / 17, off = (c % 17) * 1024;
+        const uint8_t* b = b_tile + (int64_t(img - 1) * KT + kt) * kImgB;
+        const uint8_t* src = img == 0 ? a : b;
+        const uint32_t dst = img == 0 ? st + off : st + T::kLdsA + (img - 1) * kImgB + off;
+        lds_dma16(dst, src + off, voff);
       }
-#pragma unroll
-      for (int q = 0; q < T::kBChunks; ++q) {
-        const int c = w_u * T::kBChunks + q, bi = c / 16, cc = c % 16;
-        const uint8_t* b = b_tile + (int64_t(bi) * KT + kt) * kImgB;
-        lds_dma16(st + kImgA + bi * kImgB + cc * 1024, b + cc * 1024, voff);
-      }
-      if (w_u < T::kBImgs) {
-        const uint8_t* b = b_tile + (int64_t(w_u) * KT + kt) * kImgB;
-        lds_dma16(st + kImgA + w_u * kImgB + kImgData, b + kImgData, voff);
-      }
-      if (w_u == T::kBImgs && lane < 32) lds_dma16(st + kImgData, a + kImgData, voff);
     };
 
     v16f acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+        for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
 
-    auto compute = [&](int s) {
+    // Operand fragments of both k-steps of one stage, with the stage's scale words.
+    // 8-bit operand of the f8f6f4 MFMA: lane half h holds K [16h, 16h+16) in bytes 0-15 and
+    // K [32+16h, 32+16h+16) in bytes 16-31 of the k-step; the e2m1 operand holds K [32h, 32h+32);
+    // the scale of lane x+32b covers K block b.
+    struct Frag {
+      v8i a[2][2];  // [ks][i]
+      v4i b[2][4];  // [ks][j]
+      uint32_t sa[2], sb[4];
+    };
+    Frag f;
+    auto read_stage = [&](int s) {
       const uint8_t* abase = lds + s * kStage;
-      const uint8_t* bbase = abase + kImgA + bimg * kImgB;
+      const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
       const uint32_t* sa = reinterpret_cast<const uint32_t*>(abase + kImgData);
       const uint32_t* sb = reinterpret_cast<const uint32_t*>(bbase + kImgData);
-      uint32_t sav[2], sbv[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) sav[i] = sa[wm * 64 + i * 32 + lr];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sbv[j] = sb[brow + j * 32 + lr];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        v8i af[2], bf[4];
-        // 8-bit operand of the f8f6f4 MFMA: lane half h holds K [16h, 16h+16) in bytes 0-15
-        // and K [32+16h, 32+16h+16) in bytes 16-31 of the 64-wide k-step; the fp4 operand
-        // holds K [32h, 32h+32) contiguously, and the scale of lane x+32b covers K block b.
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          int r = wm * 64 + i * 32 + lr;
-          v4i lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + lk));
-          v4i hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + 2 + lk));
-          af[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        for (int i2 = 0; i2 < 2; ++i2) {
+          int r = wm * 64 + i2 * 32 + lr;
+          f.a[ks][i2].lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + lk));
+          f.a[ks][i2].hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + 2 + lk));
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          int n = brow + j * 32 + lr;
-          v4i v = *reinterpret_cast<const v4i*>(bbase + img_b_off(n, ks * 2 + lk));
-          bf[j] = v8i{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-        }
+        for (int j = 0; j < 4; ++j)
+          f.b[ks][j] = *reinterpret_cast<const v4i*>(bbase + img_b_off(brow + j * 32 + lr, ks * 2 + lk));
+      }
+#pragma unroll
+      for (int i2 = 0; i2 < 2; ++i2) f.sa[i2] = sa[wm * 64 + i2 * 32 + lr];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) f.sb[j] = sb[brow + j * 32 + lr];
+    };
+    auto mma_stage = [&]() {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
         const int sh = 8 * (ks * 2 + lk);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          int sca = static_cast<int>((sav[i] >> sh) & 0xffu);
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int sca = static_cast<int>((f.sa[i2] >> sh) & 0xffu);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            int scb = static_cast<int>((sbv[j] >> sh) & 0xffu);
-            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                af[i], bf[j], acc[i][j], 0 /*A e4m3*/, 4 /*B e2m1*/, 0, sca, 0, scb);
+            const int scb = static_cast<int>((f.sb[j] >> sh) & 0xffu);
+            acc[i2][j] = mfma_scale_f8_f4(f.a[ks][i2], f.b[ks][j], acc[i2][j], 0 /*A e4m3*/,
+                                          4 /*B e2m1*/, 0, sca, 0, scb);
           }
         }
       }
     };
 
+    // Ping-pong: the two wavefronts of a SIMD (one per group) alternate between reading a
+    // stage's operands from LDS and running its 16 MFMAs, half a stage apart, so one of them
+    // always feeds the MFMA pipe while the other's reads proceed. All wavefronts meet at a
+    // barrier every half stage; group 1 starts one barrier late and group 0 ends one
+    // barrier later, so both execute 2 KT + 1 barriers per tile. Each wavefront copies its
+    // pieces of stage kt+2 (clamped to the last stage: a clamped copy rewrites a slot with
+    // its own bytes) when it starts reading stage kt; that slot's previous stage was read by
+    // both groups before the barrier that started the phase. The CU's vector-memory path
+    // takes ~64 B/clk, so splitting the copies between the groups keeps each read phase
+    // shorter than the other group's MFMA phase. Both groups wait for their own pieces of
+    // stage kt+1 in the phase before the barrier after which group 0 reads stage kt+1: group 0
+    // after its MFMAs of stage kt, group 1 after its reads of stage kt.
+    const int last = KT - 1;
     wait_vmcnt<0>();  // the previous tile's epilogue stores
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s)
-      if (s < KT) issue(s);
-    for (int kt = 0; kt < KT; ++kt) {
-      if (w_u <= T::kBImgs)
-        wait_stage<T::kCopiesLead, kStages - 2>(kt, KT);
-      else
-        wait_stage<T::kCopiesRest, kStages - 2>(kt, KT);
-      // every wavefront's copies of stage kt have landed, and every wavefront is done with
-      // stage kt-1, whose buffer the next copy overwrites
+    issue(0);
+    issue(min(1, last));
+    wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
+    __syncthreads();
+    if (wm == 0) {
+      for (int kt = 0; kt < KT; ++kt) {
+        issue(min(kt + 2, last));
+        read_stage(kt % kStages);
+        wait_vmcnt_lds<2 * T::kPieces>();  // own reads done (copies may be in flight)
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_stage();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<T::kPieces>();  // own pieces of stage kt+1 landed
+        __syncthreads();
+      }
       __syncthreads();
-      if (kt + kStages - 1 < KT) issue(kt + kStages - 1);
-      compute(kt % kStages);
+    } else {
+      __syncthreads();
+      for (int kt = 0; kt < KT; ++kt) {
+        issue(min(kt + 2, last));
+        read_stage(kt % kStages);
+        wait_vmcnt_lds<T::kPieces>();  // own reads done, own pieces of stage kt+1 landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_stage();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+      }
     }
+    wait_vmcnt<0>();  // no copy may land in the stage buffers the epilogue reuses
     __syncthreads();  // the epilogue reuses the stage buffers
 
     if (MODE == kGateUp) {

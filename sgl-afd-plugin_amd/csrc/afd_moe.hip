@@ -192,7 +192,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   // the down A images; their scales live inside the images (xs, hs empty).
   // FP8 block: xq / xs are the per-token e4m3 rows and fp32 1x128 scales, hq / hs the
   // padded-row intermediate and its scales.
-  L.xq = take(mx ? max_tiles * (H / kImgK) * kImgA : uint64_t(n) * H);
+  L.xq = take(mx ? max_tiles * (H / kImgK) * kImgA + kImgReadSlack : uint64_t(n) * H);
   L.xs = take(mx ? 0 : uint64_t(n) * (H / 128) * 4);
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
@@ -202,7 +202,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.tile_expert = take(uint64_t(np_max / kBlockM) * 4);
   L.num_tiles = take(4);
   L.hist = take(uint64_t(128) * E * 4);
-  L.hq = take(mx ? max_tiles * (I / kImgK) * kImgA : uint64_t(np_max) * I);
+  L.hq = take(mx ? max_tiles * (I / kImgK) * kImgA + kImgReadSlack : uint64_t(np_max) * I);
   L.hs = take(mx ? 0 : uint64_t(np_max) * (I / 128) * 4);
   L.y = take(uint64_t(np_max) * H * 2);
   L.total = o;

@@ -47,8 +47,9 @@ def test_workspace_layout_dsv4_rank():
     tiles = L["np_max"] // 128
     assert L["max_tiles"] == tiles
     # MXFP4: xq holds one A tile image (16896 B) per row tile and 128-wide K stage
-    assert L["xq"] == 0 and L["xs"] == tiles * (4096 // 128) * 16896
-    assert L["hs"] - L["hq"] == tiles * (2048 // 128) * 16896
+    # (+ 512 B of readable slack after the last image, rounded to 256 B)
+    assert L["xq"] == 0 and L["xs"] == -(-(tiles * (4096 // 128) * 16896 + 512) // 256) * 256
+    assert L["hs"] - L["hq"] == -(-(tiles * (2048 // 128) * 16896 + 512) // 256) * 256
     offs = [L[k] for k in ("xq", "xs", "counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos",
                            "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
