@@ -25,11 +25,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
 }
 
 // Round to nearest even; NaN stays a quiet NaN (the rounding of torch's .to(bfloat16)).
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even and quiets NaNs: bit for bit the
+// rounding of torch's .to(bfloat16) (checked on 2^28 fp32 patterns incl. ties and denormals).
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f_t __attribute__((ext_vector_type(2)));
+// (bf16(lo) | bf16(hi) << 16) with one conversion instruction
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  v2bf b = __builtin_convertvector((v2f_t{lo, hi}), v2bf);
+  return __builtin_bit_cast(uint32_t, b);
+}
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>(pk_bf16(f, 0.0f));
 }
 
 // ---------------------------------------------------------------- e4m3fn (OCP FP8)

@@ -40,6 +40,8 @@ struct MxGemmArgs {
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
   const int32_t* num_tiles;     // [1]
+  const int32_t* padded_offsets;  // [E + 1] first padded row of each expert
+  const int32_t* counts;          // [E] pairs of each expert (its first rows)
   int K, N;
   uint8_t* h_img;  // gate_up out: the down GEMM's A images [row tiles][N/256]
   uint16_t* y;     // down out: bf16 [np][N]
@@ -293,16 +295,21 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       }
       __syncthreads();
     } else {
+      // the expert's pairs fill its first rows, padding the rest: rows [0, nvalid) of this
+      // tile are real
+      const int nvalid = min(kBM, p.padded_offsets[e] + p.counts[e] - m0);
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
-            int col = wn * 128 + j * 32 + lr;
-            yl[row * T::kYStride + col] = f32_to_bf16(acc[i][j][q]);
+          for (int q = 0; q < 16; q += 2) {
+            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);  // q and q + 1: rows
+            int col = wn * 128 + j * 32 + lr;                               // row and row + 1
+            uint32_t two = pk_bf16(acc[i][j][q], acc[i][j][q + 1]);
+            yl[row * T::kYStride + col] = static_cast<uint16_t>(two);
+            yl[(row + 1) * T::kYStride + col] = static_cast<uint16_t>(two >> 16);
           }
       __syncthreads();
       constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
@@ -310,9 +317,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       for (int q = 0; q < 16; ++q) {
         int idx = q * T::kThreads + t;
         int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
-        int grow = m0 + row;
-        if (p.sorted_pairs[grow] >= 0)
-          *reinterpret_cast<v4i*>(p.y + int64_t(grow) * p.N + n0 + c * 8) =
+        if (row < nvalid)
+          *reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8) =
               *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8);
       }
       __syncthreads();
@@ -355,6 +361,8 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
+  p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
+  p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
   p.K = cfg.hidden;
   p.N = 2 * cfg.inter;
   p.h_img = ws + L.hq;
@@ -371,6 +379,8 @@ int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
+  p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
+  p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
   p.K = cfg.inter;
   p.N = cfg.hidden;
   p.h_img = nullptr;

@@ -71,8 +71,7 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   v4i o;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    o[i] = static_cast<int>(uint32_t(f32_to_bf16(acc[2 * i])) |
-                            (uint32_t(f32_to_bf16(acc[2 * i + 1])) << 16));
+    o[i] = static_cast<int>(pk_bf16(acc[2 * i], acc[2 * i + 1]));
   *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
 }
 
