@@ -83,7 +83,7 @@ typedef struct afd_moe_cfg {
  *    tile followed by that tile's UE8M0 scales: [E][N/256][K/128][256 x 64 B | 256 x 4 B]
  *    (17408 bytes each; N = 2I, K = H for w13; N = H, K = I for w2). In a tile, 16-byte
  *    chunk c (32 e2m1 values, element 2i in the low nibble) of row n sits at byte
- *    n*64 + 16*(c ^ (((n >> 1) ^ (n >> 2)) & 3)); scale j of row n at 16384 + 4n + j. w13 rows
+ *    n*64 + 16*(c ^ (((n >> 1) ^ (n >> 2)) & 3)); scale j of row n at 16384 + 4n + (2(j & 1) | (j >> 1)). w13 rows
  *    interleave gate and up in groups of 32 (physical row 64j+q is gate row 32j+q for
  *    q < 32, else up row 32j+q-32). s13 and s2 are not used (NULL).
  *  FP8_BLOCK: w13 u8 [E][2I][H], s13 f32 [E][2I/128][H/128], w2 u8 [E][H][I],

@@ -3,6 +3,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 #include "../../include/afd.h"
@@ -110,6 +112,16 @@ __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d)
       __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(c), clamp_e4m3(d), lo, true));
 }
 
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}): an
+// unrolled loop whose index is a constant expression in the body
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // ---------------------------------------------------------------- MX GEMM operand tile images
 // The MX grouped GEMMs copy their operands HBM -> LDS as contiguous "tile images": the exact
 // LDS bytes of one K stage (128 K values) of one row tile, followed by the UE8M0 scales of
@@ -128,6 +140,11 @@ constexpr int kImgK = 128;                        // K values per image
 // The MX GEMM copies an A image's 512 B of scales as a 1 KiB piece, reading the 512 B that
 // follow; buffers of A images keep that much readable memory after their last image.
 constexpr int kImgReadSlack = 512;
+
+// The 4 UE8M0 scale bytes of a row (K blocks 0..3 of the stage) are stored in the order
+// block 0, 2, 1, 3: lane half h of an MFMA operand reads the 16-bit half at byte 2h and finds
+// its k-step-ks block (2 ks + h) in byte ks, which the MFMA's op_sel picks directly.
+__host__ __device__ __forceinline__ int scale_byte(int j) { return ((j & 1) << 1) | (j >> 1); }
 
 // byte offset of logical 16-byte chunk c (0..7) of row r in an A image
 __host__ __device__ __forceinline__ int img_a_off(int r, int c) {

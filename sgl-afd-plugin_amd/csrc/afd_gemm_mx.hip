@@ -24,6 +24,8 @@
 // tile) and each weight slice (the ~4 row tiles of an expert) in their L2, so HBM sees every
 // A image and, but for the experts cut by an XCD boundary, every expert's weights once. Small
 // jobs use the same walk over all row tiles and the whole grid.
+#include <type_traits>
+
 #include "afd_common.h"
 #include "afd_internal.h"
 
@@ -62,10 +64,13 @@ struct MxTile {
   static constexpr int kStage = kLdsA + kBImgs * kImgB;
   static constexpr int kStages = 3;
   static constexpr int kLds = kStages * kStage;
-  // a stage is 17 pieces of 1 KiB per image; every wavefront copies kPieces of them (pieces
-  // past the last repeat earlier ones: the same bytes to the same place)
-  static constexpr int kStagePieces = 17 * (1 + kBImgs);
-  static constexpr int kPieces = (kStagePieces + kWaves - 1) / kWaves;
+  // a stage is kImgs images of 17 pieces of 1 KiB: every wavefront copies kQP of the 16 data
+  // pieces of each image plus one scale piece (scale pieces past the kImgs real ones repeat
+  // one: the same bytes to the same place)
+  static constexpr int kImgs = 1 + kBImgs;
+  static constexpr int kQP = 16 / kWaves;
+  static constexpr int kPieces = kImgs * kQP + 1;
+  static_assert(kWaves >= kImgs, "one scale piece per image");
   static constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
   static constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
   static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
@@ -117,19 +122,31 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     // this wavefront's copies of stage kt into ring slot kt % 3: piece c of image c / 17 (0 = A,
     // its 17th piece being the scales plus the 512 B that follow them in memory). Scalar
     // address arithmetic only, so the issuing code has no branches.
-    auto issue = [&](int kt) {
+    // Piece q of this wavefront: for q < kImgs * kQP, piece w * kQP + q % kQP of image
+    // q / kQP (0 = A, then the B images); for q = kImgs * kQP, piece 16 (the scales) of image
+    // w % kImgs (wavefronts past kImgs repeat one). Only the last depends on the wavefront
+    // beyond an offset, so it is resolved once per tile; the others are address arithmetic.
+    const int img16 = w_u % T::kImgs;
+    const uint8_t* src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
+    const int step16 = img16 == 0 ? kImgA : kImgB;
+    const uint32_t dst16 = img16 == 0 ? kImgData : T::kLdsA + (img16 - 1) * kImgB + kImgData;
+    auto issue_piece = [&](int kt, auto qc) {
+      constexpr int q = decltype(qc)::value;
       const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
-      const uint8_t* a = a_tile + int64_t(kt) * kImgA;
-#pragma unroll
-      for (int q = 0; q < T::kPieces; ++q) {
-        int c = w_u * T::kPieces + q;
-        c = c < T::kStagePieces ? c : c - T::kStagePieces;
-        const int img = c / 17, off = (c % 17) * 1024;
-        const uint8_t* b = b_tile + (int64_t(img - 1) * KT + kt) * kImgB;
-        const uint8_t* src = img == 0 ? a : b;
-        const uint32_t dst = img == 0 ? st + off : st + T::kLdsA + (img - 1) * kImgB + off;
-        lds_dma16(dst, src + off, voff);
+      if constexpr (q == T::kImgs * T::kQP) {
+        lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
+      } else {
+        constexpr int img = q / T::kQP;
+        const int off = (w_u * T::kQP + q % T::kQP) * 1024;
+        if constexpr (img == 0)
+          lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
+        else
+          lds_dma16(st + T::kLdsA + (img - 1) * kImgB + off,
+                    b_tile + (int64_t(img - 1) * KT + kt) * kImgB + off, voff);
       }
+    };
+    auto issue = [&](int kt) {
+      static_for<T::kPieces>([&](auto q) { issue_piece(kt, q); });
     };
 
     v16f acc[2][4];
@@ -147,14 +164,14 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     struct Frag {
       v8i a[2][2];  // [ks][i]
       v4i b[2][4];  // [ks][j]
-      uint32_t sa[2], sb[4];
+      uint32_t sa[2], sb[4];  // bytes 0, 1: the scales of k-steps 0, 1 for this lane half
     };
     Frag f;
     auto read_stage = [&](int s) {
       const uint8_t* abase = lds + s * kStage;
       const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
-      const uint32_t* sa = reinterpret_cast<const uint32_t*>(abase + kImgData);
-      const uint32_t* sb = reinterpret_cast<const uint32_t*>(bbase + kImgData);
+      const uint16_t* sa = reinterpret_cast<const uint16_t*>(abase + kImgData) + lk;
+      const uint16_t* sb = reinterpret_cast<const uint16_t*>(bbase + kImgData) + lk;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
@@ -168,39 +185,48 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
           f.b[ks][j] = *reinterpret_cast<const v4i*>(bbase + img_b_off(brow + j * 32 + lr, ks * 2 + lk));
       }
 #pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2) f.sa[i2] = sa[wm * 64 + i2 * 32 + lr];
+      for (int i2 = 0; i2 < 2; ++i2) f.sa[i2] = sa[2 * (wm * 64 + i2 * 32 + lr)];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) f.sb[j] = sb[brow + j * 32 + lr];
+      for (int j = 0; j < 4; ++j) f.sb[j] = sb[2 * (brow + j * 32 + lr)];
     };
-    auto mma_stage = [&]() {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int sh = 8 * (ks * 2 + lk);
-#pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2) {
-          const int sca = static_cast<int>((f.sa[i2] >> sh) & 0xffu);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int scb = static_cast<int>((f.sb[j] >> sh) & 0xffu);
+    // the 16 MFMAs of a stage; with Copy, this wavefront's pieces of stage copy_kt are issued
+    // one after every second MFMA (copy instructions are ordering points for the compiler,
+    // so the interleave holds)
+    auto mma_stage = [&](auto copy, int copy_kt) {
+      constexpr bool Copy = decltype(copy)::value;
+      static_for<2>([&](auto ksc) {
+        constexpr int ks = decltype(ksc)::value;
+        static_for<2>([&](auto i2c) {
+          constexpr int i2 = decltype(i2c)::value;
+          static_for<4>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            // op_sel ks: byte ks of the lane's scale half-word
             acc[i2][j] = mfma_scale_f8_f4(f.a[ks][i2], f.b[ks][j], acc[i2][j], 0 /*A e4m3*/,
-                                          4 /*B e2m1*/, 0, sca, 0, scb);
-          }
-        }
-      }
+                                          4 /*B e2m1*/, ks, static_cast<int>(f.sa[i2]), ks,
+                                          static_cast<int>(f.sb[j]));
+            if constexpr (Copy) {
+              constexpr int m = ks * 8 + i2 * 4 + j;
+              if constexpr ((m & 1) && m / 2 < T::kPieces)
+                issue_piece(copy_kt, std::integral_constant<int, m / 2>{});
+            }
+          });
+        });
+      });
     };
 
     // Ping-pong: the two wavefronts of a SIMD (one per group) alternate between reading a
     // stage's operands from LDS and running its 16 MFMAs, half a stage apart, so one of them
     // always feeds the MFMA pipe while the other's reads proceed. All wavefronts meet at a
     // barrier every half stage; group 1 starts one barrier late and group 0 ends one
-    // barrier later, so both execute 2 KT + 1 barriers per tile. Each wavefront copies its
-    // pieces of stage kt+2 (clamped to the last stage: a clamped copy rewrites a slot with
-    // its own bytes) when it starts reading stage kt; that slot's previous stage was read by
-    // both groups before the barrier that started the phase. The CU's vector-memory path
-    // takes ~64 B/clk, so splitting the copies between the groups keeps each read phase
-    // shorter than the other group's MFMA phase. Both groups wait for their own pieces of
-    // stage kt+1 in the phase before the barrier after which group 0 reads stage kt+1: group 0
-    // after its MFMAs of stage kt, group 1 after its reads of stage kt.
+    // barrier later, so both execute 2 KT + 1 barriers per tile. The CU's vector-memory path
+    // takes ~64 B/clk, so the copies are split between the groups, which keeps each read
+    // phase shorter than the other group's MFMA phase. Each group copies its pieces of stage
+    // kt+2 when it starts reading stage kt (copies issued between MFMAs delay them); the target
+    // slot's previous stage was read by both groups before the barrier that started the phase.
+    // Copies are clamped to the last stage (a clamped copy rewrites a slot with its own
+    // bytes). Both groups wait for their own pieces of stage kt+1 in the phase before the
+    // barrier after which group 0 reads stage kt+1: group 0 after its MFMAs of stage kt,
+    // group 1 after its reads of stage kt.
     const int last = KT - 1;
     wait_vmcnt<0>();  // the previous tile's epilogue stores
     issue(0);
@@ -215,7 +241,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage();
+        mma_stage(std::false_type{}, 0);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<T::kPieces>();  // own pieces of stage kt+1 landed
@@ -231,7 +257,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage();
+        mma_stage(std::false_type{}, 0);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
@@ -291,7 +317,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         uint8_t* img = p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + cb / 4) * kImgA;
         *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j)) = out[0];
         *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j + 1)) = out[1];
-        img[kImgData + row * 4 + j] = static_cast<uint8_t>(code);
+        img[kImgData + row * 4 + scale_byte(j)] = static_cast<uint8_t>(code);
       }
       __syncthreads();
     } else {

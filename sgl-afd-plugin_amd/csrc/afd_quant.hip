@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kQuantThreads) void pack_mxfp4_kernel(
     const int ks = cb / 4, j = cb % 4;
     uint8_t* img = out + ((mat * ntiles + nt) * kstages + ks) * int64_t(kImgB);
     *reinterpret_cast<v4i*>(img + img_b_off(n, j)) = packed;
-    img[kImgData + n * 4 + j] = static_cast<uint8_t>(code);
+    img[kImgData + n * 4 + scale_byte(j)] = static_cast<uint8_t>(code);
   }
 }
 
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kQuantThreads) void gather_quant_mxfp8_kernel(
     uint8_t* img = out + (mt * kstages + ks) * int64_t(kImgA);
     *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j)) = out0;
     *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j + 1)) = out1;
-    img[kImgData + r * 4 + j] = static_cast<uint8_t>(code);
+    img[kImgData + r * 4 + scale_byte(j)] = static_cast<uint8_t>(code);
   }
 }
 

@@ -6,6 +6,7 @@ import numpy as np
 IMG_DATA = 16384
 IMG_A = IMG_DATA + 128 * 4
 IMG_B = IMG_DATA + 256 * 4
+SCALE_ORDER = [0, 2, 1, 3]  # physical byte p of a row's scale word holds block SCALE_ORDER[p]
 
 
 def b_images(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
@@ -14,7 +15,8 @@ def b_images(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     k = kb * 2
     nt, kt = n // 256, k // 128
     data = packed.reshape(e, nt, 256, kt, 4, 16).transpose(0, 1, 3, 2, 4, 5)  # e nt kt row chunk byte
-    sc = scales.reshape(e, nt, 256, kt, 4).transpose(0, 1, 3, 2, 4)  # e nt kt row j
+    # scale bytes of a row in the order of blocks 0, 2, 1, 3 (a self-inverse permutation)
+    sc = scales.reshape(e, nt, 256, kt, 4).transpose(0, 1, 3, 2, 4)[..., SCALE_ORDER]  # e nt kt row
     img = np.zeros((e, nt, kt, IMG_B), dtype=np.uint8)
     body = np.zeros((e, nt, kt, 256, 4, 16), dtype=np.uint8)
     rows = np.arange(256)
@@ -38,5 +40,6 @@ def a_rows(images: np.ndarray, k: int):
         phys = c ^ ((rows ^ (rows >> 3)) & 7)
         data[:, :, rows, c, :] = body[:, :, rows, phys, :]
     codes = data.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, k)
-    sc = img[..., IMG_DATA:].reshape(tiles, kt, 128, 4).transpose(0, 2, 1, 3).reshape(tiles * 128, k // 32)
+    sc = img[..., IMG_DATA:].reshape(tiles, kt, 128, 4)[..., SCALE_ORDER]
+    sc = sc.transpose(0, 2, 1, 3).reshape(tiles * 128, k // 32)
     return codes, sc
