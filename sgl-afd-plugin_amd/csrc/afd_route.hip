@@ -47,41 +47,83 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ poff,
     int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ num_tiles) {
+  __shared__ int part[kScanThreads];
   __shared__ int tot[kMaxLocalExperts];
   __shared__ int pof[kMaxLocalExperts + 1];
   const int t = threadIdx.x;
-  // per expert: running exclusive prefix over chunks, in place
-  for (int e = t; e < num_local; e += kScanThreads) {
+  // Expert e's chunks are split over G = kScanThreads / num_local threads (e, g); each sums
+  // its contiguous run of chunks with independent loads, the runs' bases come from the
+  // partial sums in LDS, then each thread rewrites its chunks as exclusive bases.
+  const int G = kScanThreads / num_local;
+  const int per = (chunks + G - 1) / G;
+  const int e = t % num_local, g = t / num_local;
+  const bool active = g < G;
+  const int c0 = active ? g * per : 0, c1 = active ? min(c0 + per, chunks) : 0;
+  int sum = 0;
+  for (int c = c0; c < c1; ++c) sum += hist[int64_t(c) * num_local + e];
+  part[t] = sum;
+  __syncthreads();
+  if (active) {
     int run = 0;
-    for (int c = 0; c < chunks; ++c) {
-      int h = hist[int64_t(c) * num_local + e];
-      hist[int64_t(c) * num_local + e] = run;
+    for (int h = 0; h < g; ++h) run += part[h * num_local + e];
+    if (g == 0) {
+      int all = 0;
+      for (int h = 0; h < G; ++h) all += part[h * num_local + e];
+      tot[e] = all;
+      counts[e] = all;
+    }
+    for (int c = c0; c < c1; ++c) {
+      const int64_t at = int64_t(c) * num_local + e;
+      const int h = hist[at];
+      hist[at] = run;
       run += h;
     }
-    tot[e] = run;
-    counts[e] = run;
   }
   __syncthreads();
-  if (t == 0) {
-    int o = 0, p = 0;
-    for (int e = 0; e < num_local; ++e) {
-      offsets[e] = o;
-      pof[e] = p;
-      poff[e] = p;
-      o += tot[e];
-      p += (tot[e] + block_m - 1) / block_m * block_m;
+  // expert offsets and block_m-padded offsets: one wavefront, 4 experts per lane
+  if (t < 64) {
+    int o[4], q[4], so = 0, sp = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ex = t * 4 + i;
+      const int c = ex < num_local ? tot[ex] : 0;
+      o[i] = so;
+      q[i] = sp;
+      so += c;
+      sp += (c + block_m - 1) / block_m * block_m;
     }
-    offsets[num_local] = o;
-    pof[num_local] = p;
-    poff[num_local] = p;
-    num_tiles[0] = p / block_m;
+    int io = so, ip = sp;  // inclusive scans of the lane totals
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int vo = __shfl_up(io, d), vp = __shfl_up(ip, d);
+      if (t >= d) {
+        io += vo;
+        ip += vp;
+      }
+    }
+    const int bo = io - so, bp = ip - sp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ex = t * 4 + i;
+      if (ex < num_local) {
+        offsets[ex] = bo + o[i];
+        poff[ex] = bp + q[i];
+        pof[ex] = bp + q[i];
+      }
+    }
+    if (t == 63) {
+      offsets[num_local] = io;
+      poff[num_local] = ip;
+      pof[num_local] = ip;
+      num_tiles[0] = ip / block_m;
+    }
   }
   __syncthreads();
   // row-tile table and -1 on the padding rows of every segment
-  for (int e = 0; e < num_local; ++e) {
-    int t0 = pof[e] / block_m, t1 = pof[e + 1] / block_m;
-    for (int i = t0 + t; i < t1; i += kScanThreads) tile_expert[i] = e;
-    for (int r = pof[e] + tot[e] + t; r < pof[e + 1]; r += kScanThreads) sorted_pairs[r] = -1;
+  for (int ex = 0; ex < num_local; ++ex) {
+    const int t0 = pof[ex] / block_m, t1 = pof[ex + 1] / block_m;
+    for (int i = t0 + t; i < t1; i += kScanThreads) tile_expert[i] = ex;
+    for (int r = pof[ex] + tot[ex] + t; r < pof[ex + 1]; r += kScanThreads) sorted_pairs[r] = -1;
   }
 }
 
