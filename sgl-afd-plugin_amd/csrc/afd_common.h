@@ -122,6 +122,17 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Division by a launch constant d >= 1 without the division sequence:
+// n / d == __umulhi(n, ceil(2^32 / d)) for every n with n * d < 2^32 (the product overshoots
+// n / d by n * (ceil(2^32/d) * d - 2^32) / 2^32 / d < n / 2^32 < 1/d, which never reaches
+// the next integer). 2^32 itself does not fit 32 bits, so d == 1 is encoded as 0.
+inline uint32_t div_magic(uint32_t d) {
+  return d <= 1 ? 0u : static_cast<uint32_t>((0x100000000ull + d - 1) / d);
+}
+__device__ __forceinline__ uint32_t div_by_magic(uint32_t n, uint32_t magic) {
+  return magic ? __umulhi(n, magic) : n;
+}
+
 // ---------------------------------------------------------------- MX GEMM operand tile images
 // The MX grouped GEMMs copy their operands HBM -> LDS as contiguous "tile images": the exact
 // LDS bytes of one K stage (128 K values) of one row tile, followed by the UE8M0 scales of

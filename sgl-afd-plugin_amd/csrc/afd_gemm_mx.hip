@@ -37,7 +37,12 @@ enum { kGateUp = 0, kDown = 1 };
 constexpr int kXcdSplitRows = 32;
 
 struct MxGemmArgs {
-  const uint8_t* a_img;         // A images [row tiles][K/128]
+  const uint8_t* a_img;         // down: A images [row tiles][K/128]
+  const uint8_t* a_rows;        // gate_up: e4m3 token rows [n][K], gathered by sorted_pairs
+  const uint8_t* a_scales;      // gate_up: their UE8M0 scales [n][K/32] in stage order
+  int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
+  uint32_t topk_magic;          // div_magic(topk)
+  uint32_t ntn_magic;           // div_magic(N / BN), for the tile walk
   const uint8_t* b_img;         // B images [E][N/256][K/128]
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
@@ -65,12 +70,12 @@ struct MxTile {
   static constexpr int kStages = 3;
   static constexpr int kLds = kStages * kStage;
   // a stage is kImgs images of 17 pieces of 1 KiB: every wavefront copies kQP of the 16 data
-  // pieces of each image plus one scale piece (scale pieces past the kImgs real ones repeat
-  // one: the same bytes to the same place)
+  // pieces of each image plus one scale piece (scale pieces past the real ones repeat one:
+  // the same bytes to the same place)
   static constexpr int kImgs = 1 + kBImgs;
   static constexpr int kQP = 16 / kWaves;
   static constexpr int kPieces = kImgs * kQP + 1;
-  static_assert(kWaves >= kImgs, "one scale piece per image");
+  static_assert(kWaves >= 2 * kImgs, "a scale piece per image, two for a gathered A");
   static constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
   static constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
   static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
@@ -112,21 +117,72 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     first = blockIdx.x >> 3;
     stride = gridDim.x >> 3;
   }
+  // A tile's metadata is loaded one tile ahead and decoded after the previous tile's K loop,
+  // whose last wait leaves no copy in flight, so no tile starts by waiting for a load.
+  // gate_up gathers its A operand from the token rows: a lane copies one 16-byte chunk of row
+  // 8 (w kQP + q) + lane / 8 of the tile for each of its A pieces q (physical chunk lane % 8,
+  // so logical chunk (lane % 8) ^ swizzle(row)) and the scale word of row 64 h + lane for
+  // scale half h, at offsets given by the pair indices of those rows. Padding rows (-1) read
+  // token 0; their results are never stored.
+  const int s_half = (w_u / T::kImgs) & 1;
+  int sp_next[T::kQP + 1], e_next = 0;
+  auto load_next = [&](int ii) {
+    const int m = mt0 + static_cast<int>(div_by_magic(static_cast<uint32_t>(ii), p.ntn_magic));
+    e_next = p.tile_expert[m];
+    if constexpr (MODE == kGateUp) {
+#pragma unroll
+      for (int q = 0; q < T::kQP; ++q)
+        sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * T::kQP + q) + (lane >> 3)];
+      sp_next[T::kQP] = p.sorted_pairs[m * kBM + 64 * s_half + lane];
+    }
+  };
+  int e_cur = 0;
+  uint32_t a_voff[T::kQP] = {}, s_voff = 0;
+  auto decode_next = [&]() {
+    e_cur = __builtin_amdgcn_readfirstlane(e_next);
+    if constexpr (MODE == kGateUp) {
+      auto token = [&](int sp) {
+        return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
+      };
+#pragma unroll
+      for (int q = 0; q < T::kQP; ++q) {
+        const int r = 8 * (w_u * T::kQP + q) + (lane >> 3);
+        const int c = (lane & 7) ^ ((r ^ (r >> 3)) & 7);
+        a_voff[q] = token(sp_next[q]) * p.K + c * 16;
+      }
+      s_voff = token(sp_next[T::kQP]) * (p.K / 32);
+    }
+  };
+  if (first < count) {
+    load_next(first);
+    decode_next();
+  }
   for (int i = first; i < count; i += stride) {
-    const int mt = mt0 + i / ntn, nt = i % ntn;
+    // i / ntn by multiply-high (exact: i * ntn < 2^32), keeping the walk in scalar registers
+    const int iq = static_cast<int>(div_by_magic(static_cast<uint32_t>(i), p.ntn_magic));
+    const int mt = mt0 + iq, nt = i - iq * ntn;
     const int m0 = mt * kBM, n0 = nt * kBN;
-    const int64_t e = p.tile_expert[mt];
-    const uint8_t* a_tile = p.a_img + int64_t(mt) * KT * kImgA;
+    const int64_t e = e_cur;
+    // down: the expert's pairs fill its first rows, padding the rest; rows below row_end are
+    // real (loaded now, used by the epilogue)
+    int row_end = 0;
+    if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
+    const bool has_next = i + stride < count;
+    if (has_next) load_next(i + stride);
+    const uint8_t* a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : p.a_rows;
     const uint8_t* b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
 
     // this wavefront's copies of stage kt into ring slot kt % 3: piece c of image c / 17 (0 = A,
     // its 17th piece being the scales plus the 512 B that follow them in memory). Scalar
     // address arithmetic only, so the issuing code has no branches.
     // Piece q of this wavefront: for q < kImgs * kQP, piece w * kQP + q % kQP of image
-    // q / kQP (0 = A, then the B images); for q = kImgs * kQP, piece 16 (the scales) of image
-    // w % kImgs (wavefronts past kImgs repeat one). Only the last depends on the wavefront
-    // beyond an offset, so it is resolved once per tile; the others are address arithmetic.
-    const int img16 = w_u % T::kImgs;
+    // q / kQP (0 = A, then the B images). The last, q = kImgs * kQP, is a scale piece:
+    // wavefront w < 2 kImgs copies that of image w % kImgs (of the gathered A of gate_up, half
+    // w / kImgs: 64 rows' words), later wavefronts repeat a B image's (the same bytes to the
+    // same place), so the costly gathered scale copy is issued once per half. Only the last
+    // piece depends on the wavefront beyond an offset, so it is resolved once per tile; the
+    // others are address arithmetic.
+    const int img16 = w_u < 2 * T::kImgs ? w_u % T::kImgs : 1 + (w_u - 2 * T::kImgs) % T::kBImgs;
     const uint8_t* src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
     const int step16 = img16 == 0 ? kImgA : kImgB;
     const uint32_t dst16 = img16 == 0 ? kImgData : T::kLdsA + (img16 - 1) * kImgB + kImgData;
@@ -134,11 +190,16 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       constexpr int q = decltype(qc)::value;
       const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
       if constexpr (q == T::kImgs * T::kQP) {
-        lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
+        if (MODE == kGateUp && img16 == 0)  // 64 rows' scale words, gathered
+          lds_dma4(st + kImgData + s_half * 256, p.a_scales + int64_t(kt) * 4, s_voff);
+        else
+          lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
       } else {
         constexpr int img = q / T::kQP;
         const int off = (w_u * T::kQP + q % T::kQP) * 1024;
-        if constexpr (img == 0)
+        if constexpr (img == 0 && MODE == kGateUp)
+          lds_dma16(st + off, p.a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
+        else if constexpr (img == 0)
           lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
         else
           lds_dma16(st + T::kLdsA + (img - 1) * kImgB + off,
@@ -172,13 +233,17 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
       const uint16_t* sa = reinterpret_cast<const uint16_t*>(abase + kImgData) + lk;
       const uint16_t* sb = reinterpret_cast<const uint16_t*>(bbase + kImgData) + lk;
+      // Row r + 32 has the swizzle of row r with chunk bit 2 flipped, so its chunk c sits 4096 B
+      // after row r's chunk c ^ 4: four lane addresses serve both row blocks, the second through
+      // the instruction's offset field.
+      const int r0 = wm * 64 + lr;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2) {
-          int r = wm * 64 + i2 * 32 + lr;
-          f.a[ks][i2].lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + lk));
-          f.a[ks][i2].hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r, ks * 4 + 2 + lk));
+          const int kc = (ks ^ i2) * 4 + lk;
+          f.a[ks][i2].lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc) + i2 * 4096);
+          f.a[ks][i2].hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc + 2) + i2 * 4096);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -228,7 +293,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     // barrier after which group 0 reads stage kt+1: group 0 after its MFMAs of stage kt,
     // group 1 after its reads of stage kt.
     const int last = KT - 1;
-    wait_vmcnt<0>();  // the previous tile's epilogue stores
+    // epilogue stores of the previous tile may still be in flight: they only delay the
+    // counted waits below (vmcnt counts stores too), never satisfy them early
     issue(0);
     issue(min(1, last));
     wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
@@ -265,6 +331,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     }
     wait_vmcnt<0>();  // no copy may land in the stage buffers the epilogue reuses
     __syncthreads();  // the epilogue reuses the stage buffers
+    if (has_next) decode_next();
 
     if (MODE == kGateUp) {
       // SwiGLU in registers: column subtiles (0,1) and (2,3) are the (gate, up) halves of
@@ -321,9 +388,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       }
       __syncthreads();
     } else {
-      // the expert's pairs fill its first rows, padding the rest: rows [0, nvalid) of this
-      // tile are real
-      const int nvalid = min(kBM, p.padded_offsets[e] + p.counts[e] - m0);
+      const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -365,9 +430,11 @@ static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream)
     per_cu = b;
   }
   const int max_tiles = max_row_tiles * (p.N / T::kBN);
+  MxGemmArgs a = p;
+  a.ntn_magic = div_magic(p.N / T::kBN);
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
-  hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, p);
+  hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }
@@ -382,7 +449,11 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
                       const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
   MxGemmArgs p;
-  p.a_img = ws + L.xq;
+  p.a_img = nullptr;
+  p.a_rows = ws + L.xq;
+  p.a_scales = ws + L.xs;
+  p.topk = cfg.topk;
+  p.topk_magic = div_magic(cfg.topk);
   p.b_img = static_cast<const uint8_t*>(wt.w13);
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
@@ -401,6 +472,10 @@ int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t
   (void)n;
   MxGemmArgs p;
   p.a_img = ws + L.hq;
+  p.a_rows = nullptr;
+  p.a_scales = nullptr;
+  p.topk = cfg.topk;
+  p.topk_magic = div_magic(cfg.topk);
   p.b_img = static_cast<const uint8_t*>(wt.w2);
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);

@@ -12,9 +12,8 @@ constexpr int kMaxLocalExperts = 256;
 constexpr int kMaxTopk = 32;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
 
-int launch_gather_quant_mxfp8(const uint16_t* x, const int32_t* sorted_pairs,
-                              const int32_t* num_tiles, int topk, int cols, int64_t max_rows,
-                              uint8_t* out, hipStream_t stream);
+int launch_quant_mxfp8_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* s,
+                            hipStream_t stream);
 
 int launch_route(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
                  const afd_ws_layout& L, hipStream_t stream);

@@ -187,12 +187,12 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   };
   afd_ws_layout L;
   const uint64_t max_tiles = uint64_t(np_max / kBlockM);
-  // MXFP4: xq holds the gate_up A images (every padded row, gathered and quantized) and hq
-  // the down A images; their scales live inside the images (xs, hs empty).
-  // FP8 block: xq / xs are the per-token e4m3 rows and fp32 1x128 scales, hq / hs the
-  // padded-row intermediate and its scales.
-  L.xq = take(mx ? max_tiles * (H / kImgK) * kImgA + kImgReadSlack : uint64_t(n) * H);
-  L.xs = take(mx ? 0 : uint64_t(n) * (H / 128) * 4);
+  // xq / xs: the per-token e4m3 rows and their scales (MXFP4: UE8M0 per 32, in stage order;
+  // FP8 block: fp32 per 1x128). MXFP4: hq holds the down GEMM's A images (the h rows in
+  // expert order, scales inside, hs empty); FP8 block: hq / hs the padded-row intermediate
+  // and its scales.
+  L.xq = take(uint64_t(n) * H);
+  L.xs = take(mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
   L.padded_offsets = take((E + 1) * 4);
@@ -224,6 +224,9 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   if (n > 0 && (!x || !ids || !w || !out)) return AFD_ERR_ARG;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
+  // the MX gate_up GEMM addresses token rows with 32-bit byte offsets
+  if (cfg->weight_fmt == AFD_W_MXFP4 && uint64_t(n) * cfg->hidden > 0xffffffffull)
+    return AFD_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto mark = [&](int i) -> int {
     if (ev && ev[i]) AFD_CHECK_HIP(hipEventRecord(static_cast<hipEvent_t>(ev[i]), s));
@@ -236,9 +239,7 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     if ((st = launch_route(ids, n, *cfg, wsb, L, s)) != AFD_OK) return st;
     if ((st = mark(1)) != AFD_OK) return st;
     if (mx)
-      st = launch_gather_quant_mxfp8(x, reinterpret_cast<const int32_t*>(wsb + L.sorted_pairs),
-                                     reinterpret_cast<const int32_t*>(wsb + L.num_tiles),
-                                     cfg->topk, cfg->hidden, L.np_max, wsb + L.xq, s);
+      st = launch_quant_mxfp8_rows(x, n, cfg->hidden, wsb + L.xq, wsb + L.xs, s);
     else
       st = afd_quant_fp8_1x128(x, n, cfg->hidden, wsb + L.xq,
                                reinterpret_cast<float*>(wsb + L.xs), stream);

@@ -24,6 +24,9 @@ __device__ __forceinline__ int64_t gate_up_source_row(int64_t r, int64_t rows, i
 }
 
 // ---------------------------------------------------------------- MXFP8 activations
+// One lane per 32-element block. kStageOrder stores a row's scales as the MX GEMM reads them:
+// within each group of 4 blocks (one 128-wide K stage), block j at byte scale_byte(j).
+template <bool kStageOrder>
 __global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
     const uint16_t* __restrict__ x, int64_t blocks, int cols, uint8_t* __restrict__ q,
     uint8_t* __restrict__ s) {
@@ -51,17 +54,24 @@ __global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
     float inv = mx_inv_scale(code);
     v4i out[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] * inv)) << (8 * j);
-      out[i / 4][i % 4] = static_cast<int>(packed);
-    }
+    for (int i = 0; i < 8; ++i)
+      out[i / 4][i % 4] = static_cast<int>(
+          pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv, v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
     v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cb * kMxBlock);
     dst[0] = out[0];
     dst[1] = out[1];
-    s[row * bpr + cb] = static_cast<uint8_t>(code);
+    const int64_t at = kStageOrder ? (cb & ~int64_t(3)) + scale_byte(static_cast<int>(cb & 3)) : cb;
+    s[row * bpr + at] = static_cast<uint8_t>(code);
   }
+}
+
+int launch_quant_mxfp8_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* s,
+                            hipStream_t stream) {
+  const int64_t blocks = rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(quant_mxfp8_kernel<true>, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+                     stream, x, blocks, cols, q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
 }
 
 // ---------------------------------------------------------------- FP8 1x128 activations
@@ -158,68 +168,6 @@ __global__ __launch_bounds__(kQuantThreads) void pack_mxfp4_kernel(
   }
 }
 
-// ---------------------------------------------------------------- MXFP8 gather + quantize
-// The A operand of the grouped gate_up GEMM: for every padded row p (rows in expert order,
-// as the router laid them out), the token's activations quantized to MXFP8 and written into
-// the A tile images of row tile p/128. Padding rows get zero codes and zero scales.
-__global__ __launch_bounds__(kQuantThreads) void gather_quant_mxfp8_kernel(
-    const uint16_t* __restrict__ x, const int32_t* __restrict__ sorted_pairs,
-    const int32_t* __restrict__ num_tiles, int topk, int cols, uint8_t* __restrict__ out) {
-  const int bpr = cols / kMxBlock, kstages = cols / kImgK;
-  const int64_t blocks = int64_t(num_tiles[0]) * kImgARows * bpr;
-  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
-       b += int64_t(gridDim.x) * kQuantThreads) {
-    const int64_t p = b / bpr;
-    const int cb = static_cast<int>(b % bpr);
-    const int sp = sorted_pairs[p];
-    v4i out0 = {0, 0, 0, 0}, out1 = {0, 0, 0, 0};
-    uint32_t code = 0;
-    if (sp >= 0) {
-      const v4i* src = reinterpret_cast<const v4i*>(x + int64_t(sp / topk) * cols + cb * kMxBlock);
-      float v[32];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v4i raw = src[i];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t u = static_cast<uint32_t>(raw[q]);
-          v[i * 8 + q * 2] = __uint_as_float(u << 16);
-          v[i * 8 + q * 2 + 1] = __uint_as_float(u & 0xffff0000u);
-        }
-      }
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      code = mx_scale_code(amax, 8);
-      const float inv = mx_inv_scale(code);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        out0[i] = static_cast<int>(
-            pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv, v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
-        out1[i] = static_cast<int>(pk4_e4m3(v[16 + i * 4] * inv, v[17 + i * 4] * inv,
-                                            v[18 + i * 4] * inv, v[19 + i * 4] * inv));
-      }
-    }
-    const int64_t mt = p / kImgARows;
-    const int r = static_cast<int>(p % kImgARows);
-    const int ks = cb / 4, j = cb % 4;
-    uint8_t* img = out + (mt * kstages + ks) * int64_t(kImgA);
-    *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j)) = out0;
-    *reinterpret_cast<v4i*>(img + img_a_off(r, 2 * j + 1)) = out1;
-    img[kImgData + r * 4 + scale_byte(j)] = static_cast<uint8_t>(code);
-  }
-}
-
-int launch_gather_quant_mxfp8(const uint16_t* x, const int32_t* sorted_pairs,
-                              const int32_t* num_tiles, int topk, int cols, int64_t max_rows,
-                              uint8_t* out, hipStream_t stream) {
-  const int64_t blocks = max_rows * (cols / kMxBlock);
-  hipLaunchKernelGGL(gather_quant_mxfp8_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
-                     stream, x, sorted_pairs, num_tiles, topk, cols, out);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
-}
-
 // Physical row of logical row lr when gate and up rows are interleaved in groups of g
 // (the inverse of gate_up_source_row).
 __device__ __forceinline__ int64_t gate_up_dest_row(int64_t lr, int64_t rows, int g) {
@@ -290,7 +238,7 @@ extern "C" int afd_quant_mxfp8(const uint16_t* x, int64_t rows, int32_t cols, ui
   if (cols <= 0 || cols % kMxBlock) return AFD_ERR_SHAPE;
   if (rows == 0) return AFD_OK;
   int64_t blocks = rows * (cols / kMxBlock);
-  hipLaunchKernelGGL(quant_mxfp8_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+  hipLaunchKernelGGL(quant_mxfp8_kernel<false>, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
                      static_cast<hipStream_t>(stream), x, blocks, cols, q, s);
   AFD_CHECK_LAUNCH();
   return AFD_OK;

@@ -46,9 +46,11 @@ def test_workspace_layout_dsv4_rank():
     assert L["np_max"] == (16384 * 8 + 64 * 127 + 127) // 128 * 128
     tiles = L["np_max"] // 128
     assert L["max_tiles"] == tiles
-    # MXFP4: xq holds one A tile image (16896 B) per row tile and 128-wide K stage
-    # (+ 512 B of readable slack after the last image, rounded to 256 B)
-    assert L["xq"] == 0 and L["xs"] == -(-(tiles * (4096 // 128) * 16896 + 512) // 256) * 256
+    # MXFP4: xq / xs are the per-token e4m3 rows and their UE8M0 scales; hq holds one A tile
+    # image (16896 B) per row tile and 128-wide K stage of h (+ 512 B of readable slack after
+    # the last image, rounded to 256 B)
+    assert L["xq"] == 0 and L["xs"] == 16384 * 4096
+    assert L["counts"] - L["xs"] == 16384 * 4096 // 32
     assert L["hs"] - L["hq"] == -(-(tiles * (2048 // 128) * 16896 + 512) // 256) * 256
     offs = [L[k] for k in ("xq", "xs", "counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos",
                            "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]

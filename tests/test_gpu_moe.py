@@ -72,19 +72,16 @@ def test_tiny_layer_mxfp4():
     s = W.SHAPES["tiny"]
     experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k, s.tokens, "mxfp4", seed=0)
     assert_close(out, ref, ids.numpy(), s.local)
-    # intermediates: the routing and the gathered, quantized activations are bit-exact
+    # intermediates: the routing and the quantized token rows are bit-exact
     n, k = ids.shape
     pos = experts.ws_view("pair_pos", torch.int32, n * k, n).cpu().numpy()
     assert np.array_equal(pos, parts["route"]["pair_pos"])
-    sp = parts["route"]["sorted_pairs"]
-    tiles = len(sp) // 128
-    img = u8(experts.ws_view("xq", torch.uint8, tiles * (s.hidden // 128) * L.IMG_A, n))
-    codes, scales = L.a_rows(img, s.hidden)
+    codes = u8(experts.ws_view("xq", torch.uint8, n * s.hidden, n)).reshape(n, s.hidden)
+    scales = u8(experts.ws_view("xs", torch.uint8, n * s.hidden // 32, n)).reshape(n, -1, 4)
     q_ref, s_ref = F.mx_quantize(F.bf16_to_f32(bits16(x)), "e4m3")
-    valid = sp >= 0
-    assert np.array_equal(codes[valid], q_ref[sp[valid] // k])
-    assert np.array_equal(scales[valid], s_ref[sp[valid] // k])
-    assert not codes[~valid].any() and not scales[~valid].any()
+    assert np.array_equal(codes, q_ref)
+    # scales in stage order: within each 128-wide K stage, block j at byte (2 (j & 1) | j >> 1)
+    assert np.array_equal(scales[..., L.SCALE_ORDER].reshape(n, -1), s_ref)
 
 
 @pytest.mark.parametrize(
