@@ -99,8 +99,9 @@ typedef struct afd_expert_weights {
 /* Byte offsets of the internal buffers of afd_moe_ffn's workspace for n tokens. */
 typedef struct afd_ws_layout {
   uint64_t total;          /* bytes the workspace must have */
-  uint64_t xq, xs;         /* quantized activations and their scales (MXFP4: gate_up A tile
-                              images of every padded row, scales inside, xs empty) */
+  uint64_t xq, xs;         /* quantized activations [n][H] and their scales (MXFP4: e4m3 and
+                              UE8M0 per 32, the 4 of each 128-wide K stage in stage order;
+                              FP8 block: e4m3 and f32 per 1x128) */
   uint64_t counts;         /* i32 [E] pairs per local expert */
   uint64_t offsets;        /* i32 [E+1] exclusive prefix of counts */
   uint64_t padded_offsets; /* i32 [E+1] the same with every segment padded to block_m */
