@@ -133,6 +133,71 @@ __device__ __forceinline__ uint32_t div_by_magic(uint32_t n, uint32_t magic) {
   return magic ? __umulhi(n, magic) : n;
 }
 
+// ---------------------------------------------------------------- persistent GEMM tile walk
+// Output tiles of a grouped GEMM: row tiles [0, rows) (read from device memory) x column
+// tiles [0, ntn). The dispatcher deals workgroups to the 8 XCDs round robin (workgroup b runs
+// on XCD b % 8), and each XCD has its own L2. With a grid that is a multiple of 8 and at
+// least kWalkSplitRows row tiles, XCD x takes the contiguous row tiles
+// [rows x / 8, rows (x + 1) / 8), else every workgroup walks all of them. A workgroup visits
+// walk positions first, first + stride, ...; 32 consecutive positions form a block of BR row
+// tiles x 32 / BR column tiles (row tiles fastest; row blocks outer, column blocks inner), so
+// the ~32 workgroups of an XCD run about one block at a time and share each activation slice
+// 32 / BR ways and each weight slice BR ways in their L2. Positions past the last row or
+// column tile are holes and are skipped.
+constexpr int kWalkSplitRows = 32;
+template <int BR>
+inline int walk_col_blocks(int ntn) {
+  return (ntn + 32 / BR - 1) / (32 / BR);
+}
+
+template <int BR>
+struct TileWalk {
+  static_assert(BR == 1 || BR == 2 || BR == 4 || BR == 8 || BR == 16 || BR == 32, "BR divides 32");
+  static constexpr int kBC = 32 / BR;
+  int mt0, rows_here, ntn, ncb, first, stride, count;
+  uint32_t ncb_magic;
+  // ncb_magic_ = div_magic(walk_col_blocks<BR>(ntn_))
+  __device__ __forceinline__ TileWalk(int rows, int ntn_, uint32_t ncb_magic_) {
+    ntn = ntn_;
+    ncb = (ntn_ + kBC - 1) / kBC;
+    ncb_magic = ncb_magic_;
+    mt0 = 0;
+    rows_here = rows;
+    first = blockIdx.x;
+    stride = gridDim.x;
+    if ((gridDim.x & 7) == 0 && rows >= kWalkSplitRows) {
+      const int xcd = blockIdx.x & 7;
+      mt0 = (rows * xcd) >> 3;
+      rows_here = ((rows * (xcd + 1)) >> 3) - mt0;
+      first = blockIdx.x >> 3;
+      stride = gridDim.x >> 3;
+    }
+    count = (rows_here + BR - 1) / BR * ncb * 32;
+  }
+  // the tile at walk position i; false for a hole
+  __device__ __forceinline__ bool at(int i, int& mt, int& nt) const {
+    const int b = i >> 5, k = i & 31;
+    const int rb = static_cast<int>(div_by_magic(static_cast<uint32_t>(b), ncb_magic));
+    const int r = rb * BR + k % BR;
+    const int c = (b - rb * ncb) * kBC + k / BR;
+    mt = mt0 + r;
+    nt = c;
+    return r < rows_here && c < ntn;
+  }
+  // the next tile position after i (count if none)
+  __device__ __forceinline__ int next(int i) const {
+    int mt, nt;
+    for (i += stride; i < count; i += stride)
+      if (at(i, mt, nt)) break;
+    return i < count ? i : count;
+  }
+  __device__ __forceinline__ int begin() const {
+    int mt, nt;
+    if (first < count && at(first, mt, nt)) return first;
+    return next(first);
+  }
+};
+
 // ---------------------------------------------------------------- MX GEMM operand tile images
 // The MX grouped GEMMs copy their operands HBM -> LDS as contiguous "tile images": the exact
 // LDS bytes of one K stage (128 K values) of one row tile, followed by the UE8M0 scales of

@@ -1,268 +1,420 @@
 // Grouped FP8-e4m3 GEMMs with 128x128-block fp32 weight scales and 1x128 fp32 activation
-// scales (the block-FP8 expert format) on gfx950 MFMA (v_mfma_f32_32x32x64_f8f6f4, e4m3 x
-// e4m3, unscaled).
+// scales (the block-FP8 expert format) on gfx950 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4 with
+// unit scales, e4m3 x e4m3).
 //
-// A K stage is exactly one 128-wide scale block: the two MFMA k-steps of a stage accumulate
-// into a per-stage partial, which is then folded into the running accumulator with
-// acc += partial * (s_a[row] * s_w[block]) - the exact block-scaled product, computed in fp32.
+//   gate_up: h[p, :] = silu(x_t . Wg_e^T) * (x_t . Wu_e^T) for every padded row p of expert e
+//            (t = token of the pair at row p), quantized to e4m3 with one fp32 scale per 1x128
+//            group (the down GEMM's A operand and its scales).
+//   down:    y[p, :] = bf16(h_p . W2_e^T).
 //
-// Tiling as in the MXFP4 kernel (128 x 256 per workgroup, 2 x 2 wavefronts of 64 x 128), with
-// a 32 KiB fp8 B stage; two stages take ~97 KiB of LDS, one workgroup per CU. W13 rows are
-// interleaved gate/up in groups of 32 as in the MXFP4 layout, so SwiGLU happens in registers;
-// W13 scales stay in logical block order ([gate blocks; up blocks]), so each wavefront's
-// column subtiles j = 0, 2 use the gate block scale and j = 1, 3 the up block scale.
+// Block scales: a 128-wide K stage kb is exactly one scale block of both operands, with the
+// product s_kb = s_x[row, kb] * s_w[block, kb]; the result is sum_kb s_kb * P_kb, P_kb the
+// stage's unscaled MFMA sum. The accumulators hold R_kb = (sum_{k <= kb} s_k P_k) / s_kb: before
+// stage kb's MFMAs they are multiplied by s_{kb-1} / s_kb, the MFMAs then add P_kb, and the
+// epilogue multiplies by the last s. This costs no second set of registers for the partial
+// sums and one multiply per accumulator and stage; it rounds differently from folding each
+// stage separately by about one fp32 rounding per stage (relative 2^-24 each). The MFMA
+// operands are swapped (weights first, activations second), so a lane's accumulators all
+// belong to one activation row and s_kb is one value per 32x32 tile.
+//
+// Tiling: a workgroup of 8 wavefronts owns a 128 x 256 output tile; wavefront (g, c) owns rows
+// [64 g, 64 g + 64) and columns [64 c, 64 c + 64): 2 x 2 MFMA tiles, 64 accumulators per lane. Both operands move HBM -> LDS with gfx950's direct global_load_lds in
+// 1 KiB pieces of 8 rows x 128 B, each lane fetching one 16-byte chunk of a row at its own
+// offset, so the activation rows are gathered (gate_up: the token rows through sorted_pairs;
+// down: the tile's rows of h) and the weight rows come straight from the [E][N][K] layout. LDS
+// holds every operand in the swizzled 128-byte-row layout of the MX kernel's A images (no bank
+// conflicts for the MFMA operand reads), in a ring of 3 stages. As in the MX kernel, the two
+// wavefronts of a SIMD (group 0: rows 0-63, group 1: rows 64-127) ping-pong between reading a
+// stage from LDS and running its 8 MFMAs (and rescaling its accumulators), half a stage
+// apart. The persistent workgroups walk the tiles XCD by XCD in blocks of 8 x 4 tiles
+// (TileWalk).
+#include <type_traits>
+
 #include "afd_common.h"
 #include "afd_internal.h"
 
 namespace afd {
 namespace fp8 {
 
-constexpr int kBM = kBlockM;  // 128
-constexpr int kBN = 256;
-constexpr int kBK = 128;
-constexpr int kThreads = 256;
-constexpr int kAStage = kBM * kBK;  // 16 KiB
-constexpr int kBStage = kBN * kBK;  // 32 KiB
-constexpr int kSAStage = kBM * 4;
-constexpr int kSBStage = 128;  // 2 floats used, padded
-constexpr int kStage = kAStage + kBStage + kSAStage + kSBStage;
-constexpr int kLdsBytes = 2 * kStage;
-constexpr int kHStride = 132;
-constexpr int kYStride = 264;
-static_assert(kBM * kHStride * 4 <= kLdsBytes, "epilogue tile must fit");
-
 enum { kGateUp = 0, kDown = 1 };
 
+// Tile walk blocks of 8 row tiles x 4 column tiles: a 1 MiB weight slice is shared 8 ways
+// (column-tile-fastest walks fetch ~3x more from beyond L2).
+constexpr int kWalkRows = 8;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBM = kBlockM;  // 128 activation rows
+constexpr int kBN = 256;      // weight rows (output columns)
+constexpr int kBK = 128;      // K per stage = one scale block
+// LDS stage: activations (128 rows x 128 B), their 128 fp32 scales, weights (256 rows x 128 B)
+constexpr int kXScales = kBM * kBK;         // 16384
+constexpr int kWOff = kXScales + kBM * 4;   // 16896
+constexpr int kStage = kWOff + kBN * kBK;   // 49664
+constexpr int kStages = 3;
+// after the ring: the tile's weight block scales for every K stage, two blocks x 32 stages
+// per 256 B group (written by one wavefront's dword copies)
+constexpr int kWScales = kStages * kStage;
+constexpr int kMaxKT = 128;
+constexpr int kLds = kWScales + 2 * kMaxKT * 4;
+// copies per wavefront and stage: 2 activation pieces, 4 weight pieces and one piece of
+// activation scales (a wavefront past the two halves repeats its first weight piece: the same
+// bytes to the same place), so every wavefront counts the same number of copies
+constexpr int kQX = kBM / 8 / kWaves;  // 2
+constexpr int kQW = kBN / 8 / kWaves;  // 4
+constexpr int kPieces = kQX + kQW + 1;
+constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
+constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
+static_assert(kQX * kWaves * 8 == kBM && kQW * kWaves * 8 == kBN, "pieces cover the tile");
+static_assert(kBM * kHStride * 4 <= kStages * kStage, "gate_up epilogue tile must fit the stages");
+static_assert(kBM * kYStride * 2 <= kStages * kStage, "down epilogue tile must fit the stages");
+static_assert(kLds <= 160 * 1024, "LDS of one CU");
+static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
+
 struct Fp8GemmArgs {
-  const uint8_t* a;   // gate_up: xq [n][K]; down: hq [np][K]
-  const float* as;    // [rows][K/128]
-  const int32_t* sorted_pairs;
-  const int32_t* tile_expert;
-  const int32_t* num_tiles;
-  const uint8_t* b;   // e4m3 [E][N][K] (gate_up rows interleaved by 32)
-  const float* bs;    // [E][N/128][K/128] logical block order
-  int K, N, topk;
-  uint8_t* hq;        // gate_up out e4m3 [np][N/2]
-  float* hs;          // gate_up out [np][N/256]
-  uint16_t* y;        // down out bf16 [np][N]
+  const uint8_t* a;   // gate_up: token rows xq [n][K]; down: hq [np][K]
+  const float* as;    // their scales: xs [n][K/128]; hs [np][K/128]
+  int topk;
+  uint32_t topk_magic;  // div_magic(topk)
+  uint32_t ncb_magic;   // div_magic(walk_col_blocks<kWalkRows>(N / 256))
+  const uint8_t* b;     // e4m3 [E][N][K] (gate_up rows interleaved gate/up by 32)
+  const float* bs;      // [E][N/128][K/128] in logical block order
+  const int32_t* sorted_pairs;    // [np] flat pair index per padded row, -1 = pad
+  const int32_t* tile_expert;     // [row tiles]
+  const int32_t* num_tiles;       // [1]
+  const int32_t* padded_offsets;  // [E + 1]
+  const int32_t* counts;          // [E]
+  int K, N;
+  uint8_t* hq;  // gate_up out: e4m3 [np][N/2]
+  float* hs;    // gate_up out: fp32 [np][N/256]
+  uint16_t* y;  // down out: bf16 [np][N]
 };
-
-__device__ __forceinline__ int row_off(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-
-template <int MODE>
-__device__ __forceinline__ int64_t a_row(const Fp8GemmArgs& p, int m) {
-  if (MODE == kGateUp) {
-    int sp = p.sorted_pairs[m];
-    return sp >= 0 ? sp / p.topk : 0;
-  }
-  return m;
-}
 
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
-  const int ntn = p.N / kBN;
-  const int tiles = p.num_tiles[0] * ntn;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
+  const int wm = w_u / 4, wn = w_u % 4, lr = lane & 31, lk = lane >> 5;
+  const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic);
   const int KT = p.K / kBK;
-  const int64_t a_ld = p.K, sa_ld = p.K / kBK, b_ld = p.K;
-  const int kb = p.K / kBK;        // scale blocks along K
-  const int nb_all = p.N / kBK;    // scale blocks along N
+  const int nblk = p.N / kBK;  // weight scale blocks along N
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const int mt = tile / ntn, nt = tile % ntn;
+  // Copy offsets. Piece q of a wavefront covers 8 rows: image row r = 8 (w Q + q) + lane / 8,
+  // physical chunk lane % 8, i.e. logical chunk (lane % 8) ^ swizzle(r) of the source row.
+  // Weight rows and down's h rows are fixed per lane (the tile is a scalar base); gate_up's
+  // rows are token rows, looked up per tile. Wavefronts 0 and 1 also copy the activation
+  // scales of rows [64 w, 64 w + 64).
+  auto chunk = [&](int r) { return (lane & 7) ^ ((r ^ (r >> 3)) & 7); };
+  uint32_t w_voff[kQW];
+#pragma unroll
+  for (int q = 0; q < kQW; ++q) {
+    const int r = 8 * (w_u * kQW + q) + (lane >> 3);
+    w_voff[q] = static_cast<uint32_t>(r * p.K + chunk(r) * 16);
+  }
+  const bool copies_scales = w_u < 2;
+  const int s_row = 64 * (w_u & 1) + lane;
+
+  // A tile's metadata is loaded one tile ahead and decoded after the previous tile's K loop,
+  // whose last wait leaves no copy in flight, so no tile starts by waiting for a load.
+  int sp_next[kQX + 1], e_next = 0;
+  auto load_next = [&](int ii) {
+    int m, nn;
+    walk.at(ii, m, nn);
+    e_next = p.tile_expert[m];
+    if constexpr (MODE == kGateUp) {
+#pragma unroll
+      for (int q = 0; q < kQX; ++q)
+        sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * kQX + q) + (lane >> 3)];
+      sp_next[kQX] = p.sorted_pairs[m * kBM + s_row];
+    }
+  };
+  int e_cur = 0;
+  uint32_t x_voff[kQX], s_voff;
+  // down: rows of the tile, relative to the tile's first row
+#pragma unroll
+  for (int q = 0; q < kQX; ++q) {
+    const int r = 8 * (w_u * kQX + q) + (lane >> 3);
+    x_voff[q] = static_cast<uint32_t>(r * p.K + chunk(r) * 16);
+  }
+  s_voff = static_cast<uint32_t>(s_row * KT * 4);
+  auto decode_next = [&]() {
+    e_cur = __builtin_amdgcn_readfirstlane(e_next);
+    if constexpr (MODE == kGateUp) {
+      // padding rows (-1) read token 0; their results are never used
+      auto token = [&](int sp) {
+        return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
+      };
+#pragma unroll
+      for (int q = 0; q < kQX; ++q) {
+        const int r = 8 * (w_u * kQX + q) + (lane >> 3);
+        x_voff[q] = token(sp_next[q]) * static_cast<uint32_t>(p.K) + chunk(r) * 16;
+      }
+      s_voff = token(sp_next[kQX]) * static_cast<uint32_t>(KT * 4);
+    }
+  };
+  int i = walk.begin();
+  if (i < walk.count) {
+    load_next(i);
+    decode_next();
+  }
+
+  for (int i_next; i < walk.count; i = i_next) {
+    int mt, nt;
+    walk.at(i, mt, nt);
+    i_next = walk.next(i);
     const int m0 = mt * kBM, n0 = nt * kBN;
-    const int64_t e = p.tile_expert[mt];
+    const int64_t e = e_cur;
+    // down: the expert's pairs fill its first rows; rows below row_end are real
+    int row_end = 0;
+    if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
+    const bool has_next = i_next < walk.count;
+    if (has_next) load_next(i_next);
 
-    const uint8_t* a_src[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      int r = j * 32 + (t >> 3);
-      a_src[j] = p.a + a_row<MODE>(p, m0 + r) * a_ld + (t & 7) * 16;
-    }
-    const uint8_t* b_src[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int n = j * 32 + (t >> 3);
-      b_src[j] = p.b + (e * p.N + n0 + n) * b_ld + (t & 7) * 16;
-    }
-    const float* sa_src = p.as + a_row<MODE>(p, m0 + (t & (kBM - 1))) * sa_ld;
-    // the two weight scale blocks this tile touches
-    int sblk = 0;
-    if (MODE == kGateUp)
-      sblk = (t == 0) ? n0 / 256 : (nb_all / 2 + n0 / 256);
-    else
-      sblk = n0 / 128 + (t & 1);
-    const float* sb_src = p.bs + (e * nb_all + sblk) * kb;
+    const uint8_t* x_tile = MODE == kGateUp ? p.a : p.a + int64_t(m0) * p.K;
+    const float* s_tile = MODE == kGateUp ? p.as : p.as + int64_t(m0) * KT;
+    const uint8_t* w_tile = p.b + (e * p.N + n0) * int64_t(p.K);
+    // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
+    // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
+    const int blk0 = MODE == kGateUp ? n0 / 256 : n0 / 128;
+    const int blk1 = MODE == kGateUp ? nblk / 2 + n0 / 256 : n0 / 128 + 1;
 
-    v4i ra[4], rb[8];
-    float rsa = 0.0f, rsb = 0.0f;
-    auto load = [&](int kt) {
-      const int k0 = kt * kBK;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const v4i*>(a_src[j] + k0);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) rb[j] = *reinterpret_cast<const v4i*>(b_src[j] + k0);
-      if (t < kBM) rsa = sa_src[kt];
-      if (t < 2) rsb = sb_src[kt];
-    };
-    auto store = [&](int s) {
-      uint8_t* base = lds + s * kStage;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int r = j * 32 + (t >> 3);
-        *reinterpret_cast<v4i*>(base + row_off(r, t & 7)) = ra[j];
+    auto issue_piece = [&](int kt, auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+      if constexpr (q < kQX) {
+        lds_dma16(st + (w_u * kQX + q) * 1024, x_tile + kt * kBK, x_voff[q]);
+      } else if constexpr (q < kQX + kQW) {
+        constexpr int qw = q - kQX;
+        lds_dma16(st + kWOff + (w_u * kQW + qw) * 1024, w_tile + kt * kBK, w_voff[qw]);
+      } else {
+        if (copies_scales)
+          lds_dma4(st + kXScales + (w_u & 1) * 256, s_tile + kt, s_voff);
+        else
+          lds_dma16(st + kWOff + w_u * kQW * 1024, w_tile + kt * kBK, w_voff[0]);
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        int n = j * 32 + (t >> 3);
-        *reinterpret_cast<v4i*>(base + kAStage + row_off(n, t & 7)) = rb[j];
-      }
-      float* sa = reinterpret_cast<float*>(base + kAStage + kBStage);
-      if (t < kBM) sa[t] = rsa;
-      if (t < 2) sa[kBM + t] = rsb;
     };
+    auto issue = [&](int kt) { static_for<kPieces>([&](auto q) { issue_piece(kt, q); }); };
 
-    v16f acc[2][4];
+    v16f acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
-    const v16f zero = {};
+        for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
 
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      if (kt + 1 < KT) load(kt + 1);
-      const uint8_t* base = lds + (kt & 1) * kStage;
-      const float* sa = reinterpret_cast<const float*>(base + kAStage + kBStage);
-      v16f part[2][4];
+    // Operand fragments of both k-steps of one stage and the stage's scales. An 8-bit operand
+    // lane half h holds K [16h, 16h+16) in bytes 0-15 and K [32+16h, 32+16h+16) in bytes 16-31
+    // of the k-step. x: activation rows 64 g + 32 i + lane % 32; w: weight rows
+    // 64 c + 32 j + lane % 32.
+    struct Frag {
+      v8i x[2][2], w[2][2];  // [ks][i], [ks][j]
+      float sx[2], sw[2];
+    };
+    Frag f;
+    float sx_prev[2] = {1.0f, 1.0f}, sw_prev[2] = {1.0f, 1.0f};
+    const float* wsc = reinterpret_cast<const float*>(lds + kWScales);
+    auto read_stage = [&](int kt) {
+      const uint8_t* xb = lds + (kt % kStages) * kStage;
+      const uint8_t* wb = xb + kWOff;
+      // row r + 32 has the swizzle of row r with chunk bit 2 flipped: its chunk c sits 4096 B
+      // after row r's chunk c ^ 4, so four lane addresses serve both row blocks
+      const int rx = wm * 64 + lr, rw = wn * 64 + lr;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        v8i af[2], bf[4];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          int r = wm * 64 + i * 32 + lr;
-          int c0 = ks * 4 + lk * 2;
-          v4i lo = *reinterpret_cast<const v4i*>(base + row_off(r, c0));
-          v4i hi = *reinterpret_cast<const v4i*>(base + row_off(r, c0 + 1));
-          af[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int kc = (ks ^ i2) * 4 + lk;
+          v4i lo = *reinterpret_cast<const v4i*>(xb + img_a_off(rx, kc) + i2 * 4096);
+          v4i hi = *reinterpret_cast<const v4i*>(xb + img_a_off(rx, kc + 2) + i2 * 4096);
+          f.x[ks][i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          lo = *reinterpret_cast<const v4i*>(wb + img_a_off(rw, kc) + i2 * 4096);
+          hi = *reinterpret_cast<const v4i*>(wb + img_a_off(rw, kc + 2) + i2 * 4096);
+          f.w[ks][i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          int n = wn * 128 + j * 32 + lr;
-          int c0 = ks * 4 + lk * 2;
-          v4i lo = *reinterpret_cast<const v4i*>(base + kAStage + row_off(n, c0));
-          v4i hi = *reinterpret_cast<const v4i*>(base + kAStage + row_off(n, c0 + 1));
-          bf[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            part[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                af[i], bf[j], ks == 0 ? zero : part[i][j], 0, 0, 0, 0, 0, 0);
       }
-      // fold the stage's partial with its block scales
-      float sbw[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sbw[j] = MODE == kGateUp ? sa[kBM + (j & 1)] : sa[kBM + wn];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        float sav[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          v4f s4 = *reinterpret_cast<const v4f*>(sa + wm * 64 + i * 32 + g * 8 + lk * 4);
-          sav[g * 4] = s4[0];
-          sav[g * 4 + 1] = s4[1];
-          sav[g * 4 + 2] = s4[2];
-          sav[g * 4 + 3] = s4[3];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int q = 0; q < 16; ++q)
-            acc[i][j][q] = fmaf(part[i][j][q], sav[q] * sbw[j], acc[i][j][q]);
+      const float* sx = reinterpret_cast<const float*>(xb + kXScales);
+      f.sx[0] = sx[wm * 64 + lr];
+      f.sx[1] = sx[wm * 64 + 32 + lr];
+      // block b of stage kt at group kt / 32, half b, word kt % 32
+      const float* sw = wsc + (kt >> 5) * 64 + (kt & 31);
+      if constexpr (MODE == kGateUp) {
+        f.sw[0] = sw[0];
+        f.sw[1] = sw[32];
+      } else {
+        f.sw[0] = f.sw[1] = sw[(wn >> 1) * 32];
       }
-      if (kt + 1 < KT) store((kt + 1) & 1);
-      __syncthreads();
-    }
+    };
+    // The stage's 8 MFMAs. Before its first k-step, a tile's accumulators go from R_{kb-1} to
+    // R_{kb-1} * s_{kb-1} / s_kb (stage kb's scales are in f); those 16 multiplies overlap the
+    // previous tiles' MFMAs. On the first stage the accumulators are 0 and the ratio is unused.
+    auto mma_stage = [&]() {
+      float ratio[2][2];
+#pragma unroll
+      for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          ratio[i2][j] = (sx_prev[i2] * sw_prev[j]) * __builtin_amdgcn_rcpf(f.sx[i2] * f.sw[j]);
+      static_for<2>([&](auto ksc) {
+        constexpr int ks = decltype(ksc)::value;
+        static_for<2>([&](auto i2c) {
+          constexpr int i2 = decltype(i2c)::value;
+          static_for<2>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            if constexpr (ks == 0) {
+#pragma unroll
+              for (int q = 0; q < 16; ++q) acc[i2][j][q] *= ratio[i2][j];
+            }
+            // D[weight row][activation row]: lane x holds activation row x % 32
+            acc[i2][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                f.w[ks][j], f.x[ks][i2], acc[i2][j], 0 /*e4m3*/, 0 /*e4m3*/, 0, 127 /*x1*/, 0,
+                127 /*x1*/);
+          });
+        });
+      });
+      sx_prev[0] = f.sx[0];
+      sx_prev[1] = f.sx[1];
+      sw_prev[0] = f.sw[0];
+      sw_prev[1] = f.sw[1];
+    };
 
-    if (MODE == kGateUp) {
-      float* hl = reinterpret_cast<float*>(lds);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
-            int col = wn * 64 + jj * 32 + lr;
-            float g = acc[i][2 * jj][q], u = acc[i][2 * jj + 1][q];
-            hl[row * kHStride + col] = g / (1.0f + expf(-g)) * u;
-          }
-      __syncthreads();
-      // one 1x128 group per row: 2 lanes per row, 64 values each
-      const int inter = p.N / 2;
-      const int row = t >> 1, half = t & 1;
-      const int grow = m0 + row;
-      const float* src = hl + row * kHStride + half * 64;
-      float v[64];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        v4f x4 = reinterpret_cast<const v4f*>(src)[i];
-        v[i * 4] = x4[0];
-        v[i * 4 + 1] = x4[1];
-        v[i * 4 + 2] = x4[2];
-        v[i * 4 + 3] = x4[3];
+    // Ping-pong as in the MX kernel: each group copies its pieces of stage kt+2 when it starts
+    // reading stage kt;
+    // copies are clamped to the last stage (a clamped copy rewrites a slot with its own
+    // bytes). Wavefront 0 first copies the tile's weight block scales; those copies are older
+    // than every piece of stage 0, so the wait for stage 0 covers them.
+    const int last = KT - 1;
+    if (w_u == 0) {
+      // lane x: block (x < 32 ? blk0 : blk1), stage 32 g + x % 32 (clamped: in bounds)
+      const float* bs_e = p.bs + e * nblk * KT;
+      const int b = lk == 0 ? blk0 : blk1;
+      for (int g = 0; g * 32 < KT; ++g) {
+        const int kb = min(lr + 32 * g, KT - 1);
+        lds_dma4(lds_base + kWScales + g * 256, bs_e, static_cast<uint32_t>((b * KT + kb) * 4));
       }
-      float amax = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(v[i]));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
-      if (p.sorted_pairs[grow] >= 0) {
-        uint8_t* dst = p.hq + int64_t(grow) * inter + n0 / 2 + half * 64;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v4i out;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            uint32_t packed = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-              packed |= f32_to_e4m3(clamp_e4m3(v[i * 16 + j * 4 + b] / sc)) << (8 * b);
-            out[j] = static_cast<int>(packed);
-          }
-          reinterpret_cast<v4i*>(dst)[i] = out;
-        }
-        if (half == 0) p.hs[int64_t(grow) * (inter / kBK) + n0 / 256] = sc;
+    }
+    issue(0);
+    issue(min(1, last));
+    wait_vmcnt<kPieces>();  // own pieces of stage 0 (and the weight scales) landed
+    __syncthreads();
+    if (wm == 0) {
+      for (int kt = 0; kt < KT; ++kt) {
+        issue(min(kt + 2, last));
+        read_stage(kt);
+        wait_vmcnt_lds<2 * kPieces>();  // own reads done (copies may be in flight)
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_stage();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<kPieces>();  // own pieces of stage kt+1 landed
+        __syncthreads();
       }
       __syncthreads();
     } else {
+      __syncthreads();
+      for (int kt = 0; kt < KT; ++kt) {
+        issue(min(kt + 2, last));
+        read_stage(kt);
+        wait_vmcnt_lds<kPieces>();  // own reads done, own pieces of stage kt+1 landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_stage();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+      }
+    }
+    // R_last * s_last
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float sl = sx_prev[i2] * sw_prev[j];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[i2][j][q] *= sl;
+      }
+    wait_vmcnt<0>();  // no copy may land in the stage buffers the epilogue reuses
+    __syncthreads();  // the epilogue reuses the stage buffers
+    if (has_next) decode_next();
+
+    // accumulator q of tile (i, j): activation row 64 g + 32 i + lane % 32, output column
+    // 64 c + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
+    if constexpr (MODE == kGateUp) {
+      // SwiGLU in registers: column tiles j = 0, 1 are the gate and up halves of one 64-row
+      // group of interleaved W13, i.e. the same 32 intermediate columns.
+      float* hl = reinterpret_cast<float*>(lds);
+#pragma unroll
+      for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int row = wm * 64 + i2 * 32 + lr;
+          const int col = wn * 32 + q4 * 8 + lk * 4;
+          v4f hv;
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const float g = acc[i2][0][q4 * 4 + e4], u = acc[i2][1][q4 * 4 + e4];
+            hv[e4] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+          }
+          *reinterpret_cast<v4f*>(hl + row * kHStride + col) = hv;
+        }
+      __syncthreads();
+      // the tile's 128 h columns are one 1x128 group per row: 4 lanes per row, 32 values each
+      const int inter = p.N / 2;
+      const int row = t >> 2, quarter = t & 3;
+      const float* src = hl + row * kHStride + quarter * 32;
+      float v[32];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        v4f x4 = reinterpret_cast<const v4f*>(src)[k];
+        v[k * 4] = x4[0];
+        v[k * 4 + 1] = x4[1];
+        v[k * 4 + 2] = x4[2];
+        v[k * 4 + 3] = x4[3];
+      }
+      float amax = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
+      v4i out[2];
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        out[k / 4][k % 4] = static_cast<int>(pk4_e4m3(v[k * 4] / sc, v[k * 4 + 1] / sc,
+                                                      v[k * 4 + 2] / sc, v[k * 4 + 3] / sc));
+      uint8_t* dst = p.hq + int64_t(m0 + row) * inter + n0 / 2 + quarter * 32;
+      reinterpret_cast<v4i*>(dst)[0] = out[0];
+      reinterpret_cast<v4i*>(dst)[1] = out[1];
+      if (quarter == 0) p.hs[int64_t(m0 + row) * (inter / kBK) + n0 / 256] = sc;
+      __syncthreads();
+    } else {
+      const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
-            int col = wn * 128 + j * 32 + lr;
-            yl[row * kYStride + col] = f32_to_bf16(acc[i][j][q]);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int row = wm * 64 + i2 * 32 + lr;
+            const int col = wn * 64 + j * 32 + q4 * 8 + lk * 4;
+            const v16f& a = acc[i2][j];
+            uint2 two = {pk_bf16(a[q4 * 4], a[q4 * 4 + 1]), pk_bf16(a[q4 * 4 + 2], a[q4 * 4 + 3])};
+            *reinterpret_cast<uint2*>(yl + row * kYStride + col) = two;
           }
       __syncthreads();
+      constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
 #pragma unroll 4
-      for (int q = 0; q < 16; ++q) {
-        int idx = q * kThreads + t;
-        int row = idx >> 5, c = idx & 31;
-        int grow = m0 + row;
-        if (p.sorted_pairs[grow] >= 0)
-          *reinterpret_cast<v4i*>(p.y + int64_t(grow) * p.N + n0 + c * 8) =
+      for (int q = 0; q < kBM * kChunksPerRow / kThreads; ++q) {
+        const int idx = q * kThreads + t;
+        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        if (row < nvalid)
+          *reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8) =
               *reinterpret_cast<const v4i*>(yl + row * kYStride + c * 8);
       }
       __syncthreads();
@@ -270,9 +422,41 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   }
 }
 
-static int persistent_grid(int max_tiles) {
-  int g = device_cu_count();  // ~97 KiB of LDS: one workgroup per CU
-  return max_tiles < g ? (max_tiles < 1 ? 1 : max_tiles) : g;
+template <int MODE>
+static int launch(Fp8GemmArgs p, int max_row_tiles, hipStream_t stream) {
+  if (p.K % kBK || p.N % kBN || p.K / kBK > kMaxKT) return AFD_ERR_SHAPE;
+  static int per_cu = 0;  // resident workgroups per CU (registers and LDS decide)
+  if (per_cu == 0) {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fp8_gemm_kernel<MODE>, kThreads, 0) !=
+            hipSuccess ||
+        b < 1)
+      b = 1;
+    per_cu = b;
+  }
+  const int max_tiles = max_row_tiles * (p.N / kBN);
+  p.ncb_magic = div_magic(walk_col_blocks<kWalkRows>(p.N / kBN));
+  int grid = device_cu_count() * per_cu;
+  if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
+  hipLaunchKernelGGL(fp8_gemm_kernel<MODE>, dim3(grid), dim3(kThreads), 0, stream, p);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws_layout& L) {
+  Fp8GemmArgs p;
+  p.topk = cfg.topk;
+  p.topk_magic = div_magic(cfg.topk);
+  p.ncb_magic = 0;
+  p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
+  p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
+  p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
+  p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
+  p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
+  p.hq = nullptr;
+  p.hs = nullptr;
+  p.y = nullptr;
+  return p;
 }
 
 }  // namespace fp8
@@ -280,49 +464,30 @@ static int persistent_grid(int max_tiles) {
 int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                        const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
-  fp8::Fp8GemmArgs p;
+  fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
   p.a = ws + L.xq;
   p.as = reinterpret_cast<const float*>(ws + L.xs);
-  p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
-  p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
-  p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
   p.b = static_cast<const uint8_t*>(wt.w13);
   p.bs = static_cast<const float*>(wt.s13);
   p.K = cfg.hidden;
   p.N = 2 * cfg.inter;
-  p.topk = cfg.topk;
   p.hq = ws + L.hq;
   p.hs = reinterpret_cast<float*>(ws + L.hs);
-  p.y = nullptr;
-  int grid = fp8::persistent_grid(L.max_tiles * (p.N / fp8::kBN));
-  hipLaunchKernelGGL(fp8::fp8_gemm_kernel<fp8::kGateUp>, dim3(grid), dim3(fp8::kThreads), 0,
-                     stream, p);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
+  return fp8::launch<fp8::kGateUp>(p, L.max_tiles, stream);
 }
 
 int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                     const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
-  fp8::Fp8GemmArgs p;
+  fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
   p.a = ws + L.hq;
   p.as = reinterpret_cast<const float*>(ws + L.hs);
-  p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
-  p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
-  p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
   p.b = static_cast<const uint8_t*>(wt.w2);
   p.bs = static_cast<const float*>(wt.s2);
   p.K = cfg.inter;
   p.N = cfg.hidden;
-  p.topk = cfg.topk;
-  p.hq = nullptr;
-  p.hs = nullptr;
   p.y = reinterpret_cast<uint16_t*>(ws + L.y);
-  int grid = fp8::persistent_grid(L.max_tiles * (p.N / fp8::kBN));
-  hipLaunchKernelGGL(fp8::fp8_gemm_kernel<fp8::kDown>, dim3(grid), dim3(fp8::kThreads), 0,
-                     stream, p);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
+  return fp8::launch<fp8::kDown>(p, L.max_tiles, stream);
 }
 
 }  // namespace afd

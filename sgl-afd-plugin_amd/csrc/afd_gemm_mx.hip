@@ -13,17 +13,13 @@
 // (two MFMA k-steps). Both operands are stored as tile images (the LDS bytes of one stage,
 // scales included: afd_common.h), so a stage is one A block of 16.5 KiB and WN/2 B blocks of
 // 17 KiB that move HBM -> LDS with gfx950's direct global_load_lds in 1 KiB pieces, without
-// register staging, into a ring of 3 (WN = 4) or 4 (WN = 2) stages; one barrier per stage.
+// register staging, into a ring of 3 stages.
 //
 // The workgroups are persistent: grid = resident workgroups, and the number of row tiles is
-// read from device memory (the router wrote it), so no host round trip is needed. The
-// dispatcher deals workgroups to the 8 XCDs round robin (workgroup b runs on XCD b % 8), and
-// each XCD has its own L2. With enough row tiles, XCD x takes the contiguous row tiles
-// [R x / 8, R (x + 1) / 8) and its workgroups walk them row tile by row tile, column tiles
-// fastest: the 32 workgroups of an XCD then share each A image (the column tiles of a row
-// tile) and each weight slice (the ~4 row tiles of an expert) in their L2, so HBM sees every
-// A image and, but for the experts cut by an XCD boundary, every expert's weights once. Small
-// jobs use the same walk over all row tiles and the whole grid.
+// read from device memory (the router wrote it), so no host round trip is needed. They walk
+// the tiles XCD by XCD in blocks of 4 row tiles x 8 column tiles (TileWalk; with 8 column
+// tiles, row tile by row tile), so the workgroups of an XCD share activation rows and weight
+// slices in their L2.
 #include <type_traits>
 
 #include "afd_common.h"
@@ -33,8 +29,9 @@ namespace afd {
 
 enum { kGateUp = 0, kDown = 1 };
 
-// Row tiles from which the grid is split by XCD (4 row tiles = one round of an XCD's 32 CUs).
-constexpr int kXcdSplitRows = 32;
+// Tile walk blocks of 4 row tiles x 8 column tiles: a row tile's gathered activation rows are
+// shared 8 ways (measured faster than 8 x 4 blocks, whose lower HBM traffic does not pay).
+constexpr int kMxWalkRows = 4;
 
 struct MxGemmArgs {
   const uint8_t* a_img;         // down: A images [row tiles][K/128]
@@ -42,7 +39,7 @@ struct MxGemmArgs {
   const uint8_t* a_scales;      // gate_up: their UE8M0 scales [n][K/32] in stage order
   int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
   uint32_t topk_magic;          // div_magic(topk)
-  uint32_t ntn_magic;           // div_magic(N / BN), for the tile walk
+  uint32_t ncb_magic;           // div_magic(walk_col_blocks<kMxWalkRows>(N / BN)), for the tile walk
   const uint8_t* b_img;         // B images [E][N/256][K/128]
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
@@ -99,24 +96,14 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
-  const int ntn = p.N / kBN, nt256 = p.N / kImgBRows;
-  const int rows = p.num_tiles[0];
-  const int tiles = rows * ntn;
+  const int nt256 = p.N / kImgBRows;
+  const TileWalk<kMxWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic);
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   const uint32_t voff = static_cast<uint32_t>(lane) * 16;
   // this wavefront's B operand: image wn/2 of the stage, rows (wn%2)*128 + j*32 + lr
   const int bimg = wn / 2, brow = (wn % 2) * 128;
 
-  // this workgroup's walk: tiles i = first, first + stride, ... < count of row tiles from mt0
-  int mt0 = 0, count = tiles, first = blockIdx.x, stride = gridDim.x;
-  if ((gridDim.x & 7) == 0 && rows >= kXcdSplitRows) {
-    const int xcd = blockIdx.x & 7;
-    mt0 = (rows * xcd) >> 3;
-    count = (((rows * (xcd + 1)) >> 3) - mt0) * ntn;
-    first = blockIdx.x >> 3;
-    stride = gridDim.x >> 3;
-  }
   // A tile's metadata is loaded one tile ahead and decoded after the previous tile's K loop,
   // whose last wait leaves no copy in flight, so no tile starts by waiting for a load.
   // gate_up gathers its A operand from the token rows: a lane copies one 16-byte chunk of row
@@ -127,7 +114,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int s_half = (w_u / T::kImgs) & 1;
   int sp_next[T::kQP + 1], e_next = 0;
   auto load_next = [&](int ii) {
-    const int m = mt0 + static_cast<int>(div_by_magic(static_cast<uint32_t>(ii), p.ntn_magic));
+    int m, nn;
+    walk.at(ii, m, nn);
     e_next = p.tile_expert[m];
     if constexpr (MODE == kGateUp) {
 #pragma unroll
@@ -153,22 +141,23 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       s_voff = token(sp_next[T::kQP]) * (p.K / 32);
     }
   };
-  if (first < count) {
-    load_next(first);
+  int i = walk.begin();
+  if (i < walk.count) {
+    load_next(i);
     decode_next();
   }
-  for (int i = first; i < count; i += stride) {
-    // i / ntn by multiply-high (exact: i * ntn < 2^32), keeping the walk in scalar registers
-    const int iq = static_cast<int>(div_by_magic(static_cast<uint32_t>(i), p.ntn_magic));
-    const int mt = mt0 + iq, nt = i - iq * ntn;
+  for (int i_next; i < walk.count; i = i_next) {
+    int mt, nt;
+    walk.at(i, mt, nt);
+    i_next = walk.next(i);
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = e_cur;
     // down: the expert's pairs fill its first rows, padding the rest; rows below row_end are
     // real (loaded now, used by the epilogue)
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    const bool has_next = i + stride < count;
-    if (has_next) load_next(i + stride);
+    const bool has_next = i_next < walk.count;
+    if (has_next) load_next(i_next);
     const uint8_t* a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : p.a_rows;
     const uint8_t* b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
 
@@ -431,7 +420,7 @@ static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream)
   }
   const int max_tiles = max_row_tiles * (p.N / T::kBN);
   MxGemmArgs a = p;
-  a.ntn_magic = div_magic(p.N / T::kBN);
+  a.ncb_magic = div_magic(walk_col_blocks<kMxWalkRows>(p.N / T::kBN));
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
   hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);

@@ -224,9 +224,8 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   if (n > 0 && (!x || !ids || !w || !out)) return AFD_ERR_ARG;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
-  // the MX gate_up GEMM addresses token rows with 32-bit byte offsets
-  if (cfg->weight_fmt == AFD_W_MXFP4 && uint64_t(n) * cfg->hidden > 0xffffffffull)
-    return AFD_ERR_SHAPE;
+  // the gate_up GEMMs address token rows with 32-bit byte offsets
+  if (uint64_t(n) * cfg->hidden > 0xffffffffull) return AFD_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto mark = [&](int i) -> int {
     if (ev && ev[i]) AFD_CHECK_HIP(hipEventRecord(static_cast<hipEvent_t>(ev[i]), s));
