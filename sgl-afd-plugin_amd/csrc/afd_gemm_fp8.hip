@@ -25,7 +25,7 @@
 // holds every operand in the swizzled 128-byte-row layout of the MX kernel's A images (no bank
 // conflicts for the MFMA operand reads), in a ring of 3 stages. As in the MX kernel, the two
 // wavefronts of a SIMD (group 0: rows 0-63, group 1: rows 64-127) ping-pong between reading a
-// stage from LDS (and rescaling its accumulators) and running its 8 MFMAs, half a stage
+// stage from LDS and running its 8 MFMAs (and rescaling its accumulators), half a stage
 // apart. The persistent workgroups walk the tiles XCD by XCD in blocks of 8 x 4 tiles
 // (TileWalk).
 #include <type_traits>
@@ -219,19 +219,6 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     auto read_stage = [&](int kt) {
       const uint8_t* xb = lds + (kt % kStages) * kStage;
       const uint8_t* wb = xb + kWOff;
-      // the scales first: LDS reads complete in order, so the rescale at the end waits only
-      // for them and runs while the operand reads are in flight
-      const float* sx = reinterpret_cast<const float*>(xb + kXScales);
-      f.sx[0] = sx[wm * 64 + lr];
-      f.sx[1] = sx[wm * 64 + 32 + lr];
-      // block b of stage kt at group kt / 32, half b, word kt % 32
-      const float* sw = wsc + (kt >> 5) * 64 + (kt & 31);
-      if constexpr (MODE == kGateUp) {
-        f.sw[0] = sw[0];
-        f.sw[1] = sw[32];
-      } else {
-        f.sw[0] = f.sw[1] = sw[(wn >> 1) * 32];
-      }
       // row r + 32 has the swizzle of row r with chunk bit 2 flipped: its chunk c sits 4096 B
       // after row r's chunk c ^ 4, so four lane addresses serve both row blocks
       const int rx = wm * 64 + lr, rw = wn * 64 + lr;
@@ -248,24 +235,38 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
           f.w[ks][i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
       }
-      // R_{kb-1} -> R_{kb-1} * s_{kb-1} / s_kb (on the first stage the accumulators are 0)
+      const float* sx = reinterpret_cast<const float*>(xb + kXScales);
+      f.sx[0] = sx[wm * 64 + lr];
+      f.sx[1] = sx[wm * 64 + 32 + lr];
+      // block b of stage kt at group kt / 32, half b, word kt % 32
+      const float* sw = wsc + (kt >> 5) * 64 + (kt & 31);
+      if constexpr (MODE == kGateUp) {
+        f.sw[0] = sw[0];
+        f.sw[1] = sw[32];
+      } else {
+        f.sw[0] = f.sw[1] = sw[(wn >> 1) * 32];
+      }
+    };
+    // The stage's 8 MFMAs. Before its first k-step, a tile's accumulators go from R_{kb-1} to
+    // R_{kb-1} * s_{kb-1} / s_kb (stage kb's scales are in f); those 16 multiplies overlap the
+    // previous tiles' MFMAs. On the first stage the accumulators are 0 and the ratio is unused.
+    auto mma_stage = [&]() {
+      float ratio[2][2];
 #pragma unroll
       for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float ratio = (sx_prev[i2] * sw_prev[j]) * __builtin_amdgcn_rcpf(f.sx[i2] * f.sw[j]);
-#pragma unroll
-          for (int q = 0; q < 16; ++q) acc[i2][j][q] *= ratio;
-        }
-    };
-    // the stage's 8 MFMAs
-    auto mma_stage = [&]() {
+        for (int j = 0; j < 2; ++j)
+          ratio[i2][j] = (sx_prev[i2] * sw_prev[j]) * __builtin_amdgcn_rcpf(f.sx[i2] * f.sw[j]);
       static_for<2>([&](auto ksc) {
         constexpr int ks = decltype(ksc)::value;
         static_for<2>([&](auto i2c) {
           constexpr int i2 = decltype(i2c)::value;
           static_for<2>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
+            if constexpr (ks == 0) {
+#pragma unroll
+              for (int q = 0; q < 16; ++q) acc[i2][j][q] *= ratio[i2][j];
+            }
             // D[weight row][activation row]: lane x holds activation row x % 32
             acc[i2][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                 f.w[ks][j], f.x[ks][i2], acc[i2][j], 0 /*e4m3*/, 0 /*e4m3*/, 0, 127 /*x1*/, 0,
