@@ -5,7 +5,7 @@
 //                     atomics; counts are order-free).
 //   2. route_scan:    one workgroup turns the [chunks][E] histogram into per-chunk exclusive
 //                     bases, counts, offsets, block_m-padded offsets, the row-tile table and
-//                     the -1 fill of padding rows.
+//                     the -1 fill of padding rows (every step spread over the experts).
 //   3. route_scatter: each chunk walks its pairs in flat order, 256 at a time; a pair's rank
 //                     among equal keys inside its wavefront comes from 9 ballots (one per key
 //                     bit), across wavefronts from LDS counts, so the placement is the stable
@@ -19,6 +19,7 @@ constexpr int kRouteThreads = 256;
 constexpr int kScanThreads = 1024;
 constexpr int kMaxChunks = 128;
 constexpr int kKeyBits = 9;  // keys 0..256 (local expert, or num_local for "not local")
+static_assert(kMaxChunks % (kScanThreads / kMaxLocalExperts) == 0, "chunk runs of the scan");
 
 __device__ __forceinline__ int pair_key(int id, int e_lo, int num_local) {
   unsigned rel = static_cast<unsigned>(id - e_lo);
@@ -51,16 +52,23 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
   __shared__ int tot[kMaxLocalExperts];
   __shared__ int pof[kMaxLocalExperts + 1];
   const int t = threadIdx.x;
-  // Expert e's chunks are split over G = kScanThreads / num_local threads (e, g); each sums
-  // its contiguous run of chunks with independent loads, the runs' bases come from the
-  // partial sums in LDS, then each thread rewrites its chunks as exclusive bases.
+  // Expert e's chunks are split over G = kScanThreads / num_local threads (e, g); each loads
+  // its contiguous run of at most kMaxPer chunks at once (independent loads, kept in
+  // registers), the runs' bases come from the partial sums in LDS, then each thread rewrites
+  // its chunks as exclusive bases without reloading them.
+  constexpr int kMaxPer = kMaxChunks / (kScanThreads / kMaxLocalExperts);
   const int G = kScanThreads / num_local;
   const int per = (chunks + G - 1) / G;
   const int e = t % num_local, g = t / num_local;
   const bool active = g < G;
   const int c0 = active ? g * per : 0, c1 = active ? min(c0 + per, chunks) : 0;
+  int hv[kMaxPer];
   int sum = 0;
-  for (int c = c0; c < c1; ++c) sum += hist[int64_t(c) * num_local + e];
+#pragma unroll
+  for (int k = 0; k < kMaxPer; ++k) {
+    hv[k] = c0 + k < c1 ? hist[int64_t(c0 + k) * num_local + e] : 0;
+    sum += hv[k];
+  }
   part[t] = sum;
   __syncthreads();
   if (active) {
@@ -72,11 +80,10 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
       tot[e] = all;
       counts[e] = all;
     }
-    for (int c = c0; c < c1; ++c) {
-      const int64_t at = int64_t(c) * num_local + e;
-      const int h = hist[at];
-      hist[at] = run;
-      run += h;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      if (c0 + k < c1) hist[int64_t(c0 + k) * num_local + e] = run;
+      run += hv[k];
     }
   }
   __syncthreads();
@@ -119,12 +126,12 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     }
   }
   __syncthreads();
-  // row-tile table and -1 on the padding rows of every segment
-  for (int ex = 0; ex < num_local; ++ex) {
-    const int t0 = pof[ex] / block_m, t1 = pof[ex + 1] / block_m;
-    for (int i = t0 + t; i < t1; i += kScanThreads) tile_expert[i] = ex;
-    for (int r = pof[ex] + tot[ex] + t; r < pof[ex + 1]; r += kScanThreads) sorted_pairs[r] = -1;
-  }
+  // row-tile table (thread e writes expert e's tiles) and -1 on the padding rows of every
+  // segment (the G threads of expert e stride over its at most block_m - 1 padding rows)
+  if (t < num_local)
+    for (int i = pof[t] / block_m, i1 = pof[t + 1] / block_m; i < i1; ++i) tile_expert[i] = t;
+  if (active)
+    for (int r = pof[e] + tot[e] + g; r < pof[e + 1]; r += G) sorted_pairs[r] = -1;
 }
 
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
