@@ -65,6 +65,16 @@ enum afd_weight_fmt {
 /* Stream-wait conditions, as HIP's hipStreamWaitValue flags. */
 enum afd_wait_cond { AFD_WAIT_GEQ = 0, AFD_WAIT_EQ = 1, AFD_WAIT_AND = 2, AFD_WAIT_NOR = 3 };
 
+/* Activation of the gate_up output (FusedMoE's moe_runner_config.activation). */
+enum afd_activation {
+  AFD_ACT_SWIGLU = 0, /* h = silu(gate) * up ("silu") */
+  AFD_ACT_SITU = 1    /* h = L tanh(up / L) * A tanh(gate / A) * sigmoid(gate) ("situ"), with
+                         A = act_alpha (SiTU's beta, FusedMoE gemm1_alpha) and L = act_limit
+                         (its linear_beta, gemm1_clamp_limit): the function the reference's
+                         SiTU hook runs, python/sgl_asap_plugin/srt/layers/quantization/
+                         mxfp4_flashinfer_trtllm_moe.py:13-16 */
+};
+
 /* Shape of one MoE layer on one F rank. Experts [expert_lo, expert_lo + num_local) are
  * local; top-k ids are global expert ids; pairs with other ids are skipped.
  * Limits: hidden a multiple of 256, inter a multiple of 128, num_local <= 256,
@@ -76,6 +86,9 @@ typedef struct afd_moe_cfg {
   int32_t expert_lo;
   int32_t num_local;
   int32_t weight_fmt; /* enum afd_weight_fmt */
+  int32_t activation; /* enum afd_activation (0: SwiGLU) */
+  float act_alpha;    /* SiTU: A > 0 (unused for SwiGLU) */
+  float act_limit;    /* SiTU: L > 0 (unused for SwiGLU) */
 } afd_moe_cfg;
 
 /* Packed expert weights of one layer (device pointers), as afd_pack_* writes them.

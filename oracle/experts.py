@@ -42,6 +42,29 @@ def _silu(g: torch.Tensor) -> torch.Tensor:
     return g / (1.0 + torch.exp(-g))
 
 
+def situ(g: torch.Tensor, u: torch.Tensor, alpha: float, limit: float) -> torch.Tensor:
+    """SiTU of the gate and up values: ``limit * tanh(u / limit) * alpha * tanh(g / alpha) *
+    sigmoid(g)``, the function the reference's SiTU hook runs: the FlashInfer kernel computes
+    ``beta * tanh(x0 / beta) * alpha * tanh(x1 / alpha) * sigmoid(x1)`` with x0 the up and x1
+    the gate row, alpha = gemm1_alpha (SiTU's beta) and beta = gemm1_beta (its linear_beta)
+    (python/sgl_asap_plugin/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:13-16,
+    call at :67-98). fp32 torch.
+
+    Pinned (tests/test_oracle_experts.py): values against an independent math-module
+    evaluation, the limit alpha, limit -> inf (SwiGLU: silu(g) * u), odd symmetry in u,
+    |h| <= alpha * limit, and that g alone carries the sigmoid."""
+    return (limit * torch.tanh(u / limit)) * (alpha * torch.tanh(g / alpha)) * torch.sigmoid(g)
+
+
+def gate_up_act(g: torch.Tensor, u: torch.Tensor, activation: str = "silu", alpha=None, limit=None):
+    """h of the gate_up output: SwiGLU silu(g) * u (SGLang's default activation), or SiTU."""
+    if activation == "silu":
+        return _silu(g) * u
+    if activation == "situ":
+        return situ(g, u, alpha, limit)
+    raise NotImplementedError(activation)
+
+
 def quantize_act(x_f32: np.ndarray, act: str) -> np.ndarray:
     """Apply the activation quantizer and return the dequantized fp32 values."""
     if act == "mxfp8":
@@ -88,12 +111,16 @@ def moe_ffn(
     act: str = "mxfp8",
     block_m: int = 128,
     return_parts: bool = False,
+    activation: str = "silu",
+    act_alpha=None,
+    act_limit=None,
 ):
     """One job through one F rank's experts.
 
     x_bf16: torch bf16 [n, H] (CPU). ids int32 [n, k] global ids. w fp32 [n, k].
     w13_deq: fp32 [E, 2I, H] logical rows [gate; up], dequantized. w2_deq: fp32 [E, H, I].
     act: activation quantizer applied to x and to h ("mxfp8", "fp8_1x128" or "bf16").
+    activation: the gate_up activation, "silu" (SwiGLU) or "situ" with act_alpha, act_limit.
     Returns bf16 bits uint16 [n, H] (and the intermediates when return_parts).
     """
     n, hdim = x_bf16.shape
@@ -116,7 +143,7 @@ def moe_ffn(
         w13 = torch.from_numpy(w13_deq[e])
         gu = a @ w13.T
         g, u = gu[:, :inter], gu[:, inter:]
-        h = (_silu(g) * u).numpy()
+        h = gate_up_act(g, u, activation, act_alpha, act_limit).numpy()
         h_deq = quantize_act(h, act)
         h_all[lo : lo + cnt] = h_deq
         y[lo : lo + cnt] = (torch.from_numpy(h_deq) @ torch.from_numpy(w2_deq[e]).T).numpy()

@@ -122,6 +122,37 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// ---------------------------------------------------------------- gate_up activations
+// h from the gate and up values of one intermediate column (afd_activation). tanh(x) is
+// 1 - 2 / (1 + e^{2x}): one exponential and one reciprocal, and exactly +-1 once e^{2x}
+// overflows or vanishes.
+__device__ __forceinline__ float act_swiglu(float g, float u) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+__device__ __forceinline__ float tanh_exp(float x) {
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * x));
+}
+// SiTU: L tanh(u / L) * A tanh(g / A) * sigmoid(g)
+__device__ __forceinline__ float act_situ(float g, float u, float a, float inv_a, float l,
+                                          float inv_l) {
+  return (l * tanh_exp(u * inv_l)) * (a * tanh_exp(g * inv_a)) *
+         __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+// the activation parameters a gate_up GEMM takes from afd_moe_cfg
+struct ActParams {
+  int act;  // enum afd_activation
+  float a, inv_a, l, inv_l;
+};
+inline ActParams act_params(const afd_moe_cfg& cfg) {
+  ActParams p;
+  p.act = cfg.activation;
+  p.a = cfg.act_alpha;
+  p.l = cfg.act_limit;
+  p.inv_a = cfg.activation == AFD_ACT_SITU ? 1.0f / cfg.act_alpha : 0.0f;
+  p.inv_l = cfg.activation == AFD_ACT_SITU ? 1.0f / cfg.act_limit : 0.0f;
+  return p;
+}
+
 // Division by a launch constant d >= 1 without the division sequence:
 // n / d == __umulhi(n, ceil(2^32 / d)) for every n with n * d < 2^32 (the product overshoots
 // n / d by n * (ceil(2^32/d) * d - 2^32) / 2^32 / d < n / 2^32 < 1/d, which never reaches

@@ -36,7 +36,9 @@
 namespace afd {
 namespace fp8 {
 
-enum { kGateUp = 0, kDown = 1 };
+// gate_up with SwiGLU or with SiTU (separate kernels: SiTU's longer epilogue would raise
+// the register pressure of the SwiGLU kernel), down
+enum { kGateUp = 0, kDown = 1, kGateUpSitu = 2 };
 
 // Tile walk blocks of 8 row tiles x 4 column tiles: a 1 MiB weight slice is shared 8 ways
 // (column-tile-fastest walks fetch ~3x more from beyond L2).
@@ -85,6 +87,7 @@ struct Fp8GemmArgs {
   const int32_t* padded_offsets;  // [E + 1]
   const int32_t* counts;          // [E]
   int K, N;
+  ActParams act;  // gate_up: the activation
   uint8_t* hq;  // gate_up out: e4m3 [np][N/2]
   float* hs;    // gate_up out: fp32 [np][N/256]
   uint16_t* y;  // down out: bf16 [np][N]
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     int m, nn;
     walk.at(ii, m, nn);
     e_next = p.tile_expert[m];
-    if constexpr (MODE == kGateUp) {
+    if constexpr (MODE != kDown) {
 #pragma unroll
       for (int q = 0; q < kQX; ++q)
         sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * kQX + q) + (lane >> 3)];
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   s_voff = static_cast<uint32_t>(s_row * KT * 4);
   auto decode_next = [&]() {
     e_cur = __builtin_amdgcn_readfirstlane(e_next);
-    if constexpr (MODE == kGateUp) {
+    if constexpr (MODE != kDown) {
       // padding rows (-1) read token 0; their results are never used
       auto token = [&](int sp) {
         return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
@@ -172,13 +175,13 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     const bool has_next = i_next < walk.count;
     if (has_next) load_next(i_next);
 
-    const uint8_t* x_tile = MODE == kGateUp ? p.a : p.a + int64_t(m0) * p.K;
-    const float* s_tile = MODE == kGateUp ? p.as : p.as + int64_t(m0) * KT;
+    const uint8_t* x_tile = MODE != kDown ? p.a : p.a + int64_t(m0) * p.K;
+    const float* s_tile = MODE != kDown ? p.as : p.as + int64_t(m0) * KT;
     const uint8_t* w_tile = p.b + (e * p.N + n0) * int64_t(p.K);
     // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
     // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
-    const int blk0 = MODE == kGateUp ? n0 / 256 : n0 / 128;
-    const int blk1 = MODE == kGateUp ? nblk / 2 + n0 / 256 : n0 / 128 + 1;
+    const int blk0 = MODE != kDown ? n0 / 256 : n0 / 128;
+    const int blk1 = MODE != kDown ? nblk / 2 + n0 / 256 : n0 / 128 + 1;
 
     auto issue_piece = [&](int kt, auto qc) {
       constexpr int q = decltype(qc)::value;
@@ -240,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
       f.sx[1] = sx[wm * 64 + 32 + lr];
       // block b of stage kt at group kt / 32, half b, word kt % 32
       const float* sw = wsc + (kt >> 5) * 64 + (kt & 31);
-      if constexpr (MODE == kGateUp) {
+      if constexpr (MODE != kDown) {
         f.sw[0] = sw[0];
         f.sw[1] = sw[32];
       } else {
@@ -344,24 +347,30 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
 
     // accumulator q of tile (i, j): activation row 64 g + 32 i + lane % 32, output column
     // 64 c + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
-    if constexpr (MODE == kGateUp) {
+    if constexpr (MODE != kDown) {
       // SwiGLU in registers: column tiles j = 0, 1 are the gate and up halves of one 64-row
       // group of interleaved W13, i.e. the same 32 intermediate columns.
       float* hl = reinterpret_cast<float*>(lds);
+      auto stage_h = [&](auto fn) {
 #pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2)
+        for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const int row = wm * 64 + i2 * 32 + lr;
-          const int col = wn * 32 + q4 * 8 + lk * 4;
-          v4f hv;
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int row = wm * 64 + i2 * 32 + lr;
+            const int col = wn * 32 + q4 * 8 + lk * 4;
+            v4f hv;
 #pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const float g = acc[i2][0][q4 * 4 + e4], u = acc[i2][1][q4 * 4 + e4];
-            hv[e4] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+            for (int e4 = 0; e4 < 4; ++e4)
+              hv[e4] = fn(acc[i2][0][q4 * 4 + e4], acc[i2][1][q4 * 4 + e4]);
+            *reinterpret_cast<v4f*>(hl + row * kHStride + col) = hv;
           }
-          *reinterpret_cast<v4f*>(hl + row * kHStride + col) = hv;
-        }
+      };
+      if constexpr (MODE == kGateUpSitu)
+        stage_h([&](float g, float u) {
+          return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+        });
+      else
+        stage_h([](float g, float u) { return act_swiglu(g, u); });
       __syncthreads();
       // the tile's 128 h columns are one 1x128 group per row: 4 lanes per row, 32 values each
       const int inter = p.N / 2;
@@ -447,6 +456,7 @@ static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws
   Fp8GemmArgs p;
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
+  p.act = act_params(cfg);
   p.ncb_magic = 0;
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
@@ -473,7 +483,8 @@ int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uin
   p.N = 2 * cfg.inter;
   p.hq = ws + L.hq;
   p.hs = reinterpret_cast<float*>(ws + L.hs);
-  return fp8::launch<fp8::kGateUp>(p, L.max_tiles, stream);
+  return cfg.activation == AFD_ACT_SITU ? fp8::launch<fp8::kGateUpSitu>(p, L.max_tiles, stream)
+                                         : fp8::launch<fp8::kGateUp>(p, L.max_tiles, stream);
 }
 
 int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,

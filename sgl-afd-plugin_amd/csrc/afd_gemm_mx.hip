@@ -27,7 +27,9 @@
 
 namespace afd {
 
-enum { kGateUp = 0, kDown = 1 };
+// gate_up with SwiGLU or with SiTU (separate kernels: SiTU's longer epilogue would raise
+// the register pressure of the SwiGLU kernel), down
+enum { kGateUp = 0, kDown = 1, kGateUpSitu = 2 };
 
 // Tile walk blocks of 4 row tiles x 8 column tiles: a row tile's gathered activation rows are
 // shared 8 ways (measured faster than 8 x 4 blocks, whose lower HBM traffic does not pay).
@@ -48,6 +50,7 @@ struct MxGemmArgs {
   const int32_t* counts;          // [E] pairs of each expert (its first rows)
   int K, N;
   uint8_t* h_img;  // gate_up out: the down GEMM's A images [row tiles][N/256]
+  ActParams act;   // gate_up: the activation
   uint16_t* y;     // down out: bf16 [np][N]
 };
 
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     int m, nn;
     walk.at(ii, m, nn);
     e_next = p.tile_expert[m];
-    if constexpr (MODE == kGateUp) {
+    if constexpr (MODE != kDown) {
 #pragma unroll
       for (int q = 0; q < T::kQP; ++q)
         sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * T::kQP + q) + (lane >> 3)];
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   uint32_t a_voff[T::kQP] = {}, s_voff = 0;
   auto decode_next = [&]() {
     e_cur = __builtin_amdgcn_readfirstlane(e_next);
-    if constexpr (MODE == kGateUp) {
+    if constexpr (MODE != kDown) {
       auto token = [&](int sp) {
         return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
       };
@@ -179,14 +182,14 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       constexpr int q = decltype(qc)::value;
       const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
       if constexpr (q == T::kImgs * T::kQP) {
-        if (MODE == kGateUp && img16 == 0)  // 64 rows' scale words, gathered
+        if (MODE != kDown && img16 == 0)  // 64 rows' scale words, gathered
           lds_dma4(st + kImgData + s_half * 256, p.a_scales + int64_t(kt) * 4, s_voff);
         else
           lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
       } else {
         constexpr int img = q / T::kQP;
         const int off = (w_u * T::kQP + q % T::kQP) * 1024;
-        if constexpr (img == 0 && MODE == kGateUp)
+        if constexpr (img == 0 && MODE != kDown)
           lds_dma16(st + off, p.a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
         else if constexpr (img == 0)
           lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
@@ -322,21 +325,28 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     __syncthreads();  // the epilogue reuses the stage buffers
     if (has_next) decode_next();
 
-    if (MODE == kGateUp) {
+    if (MODE != kDown) {
       // SwiGLU in registers: column subtiles (0,1) and (2,3) are the (gate, up) halves of
       // one 64-row group of interleaved W13, i.e. the same 32 intermediate columns.
       float* hl = reinterpret_cast<float*>(lds);
+      auto stage_h = [&](auto fn) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+          for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
-            int col = wn * 64 + jj * 32 + lr;
-            float g = acc[i][2 * jj][q], u = acc[i][2 * jj + 1][q];
-            hl[row * T::kHStride + col] = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-          }
+            for (int q = 0; q < 16; ++q) {
+              int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
+              int col = wn * 64 + jj * 32 + lr;
+              hl[row * T::kHStride + col] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
+            }
+      };
+      if constexpr (MODE == kGateUpSitu)
+        stage_h([&](float g, float u) {
+          return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+        });
+      else
+        stage_h([](float g, float u) { return act_swiglu(g, u); });
       __syncthreads();
       // the 128 x (kBN/2) h tile is WN/2 K stages of the down GEMM's A operand, starting at
       // stage n0/256 of row tile mt
@@ -443,6 +453,7 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.a_scales = ws + L.xs;
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
+  p.act = act_params(cfg);
   p.b_img = static_cast<const uint8_t*>(wt.w13);
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
@@ -453,13 +464,15 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.N = 2 * cfg.inter;
   p.h_img = ws + L.hq;
   p.y = nullptr;
-  return launch_mx_any<kGateUp>(p, L.max_tiles, stream);
+  return cfg.activation == AFD_ACT_SITU ? launch_mx_any<kGateUpSitu>(p, L.max_tiles, stream)
+                                         : launch_mx_any<kGateUp>(p, L.max_tiles, stream);
 }
 
 int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                    const afd_ws_layout& L, int32_t n, hipStream_t stream) {
   (void)n;
   MxGemmArgs p;
+  p.act = act_params(cfg);
   p.a_img = ws + L.hq;
   p.a_rows = nullptr;
   p.a_scales = nullptr;

@@ -5,6 +5,7 @@
 //
 // finalize and combine are HBM-bound gathers with fixed summation order, so their results
 // are reproducible bit for bit (no atomics).
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -148,6 +149,13 @@ static int check_cfg(const afd_moe_cfg* cfg) {
     return AFD_ERR_SHAPE;
   if (cfg->weight_fmt != AFD_W_MXFP4 && cfg->weight_fmt != AFD_W_FP8_BLOCK)
     return AFD_ERR_UNSUPPORTED;
+  if (cfg->activation != AFD_ACT_SWIGLU && cfg->activation != AFD_ACT_SITU)
+    return AFD_ERR_UNSUPPORTED;
+  // SiTU's two constants are positive and finite (the reference raises ValueError without them)
+  if (cfg->activation == AFD_ACT_SITU &&
+      !(cfg->act_alpha > 0.0f && cfg->act_alpha < INFINITY && cfg->act_limit > 0.0f &&
+        cfg->act_limit < INFINITY))
+    return AFD_ERR_ARG;
   return AFD_OK;
 }
 

@@ -25,6 +25,9 @@ AFD_ERR_WORKSPACE = -5
 AFD_W_MXFP4 = 1
 AFD_W_FP8_BLOCK = 2
 
+AFD_ACT_SWIGLU = 0
+AFD_ACT_SITU = 1
+
 AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 
 # Every entry point include/afd.h declares; tests check the library exports all of them.
@@ -66,6 +69,9 @@ class AfdMoeCfg(ctypes.Structure):
         ("expert_lo", ctypes.c_int32),
         ("num_local", ctypes.c_int32),
         ("weight_fmt", ctypes.c_int32),
+        ("activation", ctypes.c_int32),
+        ("act_alpha", ctypes.c_float),
+        ("act_limit", ctypes.c_float),
     ]
 
 

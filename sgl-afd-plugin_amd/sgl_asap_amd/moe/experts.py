@@ -109,9 +109,35 @@ def pack_fp8_block_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> 
     return ExpertWeights("fp8_block", e, h, inter, q13, s13, q2, s2)
 
 
-def moe_cfg(weights: ExpertWeights, top_k: int, expert_lo: int) -> _lib.AfdMoeCfg:
+ACTIVATIONS = {"silu": _lib.AFD_ACT_SWIGLU, "situ": _lib.AFD_ACT_SITU}
+
+
+def moe_cfg(
+    weights: ExpertWeights,
+    top_k: int,
+    expert_lo: int,
+    activation: str = "silu",
+    gemm1_alpha: Optional[float] = None,
+    gemm1_clamp_limit: Optional[float] = None,
+) -> _lib.AfdMoeCfg:
+    """The C config of a layer. ``activation`` is FusedMoE's ("silu": SwiGLU; "situ": SiTU
+    with ``gemm1_alpha`` = its beta and ``gemm1_clamp_limit`` = its linear_beta, as the
+    reference's ERNIE 5.5 experts pass them, P/srt/models/ernie55.py:43-55)."""
+    if activation not in ACTIVATIONS:
+        raise NotImplementedError(f"activation {activation!r} (supported: {sorted(ACTIVATIONS)})")
+    alpha = limit = 0.0
+    if activation == "situ":
+        if gemm1_alpha is None or gemm1_clamp_limit is None:
+            # the reference's message (P/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:110-113)
+            raise ValueError(
+                "SiTU needs the layer's gemm1_alpha (beta) and gemm1_clamp_limit (linear_beta)"
+            )
+        alpha, limit = float(gemm1_alpha), float(gemm1_clamp_limit)
+        if not (0.0 < alpha < float("inf") and 0.0 < limit < float("inf")):
+            raise ValueError(f"SiTU constants must be positive and finite, got {alpha}, {limit}")
     return _lib.AfdMoeCfg(
-        weights.hidden, weights.inter, top_k, expert_lo, weights.num_local, WEIGHT_FORMATS[weights.fmt]
+        weights.hidden, weights.inter, top_k, expert_lo, weights.num_local, WEIGHT_FORMATS[weights.fmt],
+        ACTIVATIONS[activation], alpha, limit,
     )
 
 
@@ -139,6 +165,9 @@ class AfdExperts(torch.nn.Module):
         local: range,
         weights: ExpertWeights,
         n_max: int = 16384,
+        activation: str = "silu",
+        gemm1_alpha: Optional[float] = None,
+        gemm1_clamp_limit: Optional[float] = None,
     ):
         super().__init__()
         if len(local) != weights.num_local:
@@ -150,7 +179,8 @@ class AfdExperts(torch.nn.Module):
         self.hidden_size, self.intermediate_size = weights.hidden, weights.inter
         self.weights = weights
         self.n_max = n_max
-        self.cfg = moe_cfg(weights, top_k, local.start)
+        self.activation = activation
+        self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit)
         self.layout = workspace_layout(self.cfg, n_max)
         self._ws: Dict[int, torch.Tensor] = {}
         self._wstruct = weights.as_struct()

@@ -66,9 +66,33 @@ def test_bad_configs_rejected_on_host():
         _lib.AfdMoeCfg(4096, 2048, 0, 0, 64, 1),  # topk 0
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 512, 1),  # too many local experts
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 7),  # unknown format
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, 5),  # unknown activation
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 0.0, 1.0),  # SiTU without beta
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 1.0, float("inf")),
     ]
     for cfg in bad:
         assert _lib.lib().afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) != 0
     good = _lib.AfdMoeCfg(256, 128, 2, 0, 8, 1)
     assert _lib.lib().afd_workspace_layout(ctypes.byref(good), 1 << 17, ctypes.byref(out)) != 0
     assert _lib.lib().afd_workspace_layout(ctypes.byref(good), (1 << 17) - 1, ctypes.byref(out)) == 0
+
+
+def test_situ_config_accepted():
+    out = _lib.AfdWsLayout()
+    ok = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 2.0, 3.0)
+    assert _lib.lib().afd_workspace_layout(ctypes.byref(ok), 16, ctypes.byref(out)) == 0
+
+
+def test_python_activation_arguments():
+    """AfdExperts' activation arguments follow FusedMoE's (activation, gemm1_alpha,
+    gemm1_clamp_limit) and fail as the reference does."""
+    from sgl_asap_amd.moe.experts import ExpertWeights, moe_cfg
+
+    wts = ExpertWeights("mxfp4", 4, 256, 128, None, None, None, None)
+    assert moe_cfg(wts, 2, 0).activation == _lib.AFD_ACT_SWIGLU
+    c = moe_cfg(wts, 2, 0, "situ", 2.0, 3.0)
+    assert (c.activation, c.act_alpha, c.act_limit) == (_lib.AFD_ACT_SITU, 2.0, 3.0)
+    with pytest.raises(ValueError):
+        moe_cfg(wts, 2, 0, "situ", 2.0, None)
+    with pytest.raises(NotImplementedError):
+        moe_cfg(wts, 2, 0, "gelu")

@@ -35,8 +35,9 @@ def deq_weights(w13, w2, fmt):
     return F.fp8_block_dequantize_2d(c13, s13), F.fp8_block_dequantize_2d(c2, s2)
 
 
-def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=None):
-    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed}")
+def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=None, situ=None):
+    """situ: None for SwiGLU, else SiTU's (gemm1_alpha, gemm1_clamp_limit)."""
+    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed} situ={situ}")
     gen = W.generator("cpu", seed)
     x = W.tokens(n, hidden, gen, "cpu")
     if zipf is None:
@@ -47,12 +48,14 @@ def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=
     pack = pack_mxfp4_experts if fmt == "mxfp4" else pack_fp8_block_experts
     weights = pack(w13, w2, device=dev())
     local = range(e_lo, e_lo + num_local)
-    experts = AfdExperts(num_experts, k, 0, local, weights, n_max=max(n, 1))
+    act_kw = {} if situ is None else dict(activation="situ", gemm1_alpha=situ[0], gemm1_clamp_limit=situ[1])
+    experts = AfdExperts(num_experts, k, 0, local, weights, n_max=max(n, 1), **act_kw)
     out = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
     w13d, w2d = deq_weights(w13, w2, fmt)
     act = "mxfp8" if fmt == "mxfp4" else "fp8_1x128"
-    ref, parts = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13d, w2d, e_lo, act=act, return_parts=True)
+    oact = {} if situ is None else dict(activation="situ", act_alpha=situ[0], act_limit=situ[1])
+    ref, parts = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13d, w2d, e_lo, act=act, return_parts=True, **oact)
     return experts, out, ref, parts, (x, ids, w)
 
 
@@ -130,3 +133,19 @@ def test_repeat_call_is_deterministic():
     again = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
     assert np.array_equal(bits16(out), bits16(again))
+
+
+@pytest.mark.parametrize(
+    "fmt,alpha,limit,seed",
+    [
+        ("mxfp4", 2.0, 3.0, 21),
+        ("mxfp4", 0.5, 0.25, 22),  # both tanh branches mostly saturated
+        ("fp8_block", 2.0, 3.0, 23),
+    ],
+)
+def test_situ_layers(fmt, alpha, limit, seed):
+    """SiTU (ERNIE 5.5's activation) through both weight formats against the oracle."""
+    experts, out, ref, parts, (x, ids, w) = run_case(
+        1024, 512, 32, 0, 16, 8, 384, fmt, seed, situ=(alpha, limit)
+    )
+    assert_close(out, ref, ids.numpy(), range(0, 16))

@@ -3,6 +3,8 @@ MLP written independently of the oracle's routed formulation, exact special case
 local pair, zero weights, repeated tokens, power-of-two weight scaling), and the
 finalize / combine formulas against torch fp32 arithmetic, bit for bit."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -131,3 +133,48 @@ def test_combine_matches_torch(num_parts):
     assert np.array_equal(OX.combine([bits(p) for p in parts]), bits(routed))
     want = (routed.float() + shared.float()).to(torch.bfloat16)
     assert np.array_equal(OX.combine([bits(p) for p in parts], bits(shared)), bits(want))
+
+
+# ---------------------------------------------------------------- SiTU
+def _situ_math(g, u, a, l):
+    """The SiTU formula evaluated independently, in float64 with the math module."""
+    sig = 1.0 / (1.0 + math.exp(-g))
+    return l * math.tanh(u / l) * a * math.tanh(g / a) * sig
+
+
+def test_situ_matches_an_independent_evaluation():
+    gen = torch.Generator().manual_seed(5)
+    g = torch.randn(200, generator=gen) * 3
+    u = torch.randn(200, generator=gen) * 3
+    for a, l in ((2.0, 3.0), (0.5, 0.25), (7.0, 1.0)):
+        got = OX.situ(g, u, a, l).double().numpy()
+        want = np.array([_situ_math(float(gi), float(ui), a, l) for gi, ui in zip(g, u)])
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * a * l)
+
+
+def test_situ_tends_to_swiglu_for_large_constants():
+    """tanh(x / c) * c -> x as c grows, so SiTU -> u * g * sigmoid(g) = silu(g) * u."""
+    gen = torch.Generator().manual_seed(6)
+    g, u = torch.randn(500, generator=gen), torch.randn(500, generator=gen)
+    big = OX.situ(g, u, 1e4, 1e4).double()
+    swiglu = (g / (1 + torch.exp(-g)) * u).double()
+    assert torch.allclose(big, swiglu, rtol=1e-5, atol=1e-7)
+
+
+def test_situ_symmetries_and_bound():
+    gen = torch.Generator().manual_seed(7)
+    g, u = torch.randn(300, generator=gen) * 4, torch.randn(300, generator=gen) * 4
+    a, l = 1.5, 0.75
+    h = OX.situ(g, u, a, l)
+    assert torch.equal(OX.situ(g, -u, a, l), -h)  # odd in the up value
+    assert bool((h.abs() <= a * l).all())  # |tanh| <= 1 and sigmoid <= 1
+    # the gate carries the sigmoid: swapping gate and up changes the value
+    assert not torch.allclose(OX.situ(u, g, a, l), h, atol=1e-3)
+
+
+def test_situ_layer_reduces_to_swiglu_layer():
+    """The whole expert call with SiTU and huge constants equals the SwiGLU call."""
+    x, ids, w, w13, w2 = setup(24, 2, 8, 0, 8, seed=9)
+    a = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16", activation="situ", act_alpha=1e5, act_limit=1e5)
+    b = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16")
+    assert rel_l2(F.bf16_to_f32(a).astype(np.float64), F.bf16_to_f32(b).astype(np.float64)) < 1e-3
