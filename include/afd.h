@@ -3,8 +3,11 @@
  * disaggregated MoE deployment.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t (as void*), only
- * enqueues work on that stream (no host synchronisation, no allocation, no global mutable
- * state besides the thread-local last HIP error) and returns 0 or a negative afd_status.
+ * enqueues work on that stream (no host synchronisation, no device memory allocation) and
+ * returns 0 or a negative afd_status. Global state: the thread-local last HIP error, and
+ * one side stream with two events per device, created on the first afd_moe_ffn call, on
+ * which the call runs its activation quantizer forked from and joined back to the caller's
+ * stream (event record / stream wait, so graph capture and stream order are unaffected).
  *
  * Reference interfaces each group replaces (paths relative to the reference repository,
  * P = python/sgl_asap_plugin):
