@@ -76,20 +76,20 @@ struct MxTile {
   static constexpr int kQP = 16 / kWaves;
   static constexpr int kPieces = kImgs * kQP + 1;
   static_assert(kWaves >= 2 * kImgs, "a scale piece per image, two for a gathered A");
-  static constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
-  static constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
-  static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
-  static_assert(kBM * kHStride * 4 <= kLds, "gate_up epilogue tile must fit the stages");
+  static constexpr int kYStride = kBN + 8;  // bf16 stride of the down epilogue tile
   static_assert(kBM * kYStride * 2 <= kLds, "down epilogue tile must fit the stages");
+  static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
   static_assert(kLds <= 160 * 1024, "LDS of one CU");
   static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
 };
 
 // The scaled MFMA with a 4-dword (e2m1) B operand. The clang builtin takes 8 dwords for every
 // operand format; the intrinsic's B operand type follows the format, and e2m1 needs only 4.
-extern "C" __device__ v16f mfma_scale_f8_f4(v8i a, v4i b, v16f c, int cbsz, int blgp,
+// The kernels pass the e2m1 weights as the first operand and the e4m3 activations as the
+// second (D = W X^T), so a lane's accumulators belong to one activation row.
+extern "C" __device__ v16f mfma_scale_f4_f8(v4i a, v8i b, v16f c, int cbsz, int blgp,
                                             int opsel_a, int scale_a, int opsel_b, int scale_b)
-    __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v8i32.v4i32");
+    __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v8i32");
 
 template <int MODE, int WN>
 __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArgs p) {
@@ -144,10 +144,68 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       s_voff = token(sp_next[T::kQP]) * (p.K / 32);
     }
   };
+  // The tile whose stages the copies below fetch. gate_up issues the next tile's first two
+  // stages right after its own K loop: its epilogue works from registers, so those copies
+  // land while it runs. down's epilogue stages its output through the LDS ring, so it issues
+  // them at the start of the tile.
+  constexpr bool kEarlyStart = MODE != kDown;
+  const uint8_t* a_tile = nullptr;
+  const uint8_t* b_tile = nullptr;
+  const uint8_t* src16 = nullptr;
+  // this wavefront's copies of stage kt into ring slot kt % 3: piece c of image c / 17 (0 = A,
+  // its 17th piece being the scales plus the 512 B that follow them in memory). Scalar
+  // address arithmetic only, so the issuing code has no branches.
+  // Piece q of this wavefront: for q < kImgs * kQP, piece w * kQP + q % kQP of image
+  // q / kQP (0 = A, then the B images). The last, q = kImgs * kQP, is a scale piece:
+  // wavefront w < 2 kImgs copies that of image w % kImgs (of the gathered A of gate_up, half
+  // w / kImgs: 64 rows' words), later wavefronts repeat a B image's (the same bytes to the
+  // same place), so the costly gathered scale copy is issued once per half. Only the last
+  // piece depends on the wavefront beyond an offset, so it is resolved once per tile; the
+  // others are address arithmetic.
+  const int img16 = w_u < 2 * T::kImgs ? w_u % T::kImgs : 1 + (w_u - 2 * T::kImgs) % T::kBImgs;
+  const int step16 = img16 == 0 ? kImgA : kImgB;
+  const uint32_t dst16 = img16 == 0 ? kImgData : T::kLdsA + (img16 - 1) * kImgB + kImgData;
+  auto copy_tile = [&](int mt, int nt, int64_t e) {
+    a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : p.a_rows;
+    b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
+    src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
+  };
+  auto issue_piece = [&](int kt, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+    if constexpr (q == T::kImgs * T::kQP) {
+      if (MODE != kDown && img16 == 0)  // 64 rows' scale words, gathered
+        lds_dma4(st + kImgData + s_half * 256, p.a_scales + int64_t(kt) * 4, s_voff);
+      else
+        lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
+    } else {
+      constexpr int img = q / T::kQP;
+      const int off = (w_u * T::kQP + q % T::kQP) * 1024;
+      if constexpr (img == 0 && MODE != kDown)
+        lds_dma16(st + off, p.a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
+      else if constexpr (img == 0)
+        lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
+      else
+        lds_dma16(st + T::kLdsA + (img - 1) * kImgB + off,
+                  b_tile + (int64_t(img - 1) * KT + kt) * kImgB + off, voff);
+    }
+  };
+  auto issue = [&](int kt) {
+    static_for<T::kPieces>([&](auto q) { issue_piece(kt, q); });
+  };
+  const int last = KT - 1;
+
   int i = walk.begin();
   if (i < walk.count) {
     load_next(i);
     decode_next();
+    if constexpr (kEarlyStart) {
+      int mt, nt;
+      walk.at(i, mt, nt);
+      copy_tile(mt, nt, e_cur);
+      issue(0);
+      issue(min(1, last));
+    }
   }
   for (int i_next; i < walk.count; i = i_next) {
     int mt, nt;
@@ -161,46 +219,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
     const bool has_next = i_next < walk.count;
     if (has_next) load_next(i_next);
-    const uint8_t* a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : p.a_rows;
-    const uint8_t* b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
-
-    // this wavefront's copies of stage kt into ring slot kt % 3: piece c of image c / 17 (0 = A,
-    // its 17th piece being the scales plus the 512 B that follow them in memory). Scalar
-    // address arithmetic only, so the issuing code has no branches.
-    // Piece q of this wavefront: for q < kImgs * kQP, piece w * kQP + q % kQP of image
-    // q / kQP (0 = A, then the B images). The last, q = kImgs * kQP, is a scale piece:
-    // wavefront w < 2 kImgs copies that of image w % kImgs (of the gathered A of gate_up, half
-    // w / kImgs: 64 rows' words), later wavefronts repeat a B image's (the same bytes to the
-    // same place), so the costly gathered scale copy is issued once per half. Only the last
-    // piece depends on the wavefront beyond an offset, so it is resolved once per tile; the
-    // others are address arithmetic.
-    const int img16 = w_u < 2 * T::kImgs ? w_u % T::kImgs : 1 + (w_u - 2 * T::kImgs) % T::kBImgs;
-    const uint8_t* src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
-    const int step16 = img16 == 0 ? kImgA : kImgB;
-    const uint32_t dst16 = img16 == 0 ? kImgData : T::kLdsA + (img16 - 1) * kImgB + kImgData;
-    auto issue_piece = [&](int kt, auto qc) {
-      constexpr int q = decltype(qc)::value;
-      const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
-      if constexpr (q == T::kImgs * T::kQP) {
-        if (MODE != kDown && img16 == 0)  // 64 rows' scale words, gathered
-          lds_dma4(st + kImgData + s_half * 256, p.a_scales + int64_t(kt) * 4, s_voff);
-        else
-          lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
-      } else {
-        constexpr int img = q / T::kQP;
-        const int off = (w_u * T::kQP + q % T::kQP) * 1024;
-        if constexpr (img == 0 && MODE != kDown)
-          lds_dma16(st + off, p.a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
-        else if constexpr (img == 0)
-          lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
-        else
-          lds_dma16(st + T::kLdsA + (img - 1) * kImgB + off,
-                    b_tile + (int64_t(img - 1) * KT + kt) * kImgB + off, voff);
-      }
-    };
-    auto issue = [&](int kt) {
-      static_for<T::kPieces>([&](auto q) { issue_piece(kt, q); });
-    };
+    if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
     v16f acc[2][4];
 #pragma unroll
@@ -257,10 +276,10 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
           constexpr int i2 = decltype(i2c)::value;
           static_for<4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            // op_sel ks: byte ks of the lane's scale half-word
-            acc[i2][j] = mfma_scale_f8_f4(f.a[ks][i2], f.b[ks][j], acc[i2][j], 0 /*A e4m3*/,
-                                          4 /*B e2m1*/, ks, static_cast<int>(f.sa[i2]), ks,
-                                          static_cast<int>(f.sb[j]));
+            // D[weight row][activation row]; op_sel ks: byte ks of the lane's scale half-word
+            acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
+                                          0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
+                                          static_cast<int>(f.sa[i2]));
             if constexpr (Copy) {
               constexpr int m = ks * 8 + i2 * 4 + j;
               if constexpr ((m & 1) && m / 2 < T::kPieces)
@@ -284,11 +303,13 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     // bytes). Both groups wait for their own pieces of stage kt+1 in the phase before the
     // barrier after which group 0 reads stage kt+1: group 0 after its MFMAs of stage kt,
     // group 1 after its reads of stage kt.
-    const int last = KT - 1;
-    // epilogue stores of the previous tile may still be in flight: they only delay the
-    // counted waits below (vmcnt counts stores too), never satisfy them early
-    issue(0);
-    issue(min(1, last));
+    // epilogue stores of the previous tile may still be in flight (with kEarlyStart they were
+    // issued after this tile's first copies): they only make the counted waits stricter
+    // (vmcnt counts stores too; loads complete in order among themselves), never early
+    if constexpr (!kEarlyStart) {
+      issue(0);
+      issue(min(1, last));
+    }
     wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
     __syncthreads();
     if (wm == 0) {
@@ -321,92 +342,101 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         __syncthreads();
       }
     }
-    wait_vmcnt<0>();  // no copy may land in the stage buffers the epilogue reuses
-    __syncthreads();  // the epilogue reuses the stage buffers
-    if (has_next) decode_next();
+    wait_vmcnt<0>();  // every copy of this tile landed
+    __syncthreads();  // and every wavefront is done reading the stages
+    if (has_next) {
+      decode_next();
+      if constexpr (kEarlyStart) {
+        int mt2, nt2;
+        walk.at(i_next, mt2, nt2);
+        copy_tile(mt2, nt2, e_cur);
+        issue(0);
+        issue(min(1, last));
+      }
+    }
 
-    if (MODE != kDown) {
-      // SwiGLU in registers: column subtiles (0,1) and (2,3) are the (gate, up) halves of
-      // one 64-row group of interleaved W13, i.e. the same 32 intermediate columns.
-      float* hl = reinterpret_cast<float*>(lds);
-      auto stage_h = [&](auto fn) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
+    // Accumulator q of tile (i, j): activation row 64 wm + 32 i + lane % 32, output column
+    // 128 wn + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4.
+    if constexpr (MODE != kDown) {
+      // Column tiles j = 2 jj and 2 jj + 1 are the gate and up halves of one 64-row group of
+      // interleaved W13, i.e. the same 32 intermediate columns: one MX block of h per (i, jj),
+      // 16 values in this lane and 16 in lane ^ 32. The block's scale needs one exchange; then
+      // lane half lk assembles 16-byte chunk lk of the block (h columns 16 lk .. 16 lk + 15)
+      // with a second, and stores it into the down GEMM's A image (stage n0 / 256 + block / 4
+      // of row tile mt).
+      const int kt_down = p.N / kImgBRows;  // K stages of the down GEMM (I / 128)
+      auto quant_store = [&](auto fn) {
+        static_for<2>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          static_for<2>([&](auto jjc) {
+            constexpr int jj = decltype(jjc)::value;
+            float h[16];
+            float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-              int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);
-              int col = wn * 64 + jj * 32 + lr;
-              hl[row * T::kHStride + col] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
+              h[q] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
+              amax = fmaxf(amax, fabsf(h[q]));
             }
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const uint32_t code = mx_scale_code(amax, 8);
+            const float inv = mx_inv_scale(code);
+            uint32_t d[4];  // h columns 8 q4 + 4 lk .. + 3
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              d[q4] = pk4_e4m3(h[4 * q4] * inv, h[4 * q4 + 1] * inv, h[4 * q4 + 2] * inv,
+                               h[4 * q4 + 3] * inv);
+            // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
+            // 16-31 (the partner's d2, d3 and its own)
+            const uint32_t p0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[0] : d[2]), 32));
+            const uint32_t p1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[1] : d[3]), 32));
+            v4i chunk;
+            chunk[0] = static_cast<int>(lk ? p0 : d[0]);
+            chunk[1] = static_cast<int>(lk ? d[2] : p0);
+            chunk[2] = static_cast<int>(lk ? p1 : d[1]);
+            chunk[3] = static_cast<int>(lk ? d[3] : p1);
+            const int row = wm * 64 + i * 32 + lr;
+            const int hblk = wn * 2 + jj;  // MX block among the tile's kBN / 64
+            uint8_t* img =
+                p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + hblk / 4) * kImgA;
+            const int jb = hblk % 4;
+            *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * jb + lk)) = chunk;
+            if (lk == 0) img[kImgData + row * 4 + scale_byte(jb)] = static_cast<uint8_t>(code);
+          });
+        });
       };
       if constexpr (MODE == kGateUpSitu)
-        stage_h([&](float g, float u) {
+        quant_store([&](float g, float u) {
           return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
         });
       else
-        stage_h([](float g, float u) { return act_swiglu(g, u); });
-      __syncthreads();
-      // the 128 x (kBN/2) h tile is WN/2 K stages of the down GEMM's A operand, starting at
-      // stage n0/256 of row tile mt
-      constexpr int kBlocksPerRow = kBN / 64;  // MX blocks of 32 h columns
-      const int kt_down = p.N / kImgBRows;     // K stages of the down GEMM (I / 128)
-      // consecutive lanes take consecutive rows of one block column: a row is 4 * kHStride
-      // bytes = 16 (mod 256) apart, so 16 lanes read 16 distinct bank groups
-      static_assert(kBlocksPerRow * kBM == 2 * T::kThreads, "two h blocks per thread");
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        int b = t + half * T::kThreads;
-        int row = b % kBM, cb = b / kBM;
-        const float* src = hl + row * T::kHStride + cb * 32;
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          v4f x4 = reinterpret_cast<const v4f*>(src)[i];
-          v[i * 4] = x4[0];
-          v[i * 4 + 1] = x4[1];
-          v[i * 4 + 2] = x4[2];
-          v[i * 4 + 3] = x4[3];
-        }
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        uint32_t code = mx_scale_code(amax, 8);
-        float inv = mx_inv_scale(code);
-        v4i out[2];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv,
-                                                        v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
-        const int j = cb % 4;
-        uint8_t* img = p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + cb / 4) * kImgA;
-        *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j)) = out[0];
-        *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * j + 1)) = out[1];
-        img[kImgData + row * 4 + scale_byte(j)] = static_cast<uint8_t>(code);
-      }
-      __syncthreads();
+        quant_store([](float g, float u) { return act_swiglu(g, u); });
     } else {
-      const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
+      // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
+      // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
+      // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile: one 8-byte LDS write per
+      // group of four. Rows [0, nvalid) of this tile are real.
+      const int nvalid = min(kBM, row_end - m0);
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
+      static_for<2>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const int row = wm * 64 + i * 32 + lr;
+        static_for<4>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int q = 0; q < 16; q += 2) {
-            int row = wm * 64 + i * 32 + (q >> 2) * 8 + lk * 4 + (q & 3);  // q and q + 1: rows
-            int col = wn * 128 + j * 32 + lr;                               // row and row + 1
-            uint32_t two = pk_bf16(acc[i][j][q], acc[i][j][q + 1]);
-            yl[row * T::kYStride + col] = static_cast<uint16_t>(two);
-            yl[(row + 1) * T::kYStride + col] = static_cast<uint16_t>(two >> 16);
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const uint2 two = {pk_bf16(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1]),
+                               pk_bf16(acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3])};
+            *reinterpret_cast<uint2*>(yl + row * T::kYStride + wn * 128 + j * 32 + q4 * 8 +
+                                      lk * 4) = two;
           }
+        });
+      });
       __syncthreads();
       constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
 #pragma unroll 4
       for (int q = 0; q < 16; ++q) {
-        int idx = q * T::kThreads + t;
-        int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        const int idx = q * T::kThreads + t;
+        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
         if (row < nvalid)
           *reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8) =
               *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8);
