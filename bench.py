@@ -27,7 +27,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "sgl-afd-plugin_amd")]
 
 PEAK_TFLOPS = {"fp4": 10100.0, "fp8": 5000.0, "bf16": 2500.0}
 PEAK_HBM_GBS = 8000.0
-STAGES = ("route", "quant", "gate_up", "down", "finalize")
+STAGES = ("hist_quant", "scatter", "gate_up", "down", "finalize")
 
 
 def parse():
@@ -506,7 +506,8 @@ def main():
         "mfma_util_vs_issued_peak": round(tflops / PEAK_TFLOPS[issued], 4),
         "stages_ms": stage_avg,
         "stages_note": "from a second pass through afd_moe_ffn_profiled (stage events on the stream); "
-        "the timed steps call afd_moe_ffn; route and quant overlap (quant = wait for it after route)",
+        "the timed steps call afd_moe_ffn. hist_quant: the expert histogram and the activation "
+        "quantization in one launch; scatter: the router's scan and pair scatter",
         "roofline": {
             "kernel": "grouped gate_up GEMM + SwiGLU (mx_gemm_kernel<gate_up>)"
             if shape.fmt == "mxfp4" else "grouped gate_up GEMM + SwiGLU (fp8_gemm_kernel<gate_up>)",

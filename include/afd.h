@@ -3,11 +3,8 @@
  * disaggregated MoE deployment.
  *
  * Every entry point takes plain device pointers, sizes and a hipStream_t (as void*), only
- * enqueues work on that stream (no host synchronisation, no device memory allocation) and
- * returns 0 or a negative afd_status. Global state: the thread-local last HIP error, and
- * one side stream with two events per device, created on the first afd_moe_ffn call, on
- * which the call runs its activation quantizer forked from and joined back to the caller's
- * stream (event record / stream wait, so graph capture and stream order are unaffected).
+ * enqueues work on that stream (no host synchronisation, no allocation, no global mutable
+ * state besides the thread-local last HIP error) and returns 0 or a negative afd_status.
  *
  * Reference interfaces each group replaces (paths relative to the reference repository,
  * P = python/sgl_asap_plugin):
@@ -173,8 +170,9 @@ int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const
                 uint16_t* out, afd_stream_t stream);
 
 /* afd_moe_ffn with hipEvent_t handles recorded on `stream` around its stages:
- * stage_events[0] before routing, [1] after routing, [2] after the activation quantizer,
- * [3] after gate_up, [4] after down, [5] after finalize. NULL entries are skipped.
+ * stage_events[0] before routing, [1] after the launch that histograms the pairs and
+ * quantizes the activations, [2] after the router's scan and scatter, [3] after gate_up,
+ * [4] after down, [5] after finalize. NULL entries are skipped.
  * Same replaced interface as afd_moe_ffn; for the per-stage timing of JobTimer
  * (P/srt/managers/scheduler.py:109-159). */
 int afd_moe_ffn_profiled(const afd_moe_cfg* cfg, const afd_expert_weights* weights,

@@ -12,11 +12,13 @@ constexpr int kMaxLocalExperts = 256;
 constexpr int kMaxTopk = 32;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
 
-int launch_quant_mxfp8_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* s,
-                            hipStream_t stream);
 
-int launch_route(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
-                 const afd_ws_layout& L, hipStream_t stream);
+// Routing of the job's pairs into the workspace; with x, the activation quantization into
+// ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs beside the
+// expert histogram. `mid` (optional) is recorded between the two launches.
+int launch_route_quant(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
+                       const afd_ws_layout& L, const uint16_t* x, hipStream_t stream,
+                       hipEvent_t mid);
 
 // Grouped MXFP4 GEMMs (afd_gemm_mx.hip).
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,

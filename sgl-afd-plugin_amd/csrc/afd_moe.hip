@@ -1,7 +1,8 @@
 // The expert call of one job on one F rank (afd_moe_ffn), its workspace layout, the
 // finalize (top-k weighted sum) and the A-side combine.
 //
-//   (quant x || route) -> grouped gate_up (+SwiGLU, +h quant) -> grouped down -> finalize
+//   (route histogram || quant x) -> route scatter -> grouped gate_up (+SwiGLU, +h quant)
+//   -> grouped down -> finalize
 //
 // finalize and combine are HBM-bound gathers with fixed summation order, so their results
 // are reproducible bit for bit (no atomics).
@@ -220,33 +221,6 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   return AFD_OK;
 }
 
-// The activation quantizer does not depend on the routing, and the router is latency-bound
-// while the quantizer is HBM-bound, so the quantizer runs on a second stream beside the router:
-// forked from the caller's stream and joined back before the grouped GEMMs with events (HIP
-// graph capture records that as a fork and a join). One side stream and event pair per device,
-// created on first use; enqueueing through them is serialized across host threads.
-struct SideStream {
-  hipStream_t s = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-};
-static std::mutex g_side_mu;
-static std::vector<SideStream> g_side;
-
-// with g_side_mu held
-static int side_stream(SideStream** out) {
-  int dev = 0;
-  AFD_CHECK_HIP(hipGetDevice(&dev));
-  if (dev >= static_cast<int>(g_side.size())) g_side.resize(dev + 1);
-  SideStream& ss = g_side[dev];
-  if (!ss.s) {
-    AFD_CHECK_HIP(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking));
-    AFD_CHECK_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
-    AFD_CHECK_HIP(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming));
-  }
-  *out = &ss;
-  return AFD_OK;
-}
-
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                         const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
                         void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream,
@@ -270,25 +244,11 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   if (n > 0) {
     uint8_t* wsb = static_cast<uint8_t*>(ws);
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
-    {
-      // quantizer on the side stream, router on the caller's; the stage marks 1 and 2 are
-      // the router's end and the join
-      std::lock_guard<std::mutex> lock(g_side_mu);
-      SideStream* side = nullptr;
-      if ((st = side_stream(&side)) != AFD_OK) return st;
-      AFD_CHECK_HIP(hipEventRecord(side->fork, s));
-      AFD_CHECK_HIP(hipStreamWaitEvent(side->s, side->fork, 0));
-      if (mx)
-        st = launch_quant_mxfp8_rows(x, n, cfg->hidden, wsb + L.xq, wsb + L.xs, side->s);
-      else
-        st = afd_quant_fp8_1x128(x, n, cfg->hidden, wsb + L.xq,
-                                 reinterpret_cast<float*>(wsb + L.xs), side->s);
-      if (st != AFD_OK) return st;
-      AFD_CHECK_HIP(hipEventRecord(side->join, side->s));
-      if ((st = launch_route(ids, n, *cfg, wsb, L, s)) != AFD_OK) return st;
-      if ((st = mark(1)) != AFD_OK) return st;
-      AFD_CHECK_HIP(hipStreamWaitEvent(s, side->join, 0));
-    }
+    // routing and the activation quantization (one launch beside the expert histogram), then
+    // the pair scatter; stage mark 1 falls between the two launches
+    st = launch_route_quant(ids, n, *cfg, wsb, L, x, s,
+                            ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
+    if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
     st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, n, s)
             : launch_fp8_gate_up(*cfg, *weights, wsb, L, n, s);

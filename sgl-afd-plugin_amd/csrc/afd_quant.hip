@@ -4,16 +4,9 @@
 // vector and no cross-lane reduction is needed for MX; FP8 groups of 128 reduce over 4 lanes.
 #include "afd_common.h"
 #include "afd_internal.h"
+#include "afd_quant_dev.h"
 
 namespace afd {
-
-constexpr int kQuantThreads = 256;
-
-static int grid_for(int64_t items) {
-  int64_t g = (items + kQuantThreads - 1) / kQuantThreads;
-  if (g > 8192) g = 8192;  // grid-stride beyond 32 workgroups per CU
-  return static_cast<int>(g < 1 ? 1 : g);
-}
 
 
 // Logical source row of physical row r when gate and up rows are interleaved in groups of g
@@ -23,102 +16,23 @@ __device__ __forceinline__ int64_t gate_up_source_row(int64_t r, int64_t rows, i
   return q < g ? j * g + q : rows / 2 + j * g + (q - g);
 }
 
-// ---------------------------------------------------------------- MXFP8 activations
-// One lane per 32-element block. kStageOrder stores a row's scales as the MX GEMM reads them:
-// within each group of 4 blocks (one 128-wide K stage), block j at byte scale_byte(j).
+// ---------------------------------------------------------------- activation quantizers
+// The loops live in afd_quant_dev.h (the router's prep kernel runs them too); these kernels
+// give them the whole grid.
 template <bool kStageOrder>
 __global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
     const uint16_t* __restrict__ x, int64_t blocks, int cols, uint8_t* __restrict__ q,
     uint8_t* __restrict__ s) {
-  const int bpr = cols / kMxBlock;
-  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
-       b += int64_t(gridDim.x) * kQuantThreads) {
-    int64_t row = b / bpr, cb = b % bpr;
-    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cb * kMxBlock);
-    v4i raw[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) raw[i] = src[i];
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t w = static_cast<uint32_t>(raw[i][j]);
-        v[i * 8 + j * 2] = __uint_as_float(w << 16);
-        v[i * 8 + j * 2 + 1] = __uint_as_float(w & 0xffff0000u);
-      }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    uint32_t code = mx_scale_code(amax, 8);
-    float inv = mx_inv_scale(code);
-    v4i out[2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      out[i / 4][i % 4] = static_cast<int>(
-          pk4_e4m3(v[i * 4] * inv, v[i * 4 + 1] * inv, v[i * 4 + 2] * inv, v[i * 4 + 3] * inv));
-    v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cb * kMxBlock);
-    dst[0] = out[0];
-    dst[1] = out[1];
-    const int64_t at = kStageOrder ? (cb & ~int64_t(3)) + scale_byte(static_cast<int>(cb & 3)) : cb;
-    s[row * bpr + at] = static_cast<uint8_t>(code);
-  }
+  quant_mxfp8_items<kStageOrder>(x, blocks, cols, q, s,
+                                 blockIdx.x * int64_t(kQuantThreads) + threadIdx.x,
+                                 int64_t(gridDim.x) * kQuantThreads);
 }
 
-int launch_quant_mxfp8_rows(const uint16_t* x, int64_t rows, int cols, uint8_t* q, uint8_t* s,
-                            hipStream_t stream) {
-  const int64_t blocks = rows * (cols / kMxBlock);
-  hipLaunchKernelGGL(quant_mxfp8_kernel<true>, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
-                     stream, x, blocks, cols, q, s);
-  AFD_CHECK_LAUNCH();
-  return AFD_OK;
-}
-
-// ---------------------------------------------------------------- FP8 1x128 activations
-// 4 consecutive lanes own one group of 128 (32 elements each); amax via two xor shuffles.
 __global__ __launch_bounds__(kQuantThreads) void quant_fp8_1x128_kernel(
     const uint16_t* __restrict__ x, int64_t quarters, int cols, uint8_t* __restrict__ q,
     float* __restrict__ s) {
-  const int qpr = cols / kMxBlock;  // quarter-groups per row
-  const int64_t stride = int64_t(gridDim.x) * kQuantThreads;
-  // all lanes of a wave iterate together so the shuffles see live partners
-  int64_t total = (quarters + stride - 1) / stride * stride;
-  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < total; b += stride) {
-    bool live = b < quarters;
-    int64_t bb = live ? b : 0;
-    int64_t row = bb / qpr, cq = bb % qpr;
-    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cq * kMxBlock);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v4i r = src[i];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t w = static_cast<uint32_t>(r[j]);
-        v[i * 8 + j * 2] = __uint_as_float(w << 16);
-        v[i * 8 + j * 2 + 1] = __uint_as_float(w & 0xffff0000u);
-      }
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
-    if (!live) continue;
-    v4i out[2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] / sc)) << (8 * j);
-      out[i / 4][i % 4] = static_cast<int>(packed);
-    }
-    v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cq * kMxBlock);
-    dst[0] = out[0];
-    dst[1] = out[1];
-    if ((cq & 3) == 0) s[row * (cols / kFp8Block) + cq / 4] = sc;
-  }
+  quant_fp8_1x128_items(x, quarters, cols, q, s, blockIdx.x * int64_t(kQuantThreads) + threadIdx.x,
+                        int64_t(gridDim.x) * kQuantThreads);
 }
 
 // ---------------------------------------------------------------- MXFP4 weight packer

@@ -1,34 +1,59 @@
 // Routing of one job's (token, k) pairs to this F rank's local experts, on gfx950.
 //
-// Three small launches, all integer work on a 4*n*k-byte id array (HBM/latency bound):
-//   1. route_hist:    chunk c of the flat pair array -> per-chunk expert histogram (LDS
-//                     atomics; counts are order-free).
-//   2. route_scan:    one workgroup turns the [chunks][E] histogram into per-chunk exclusive
-//                     bases, counts, offsets, block_m-padded offsets, the row-tile table and
-//                     the -1 fill of padding rows (every step spread over the experts).
-//   3. route_scatter: each chunk walks its pairs in flat order, 256 at a time; a pair's rank
-//                     among equal keys inside its wavefront comes from 9 ballots (one per key
-//                     bit), across wavefronts from LDS counts, so the placement is the stable
-//                     order (ascending flat index inside each expert) bit for bit.
+// Two launches, integer work on a 4*n*k-byte id array (HBM/latency bound):
+//   1. route_prep:    workgroup c < chunks histograms chunk c of the flat pair array by local
+//                     expert (LDS atomics; counts are order-free); with the expert call, the
+//                     remaining workgroups quantize the activations meanwhile (afd_quant_dev.h).
+//   2. route_scatter: workgroup c first reads the whole [chunks][E] histogram (it is in L2) to
+//                     get each expert's count, its own chunk's base per expert and the
+//                     block_m-padded expert offsets (a wavefront scan); workgroup 0 also writes
+//                     counts, offsets, padded offsets, the row-tile table, the tile count and
+//                     the -1 fill of padding rows. It then walks its pairs in flat order, 256 at
+//                     a time; a pair's rank among equal keys inside its wavefront comes from 9
+//                     ballots (one per key bit), across wavefronts from LDS counts, so the
+//                     placement is the stable order (ascending flat index inside each expert)
+//                     bit for bit.
 #include "afd_common.h"
 #include "afd_internal.h"
+#include "afd_quant_dev.h"
 
 namespace afd {
 
 constexpr int kRouteThreads = 256;
-constexpr int kScanThreads = 1024;
 constexpr int kMaxChunks = 128;
 constexpr int kKeyBits = 9;  // keys 0..256 (local expert, or num_local for "not local")
-static_assert(kMaxChunks % (kScanThreads / kMaxLocalExperts) == 0, "chunk runs of the scan");
+static_assert(kRouteThreads == kQuantThreads, "the prep kernel's workgroups do either job");
 
 __device__ __forceinline__ int pair_key(int id, int e_lo, int num_local) {
   unsigned rel = static_cast<unsigned>(id - e_lo);
   return rel < static_cast<unsigned>(num_local) ? static_cast<int>(rel) : num_local;
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_hist_kernel(
-    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int e_lo, int num_local,
-    int32_t* __restrict__ hist) {
+// activation quantization run by the prep kernel beside the histogram
+enum { kPrepNone = 0, kPrepMxfp8 = 1, kPrepFp8 = 2 };
+struct PrepQuant {
+  const uint16_t* x;
+  int64_t items;  // MX blocks of 32 (MXFP8) or quarter groups of 32 (FP8 1x128)
+  int cols;
+  uint8_t* q;
+  void* s;
+};
+
+template <int QUANT>
+__global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
+    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int chunks, int e_lo,
+    int num_local, int32_t* __restrict__ hist, PrepQuant pq) {
+  if (static_cast<int>(blockIdx.x) >= chunks) {
+    const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
+    const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;
+    if constexpr (QUANT == kPrepMxfp8)
+      quant_mxfp8_items<true>(pq.x, pq.items, pq.cols, pq.q, static_cast<uint8_t*>(pq.s), first,
+                              stride);
+    else if constexpr (QUANT == kPrepFp8)
+      quant_fp8_1x128_items(pq.x, pq.items, pq.cols, pq.q, static_cast<float*>(pq.s), first,
+                            stride);
+    return;
+  }
   __shared__ int cnt[kMaxLocalExperts];
   for (int e = threadIdx.x; e < num_local; e += kRouteThreads) cnt[e] = 0;
   __syncthreads();
@@ -43,48 +68,48 @@ __global__ __launch_bounds__(kRouteThreads) void route_hist_kernel(
     hist[int64_t(blockIdx.x) * num_local + e] = cnt[e];
 }
 
-__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
-    int32_t* __restrict__ hist, int chunks, int num_local, int block_m,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets, int32_t* __restrict__ poff,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ tile_expert,
+__global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
+    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int chunks, int e_lo,
+    int num_local, int block_m, const int32_t* __restrict__ hist, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ poff, int32_t* __restrict__ sorted_pairs,
+    int32_t* __restrict__ pair_pos, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ num_tiles) {
-  __shared__ int part[kScanThreads];
+  constexpr int kWaves = kRouteThreads / 64;
+  constexpr int kMaxPer = kMaxChunks / (kRouteThreads / kMaxLocalExperts);
+  __shared__ int run[kMaxLocalExperts + 1];
+  __shared__ int wcnt[kWaves][kMaxLocalExperts + 1];
+  __shared__ int part_all[kRouteThreads], part_before[kRouteThreads];
   __shared__ int tot[kMaxLocalExperts];
   __shared__ int pof[kMaxLocalExperts + 1];
-  const int t = threadIdx.x;
-  // Expert e's chunks are split over G = kScanThreads / num_local threads (e, g); each loads
-  // its contiguous run of at most kMaxPer chunks at once (independent loads, kept in
-  // registers), the runs' bases come from the partial sums in LDS, then each thread rewrites
-  // its chunks as exclusive bases without reloading them.
-  constexpr int kMaxPer = kMaxChunks / (kScanThreads / kMaxLocalExperts);
-  const int G = kScanThreads / num_local;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int c = blockIdx.x;
+  // Expert e's chunks are split over G = kRouteThreads / num_local threads (e, g), each a
+  // contiguous run of at most kMaxPer chunks loaded at once: the counts in all chunks and in
+  // the chunks before this one.
+  const int G = kRouteThreads / num_local;
   const int per = (chunks + G - 1) / G;
   const int e = t % num_local, g = t / num_local;
   const bool active = g < G;
   const int c0 = active ? g * per : 0, c1 = active ? min(c0 + per, chunks) : 0;
-  int hv[kMaxPer];
-  int sum = 0;
+  int all = 0, before = 0;
 #pragma unroll
   for (int k = 0; k < kMaxPer; ++k) {
-    hv[k] = c0 + k < c1 ? hist[int64_t(c0 + k) * num_local + e] : 0;
-    sum += hv[k];
+    const int h = c0 + k < c1 ? hist[int64_t(c0 + k) * num_local + e] : 0;
+    all += h;
+    before += c0 + k < c ? h : 0;
   }
-  part[t] = sum;
+  part_all[t] = all;
+  part_before[t] = before;
+  for (int i = t; i < kWaves * (kMaxLocalExperts + 1); i += kRouteThreads) (&wcnt[0][0])[i] = 0;
   __syncthreads();
-  if (active) {
-    int run = 0;
-    for (int h = 0; h < g; ++h) run += part[h * num_local + e];
-    if (g == 0) {
-      int all = 0;
-      for (int h = 0; h < G; ++h) all += part[h * num_local + e];
-      tot[e] = all;
-      counts[e] = all;
+  if (active && g == 0) {
+    int a = 0, b = 0;
+    for (int h = 0; h < G; ++h) {
+      a += part_all[h * num_local + e];
+      b += part_before[h * num_local + e];
     }
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k) {
-      if (c0 + k < c1) hist[int64_t(c0 + k) * num_local + e] = run;
-      run += hv[k];
-    }
+    tot[e] = a;
+    run[e] = b;  // this chunk's rank base inside expert e; the segment start is added below
   }
   __syncthreads();
   // expert offsets and block_m-padded offsets: one wavefront, 4 experts per lane
@@ -93,11 +118,11 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ex = t * 4 + i;
-      const int c = ex < num_local ? tot[ex] : 0;
+      const int n_e = ex < num_local ? tot[ex] : 0;
       o[i] = so;
       q[i] = sp;
-      so += c;
-      sp += (c + block_m - 1) / block_m * block_m;
+      so += n_e;
+      sp += (n_e + block_m - 1) / block_m * block_m;
     }
     int io = so, ip = sp;  // inclusive scans of the lane totals
 #pragma unroll
@@ -113,38 +138,33 @@ __global__ __launch_bounds__(kScanThreads) void route_scan_kernel(
     for (int i = 0; i < 4; ++i) {
       const int ex = t * 4 + i;
       if (ex < num_local) {
-        offsets[ex] = bo + o[i];
-        poff[ex] = bp + q[i];
         pof[ex] = bp + q[i];
+        if (c == 0) {
+          counts[ex] = tot[ex];
+          offsets[ex] = bo + o[i];
+          poff[ex] = bp + q[i];
+        }
       }
     }
     if (t == 63) {
-      offsets[num_local] = io;
-      poff[num_local] = ip;
       pof[num_local] = ip;
-      num_tiles[0] = ip / block_m;
+      if (c == 0) {
+        offsets[num_local] = io;
+        poff[num_local] = ip;
+        num_tiles[0] = ip / block_m;
+      }
     }
   }
   __syncthreads();
-  // row-tile table (thread e writes expert e's tiles) and -1 on the padding rows of every
-  // segment (the G threads of expert e stride over its at most block_m - 1 padding rows)
-  if (t < num_local)
-    for (int i = pof[t] / block_m, i1 = pof[t + 1] / block_m; i < i1; ++i) tile_expert[i] = t;
-  if (active)
-    for (int r = pof[e] + tot[e] + g; r < pof[e + 1]; r += G) sorted_pairs[r] = -1;
-}
-
-__global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
-    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int e_lo, int num_local,
-    const int32_t* __restrict__ hist, const int32_t* __restrict__ poff,
-    int32_t* __restrict__ sorted_pairs, int32_t* __restrict__ pair_pos) {
-  constexpr int kWaves = kRouteThreads / 64;
-  __shared__ int run[kMaxLocalExperts + 1];
-  __shared__ int wcnt[kWaves][kMaxLocalExperts + 1];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  for (int e = t; e < num_local; e += kRouteThreads)
-    run[e] = poff[e] + hist[int64_t(blockIdx.x) * num_local + e];
-  for (int i = t; i < kWaves * (kMaxLocalExperts + 1); i += kRouteThreads) (&wcnt[0][0])[i] = 0;
+  for (int ex = t; ex < num_local; ex += kRouteThreads) run[ex] += pof[ex];
+  if (c == 0) {
+    // row-tile table (thread e writes expert e's tiles) and -1 on the padding rows of every
+    // segment (the G threads of expert e stride over its at most block_m - 1 padding rows)
+    if (t < num_local)
+      for (int i = pof[t] / block_m, i1 = pof[t + 1] / block_m; i < i1; ++i) tile_expert[i] = t;
+    if (active)
+      for (int r = pof[e] + tot[e] + g; r < pof[e + 1]; r += G) sorted_pairs[r] = -1;
+  }
   __syncthreads();
   const int64_t lo = int64_t(blockIdx.x) * chunk;
   const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
@@ -196,31 +216,45 @@ void route_chunking(int64_t pairs, int* chunks, int* chunk) {
   *chunks = pairs == 0 ? 0 : static_cast<int>((pairs + c - 1) / c);
 }
 
-int launch_route(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
-                 const afd_ws_layout& L, hipStream_t stream) {
+int launch_route_quant(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
+                       const afd_ws_layout& L, const uint16_t* x, hipStream_t stream,
+                       hipEvent_t mid) {
   const int64_t pairs = int64_t(n) * cfg.topk;
   int chunks, chunk;
   route_chunking(pairs, &chunks, &chunk);
   int32_t* hist = reinterpret_cast<int32_t*>(ws + L.hist);
-  int32_t* poff = reinterpret_cast<int32_t*>(ws + L.padded_offsets);
-  int32_t* sorted = reinterpret_cast<int32_t*>(ws + L.sorted_pairs);
-  int32_t* ppos = reinterpret_cast<int32_t*>(ws + L.pair_pos);
-  if (chunks > 0) {
-    hipLaunchKernelGGL(route_hist_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, ids,
-                       pairs, chunk, cfg.expert_lo, cfg.num_local, hist);
+  PrepQuant pq{x, 0, cfg.hidden, ws + L.xq, ws + L.xs};
+  int quant_grid = 0;
+  const int fmt = x == nullptr ? kPrepNone : cfg.weight_fmt == AFD_W_MXFP4 ? kPrepMxfp8 : kPrepFp8;
+  if (fmt != kPrepNone) {
+    pq.items = int64_t(n) * (cfg.hidden / kMxBlock);
+    quant_grid = grid_for(pq.items);
+  }
+  if (chunks + quant_grid > 0) {
+    const dim3 grid(chunks + quant_grid);
+    if (fmt == kPrepMxfp8)
+      hipLaunchKernelGGL(route_prep_kernel<kPrepMxfp8>, grid, dim3(kRouteThreads), 0, stream, ids,
+                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
+    else if (fmt == kPrepFp8)
+      hipLaunchKernelGGL(route_prep_kernel<kPrepFp8>, grid, dim3(kRouteThreads), 0, stream, ids,
+                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
+    else
+      hipLaunchKernelGGL(route_prep_kernel<kPrepNone>, grid, dim3(kRouteThreads), 0, stream, ids,
+                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
     AFD_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, hist, chunks,
-                     cfg.num_local, L.block_m, reinterpret_cast<int32_t*>(ws + L.counts),
-                     reinterpret_cast<int32_t*>(ws + L.offsets), poff, sorted,
+  if (mid) AFD_CHECK_HIP(hipEventRecord(mid, stream));
+  // at least one workgroup, which writes the (empty) tables when there are no pairs
+  hipLaunchKernelGGL(route_scatter_kernel, dim3(chunks > 0 ? chunks : 1), dim3(kRouteThreads), 0,
+                     stream, ids, pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, L.block_m,
+                     hist, reinterpret_cast<int32_t*>(ws + L.counts),
+                     reinterpret_cast<int32_t*>(ws + L.offsets),
+                     reinterpret_cast<int32_t*>(ws + L.padded_offsets),
+                     reinterpret_cast<int32_t*>(ws + L.sorted_pairs),
+                     reinterpret_cast<int32_t*>(ws + L.pair_pos),
                      reinterpret_cast<int32_t*>(ws + L.tile_expert),
                      reinterpret_cast<int32_t*>(ws + L.num_tiles));
   AFD_CHECK_LAUNCH();
-  if (chunks > 0) {
-    hipLaunchKernelGGL(route_scatter_kernel, dim3(chunks), dim3(kRouteThreads), 0, stream, ids,
-                       pairs, chunk, cfg.expert_lo, cfg.num_local, hist, poff, sorted, ppos);
-    AFD_CHECK_LAUNCH();
-  }
   return AFD_OK;
 }
 
@@ -233,6 +267,6 @@ extern "C" int afd_route(const int32_t* ids, int32_t n, const afd_moe_cfg* cfg, 
   if (st != AFD_OK) return st;
   if ((!ids && n > 0) || !ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
-  return afd::launch_route(ids, n, *cfg, static_cast<uint8_t*>(ws), L,
-                           static_cast<hipStream_t>(stream));
+  return afd::launch_route_quant(ids, n, *cfg, static_cast<uint8_t*>(ws), L, nullptr,
+                                 static_cast<hipStream_t>(stream), nullptr);
 }
