@@ -58,17 +58,17 @@ constexpr int kStages = 3;
 // per 256 B group (written by one wavefront's dword copies)
 constexpr int kWScales = kStages * kStage;
 constexpr int kMaxKT = 128;
-constexpr int kLds = kWScales + 2 * kMaxKT * 4;
+// then the gate_up epilogue's per-row amax of each column wavefront, [128 rows][4]
+constexpr int kAmax = kWScales + 2 * kMaxKT * 4;
+constexpr int kLds = kAmax + kBM * 4 * 4;
 // copies per wavefront and stage: 2 activation pieces, 4 weight pieces and one piece of
 // activation scales (a wavefront past the two halves repeats its first weight piece: the same
 // bytes to the same place), so every wavefront counts the same number of copies
 constexpr int kQX = kBM / 8 / kWaves;  // 2
 constexpr int kQW = kBN / 8 / kWaves;  // 4
 constexpr int kPieces = kQX + kQW + 1;
-constexpr int kHStride = kBN / 2 + 4;  // fp32 stride of the gate_up epilogue tile
 constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
 static_assert(kQX * kWaves * 8 == kBM && kQW * kWaves * 8 == kBN, "pieces cover the tile");
-static_assert(kBM * kHStride * 4 <= kStages * kStage, "gate_up epilogue tile must fit the stages");
 static_assert(kBM * kYStride * 2 <= kStages * kStage, "down epilogue tile must fit the stages");
 static_assert(kLds <= 160 * 1024, "LDS of one CU");
 static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
@@ -157,10 +157,69 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
       s_voff = token(sp_next[kQX]) * static_cast<uint32_t>(KT * 4);
     }
   };
+  // The tile whose stages the copies below fetch. gate_up starts the next tile's copies
+  // (weight scales and the first two stages) right after its own K loop: its epilogue works
+  // from registers and a small LDS area outside the ring, so the copies land while it runs.
+  // down's epilogue stages its output through the ring, so it starts them at the tile start.
+  constexpr bool kEarlyStart = MODE != kDown;
+  const uint8_t* x_tile = nullptr;
+  const float* s_tile = nullptr;
+  const uint8_t* w_tile = nullptr;
+  int blk0 = 0, blk1 = 0;
+  int64_t e_copy = 0;
+  auto copy_tile = [&](int mt, int nt, int64_t e) {
+    x_tile = MODE != kDown ? p.a : p.a + int64_t(mt) * kBM * p.K;
+    s_tile = MODE != kDown ? p.as : p.as + int64_t(mt) * kBM * KT;
+    w_tile = p.b + (e * p.N + int64_t(nt) * kBN) * int64_t(p.K);
+    // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
+    // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
+    blk0 = MODE != kDown ? nt * kBN / 256 : nt * kBN / 128;
+    blk1 = MODE != kDown ? nblk / 2 + nt * kBN / 256 : nt * kBN / 128 + 1;
+    e_copy = e;
+  };
+  auto issue_piece = [&](int kt, auto qc) {
+    constexpr int q = decltype(qc)::value;
+    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+    if constexpr (q < kQX) {
+      lds_dma16(st + (w_u * kQX + q) * 1024, x_tile + kt * kBK, x_voff[q]);
+    } else if constexpr (q < kQX + kQW) {
+      constexpr int qw = q - kQX;
+      lds_dma16(st + kWOff + (w_u * kQW + qw) * 1024, w_tile + kt * kBK, w_voff[qw]);
+    } else {
+      if (copies_scales)
+        lds_dma4(st + kXScales + (w_u & 1) * 256, s_tile + kt, s_voff);
+      else
+        lds_dma16(st + kWOff + w_u * kQW * 1024, w_tile + kt * kBK, w_voff[0]);
+    }
+  };
+  auto issue = [&](int kt) { static_for<kPieces>([&](auto q) { issue_piece(kt, q); }); };
+  const int last = KT - 1;
+  // Wavefront 0 first copies the tile's weight block scales (lane x: block x < 32 ? blk0 :
+  // blk1, stage 32 g + x % 32, clamped in bounds); those copies are older than every piece of
+  // stage 0, so the wait for stage 0 covers them. Then the first two stages.
+  auto start_copies = [&]() {
+    if (w_u == 0) {
+      const float* bs_e = p.bs + e_copy * nblk * KT;
+      const int b = lk == 0 ? blk0 : blk1;
+      for (int g = 0; g * 32 < KT; ++g) {
+        const int kb = min(lr + 32 * g, KT - 1);
+        lds_dma4(lds_base + kWScales + g * 256, bs_e, static_cast<uint32_t>((b * KT + kb) * 4));
+      }
+    }
+    issue(0);
+    issue(min(1, last));
+  };
+
   int i = walk.begin();
   if (i < walk.count) {
     load_next(i);
     decode_next();
+    if constexpr (kEarlyStart) {
+      int mt, nt;
+      walk.at(i, mt, nt);
+      copy_tile(mt, nt, e_cur);
+      start_copies();
+    }
   }
 
   for (int i_next; i < walk.count; i = i_next) {
@@ -174,31 +233,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
     const bool has_next = i_next < walk.count;
     if (has_next) load_next(i_next);
-
-    const uint8_t* x_tile = MODE != kDown ? p.a : p.a + int64_t(m0) * p.K;
-    const float* s_tile = MODE != kDown ? p.as : p.as + int64_t(m0) * KT;
-    const uint8_t* w_tile = p.b + (e * p.N + n0) * int64_t(p.K);
-    // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
-    // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
-    const int blk0 = MODE != kDown ? n0 / 256 : n0 / 128;
-    const int blk1 = MODE != kDown ? nblk / 2 + n0 / 256 : n0 / 128 + 1;
-
-    auto issue_piece = [&](int kt, auto qc) {
-      constexpr int q = decltype(qc)::value;
-      const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
-      if constexpr (q < kQX) {
-        lds_dma16(st + (w_u * kQX + q) * 1024, x_tile + kt * kBK, x_voff[q]);
-      } else if constexpr (q < kQX + kQW) {
-        constexpr int qw = q - kQX;
-        lds_dma16(st + kWOff + (w_u * kQW + qw) * 1024, w_tile + kt * kBK, w_voff[qw]);
-      } else {
-        if (copies_scales)
-          lds_dma4(st + kXScales + (w_u & 1) * 256, s_tile + kt, s_voff);
-        else
-          lds_dma16(st + kWOff + w_u * kQW * 1024, w_tile + kt * kBK, w_voff[0]);
-      }
-    };
-    auto issue = [&](int kt) { static_for<kPieces>([&](auto q) { issue_piece(kt, q); }); };
+    if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
     v16f acc[2][2];
 #pragma unroll
@@ -284,22 +319,10 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     };
 
     // Ping-pong as in the MX kernel: each group copies its pieces of stage kt+2 when it starts
-    // reading stage kt;
-    // copies are clamped to the last stage (a clamped copy rewrites a slot with its own
-    // bytes). Wavefront 0 first copies the tile's weight block scales; those copies are older
-    // than every piece of stage 0, so the wait for stage 0 covers them.
-    const int last = KT - 1;
-    if (w_u == 0) {
-      // lane x: block (x < 32 ? blk0 : blk1), stage 32 g + x % 32 (clamped: in bounds)
-      const float* bs_e = p.bs + e * nblk * KT;
-      const int b = lk == 0 ? blk0 : blk1;
-      for (int g = 0; g * 32 < KT; ++g) {
-        const int kb = min(lr + 32 * g, KT - 1);
-        lds_dma4(lds_base + kWScales + g * 256, bs_e, static_cast<uint32_t>((b * KT + kb) * 4));
-      }
-    }
-    issue(0);
-    issue(min(1, last));
+    // reading stage kt; copies are clamped to the last stage (a clamped copy rewrites a slot
+    // with its own bytes). Epilogue stores of the previous tile still in flight only make the
+    // counted waits stricter (loads complete in order among themselves).
+    if constexpr (!kEarlyStart) start_copies();
     wait_vmcnt<kPieces>();  // own pieces of stage 0 (and the weight scales) landed
     __syncthreads();
     if (wm == 0) {
@@ -341,66 +364,74 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[i2][j][q] *= sl;
       }
-    wait_vmcnt<0>();  // no copy may land in the stage buffers the epilogue reuses
-    __syncthreads();  // the epilogue reuses the stage buffers
-    if (has_next) decode_next();
+    wait_vmcnt<0>();  // every copy of this tile landed
+    __syncthreads();  // and every wavefront is done reading the stages
+    if (has_next) {
+      decode_next();
+      if constexpr (kEarlyStart) {
+        int mt2, nt2;
+        walk.at(i_next, mt2, nt2);
+        copy_tile(mt2, nt2, e_cur);
+        start_copies();
+      }
+    }
 
     // accumulator q of tile (i, j): activation row 64 g + 32 i + lane % 32, output column
     // 64 c + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
     if constexpr (MODE != kDown) {
-      // SwiGLU in registers: column tiles j = 0, 1 are the gate and up halves of one 64-row
-      // group of interleaved W13, i.e. the same 32 intermediate columns.
-      float* hl = reinterpret_cast<float*>(lds);
-      auto stage_h = [&](auto fn) {
+      // SwiGLU (or SiTU) in registers: column tiles j = 0, 1 are the gate and up halves of one
+      // 64-row group of interleaved W13, i.e. the same 32 intermediate columns; the lane holds
+      // h columns 32 c + 8 q4 + 4 lk + (0..3) of its two rows. The tile's 128 h columns are
+      // one 1x128 group per row: the row's amax over its 4 column wavefronts goes through a
+      // 2 KiB LDS area; then each lane half assembles 16 contiguous codes with one exchange
+      // and stores them.
+      const int inter = p.N / 2;
+      float* amax_l = reinterpret_cast<float*>(lds + kAmax);
+      auto quant_store = [&](auto fn) {
+        float h[2][16];
 #pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2)
+        for (int i2 = 0; i2 < 2; ++i2) {
+          float m = 0.0f;
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            const int row = wm * 64 + i2 * 32 + lr;
-            const int col = wn * 32 + q4 * 8 + lk * 4;
-            v4f hv;
-#pragma unroll
-            for (int e4 = 0; e4 < 4; ++e4)
-              hv[e4] = fn(acc[i2][0][q4 * 4 + e4], acc[i2][1][q4 * 4 + e4]);
-            *reinterpret_cast<v4f*>(hl + row * kHStride + col) = hv;
+          for (int q = 0; q < 16; ++q) {
+            h[i2][q] = fn(acc[i2][0][q], acc[i2][1][q]);
+            m = fmaxf(m, fabsf(h[i2][q]));
           }
+          m = fmaxf(m, __shfl_xor(m, 32));
+          if (lk == 0) amax_l[(wm * 64 + i2 * 32 + lr) * 4 + wn] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int row = wm * 64 + i2 * 32 + lr;
+          const v4f a4 = *reinterpret_cast<const v4f*>(amax_l + row * 4);
+          const float amax = fmaxf(fmaxf(a4[0], a4[1]), fmaxf(a4[2], a4[3]));
+          const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
+          uint32_t d[4];
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            d[q4] = pk4_e4m3(h[i2][4 * q4] / sc, h[i2][4 * q4 + 1] / sc, h[i2][4 * q4 + 2] / sc,
+                             h[i2][4 * q4 + 3] / sc);
+          // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
+          // 16-31 (the partner's d2, d3 and its own)
+          const uint32_t p0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[0] : d[2]), 32));
+          const uint32_t p1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[1] : d[3]), 32));
+          v4i chunk;
+          chunk[0] = static_cast<int>(lk ? p0 : d[0]);
+          chunk[1] = static_cast<int>(lk ? d[2] : p0);
+          chunk[2] = static_cast<int>(lk ? p1 : d[1]);
+          chunk[3] = static_cast<int>(lk ? d[3] : p1);
+          *reinterpret_cast<v4i*>(p.hq + int64_t(m0 + row) * inter + n0 / 2 + wn * 32 + lk * 16) =
+              chunk;
+          if (wn == 0 && lk == 0) p.hs[int64_t(m0 + row) * (inter / kBK) + n0 / 256] = sc;
+        }
       };
       if constexpr (MODE == kGateUpSitu)
-        stage_h([&](float g, float u) {
+        quant_store([&](float g, float u) {
           return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
         });
       else
-        stage_h([](float g, float u) { return act_swiglu(g, u); });
-      __syncthreads();
-      // the tile's 128 h columns are one 1x128 group per row: 4 lanes per row, 32 values each
-      const int inter = p.N / 2;
-      const int row = t >> 2, quarter = t & 3;
-      const float* src = hl + row * kHStride + quarter * 32;
-      float v[32];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        v4f x4 = reinterpret_cast<const v4f*>(src)[k];
-        v[k * 4] = x4[0];
-        v[k * 4 + 1] = x4[1];
-        v[k * 4 + 2] = x4[2];
-        v[k * 4 + 3] = x4[3];
-      }
-      float amax = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 32; ++k) amax = fmaxf(amax, fabsf(v[k]));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
-      v4i out[2];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        out[k / 4][k % 4] = static_cast<int>(pk4_e4m3(v[k * 4] / sc, v[k * 4 + 1] / sc,
-                                                      v[k * 4 + 2] / sc, v[k * 4 + 3] / sc));
-      uint8_t* dst = p.hq + int64_t(m0 + row) * inter + n0 / 2 + quarter * 32;
-      reinterpret_cast<v4i*>(dst)[0] = out[0];
-      reinterpret_cast<v4i*>(dst)[1] = out[1];
-      if (quarter == 0) p.hs[int64_t(m0 + row) * (inter / kBK) + n0 / 256] = sc;
-      __syncthreads();
+        quant_store([](float g, float u) { return act_swiglu(g, u); });
     } else {
       const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
