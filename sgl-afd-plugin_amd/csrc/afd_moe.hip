@@ -56,18 +56,34 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   float acc[kFinElems];
 #pragma unroll
   for (int i = 0; i < kFinElems; ++i) acc[i] = 0.0f;
-  for (int kk = 0; kk < k; ++kk) {
-    const int pos = pair_pos[tok * k + kk];
-    if (pos < 0) continue;
-    const float wk = w[tok * k + kk];
-    v4i raw = *reinterpret_cast<const v4i*>(y + int64_t(pos) * hidden + col);
+  // up to 8 pairs at a time: their positions, then their rows, are loaded together; the sum
+  // still runs over kk in ascending order
+  constexpr int kBatch = 8;
+  for (int k0 = 0; k0 < k; k0 += kBatch) {
+    int pos[kBatch];
+    float wk[kBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t u = static_cast<uint32_t>(raw[i]);
-      const float p0 = wk * __uint_as_float(u << 16);
-      const float p1 = wk * __uint_as_float(u & 0xffff0000u);
-      acc[2 * i] = acc[2 * i] + p0;
-      acc[2 * i + 1] = acc[2 * i + 1] + p1;
+    for (int j = 0; j < kBatch; ++j) {
+      const bool in = k0 + j < k;
+      pos[j] = in ? pair_pos[tok * k + k0 + j] : -1;
+      wk[j] = in ? w[tok * k + k0 + j] : 0.0f;
+    }
+    v4i raw[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      raw[j] = pos[j] >= 0 ? *reinterpret_cast<const v4i*>(y + int64_t(pos[j]) * hidden + col)
+                           : v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (pos[j] < 0) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t u = static_cast<uint32_t>(raw[j][i]);
+        const float p0 = wk[j] * __uint_as_float(u << 16);
+        const float p1 = wk[j] * __uint_as_float(u & 0xffff0000u);
+        acc[2 * i] = acc[2 * i] + p0;
+        acc[2 * i + 1] = acc[2 * i + 1] + p1;
+      }
     }
   }
   v4i o;

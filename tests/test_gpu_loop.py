@@ -168,3 +168,22 @@ def _lib_copy(dst, src_ptr):
     from sgl_asap_amd.transport import hip
 
     hip.copy_async(dst.data_ptr(), src_ptr, dst.numel() * 2, torch.cuda.current_stream().cuda_stream)
+
+
+def test_graph_replays_match_eager_every_time():
+    """Each captured bucket graph replayed several times, with eager expert calls and
+    synchronizations between the replays: every replay equals the eager result bit for bit."""
+    from sgl_asap_amd.runner.graph_runner import FfnGraphRunner
+
+    say("graphs: repeated replays interleaved with eager calls")
+    experts = make_experts(64)
+    runner = FfnGraphRunner(experts, 64, LOCAL)
+    for rep in range(4):
+        for n in (5, 16, 33):
+            x, topk = job(n, 500 + 10 * rep + n)
+            ids = topk.topk_ids.to(torch.int32)
+            got = runner.run(0, x, ids, topk.topk_weights, buffer=rep % 2)
+            torch.cuda.synchronize()
+            got_bits = bits16(got)
+            want = direct(experts, 0, x, topk)  # eager work between the replays
+            assert np.array_equal(got_bits, want), (rep, n)
