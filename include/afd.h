@@ -15,7 +15,9 @@
  *                                (local_expert_offset / local_num_experts routing,
  *                                P/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:87-93)
  *   afd_quant_mxfp8 / _fp8_1x128 the activation quantizer quantize_routed_input
- *                                (mxfp4_flashinfer_trtllm_moe.py:59-61)
+ *   / afd_quant_act              (mxfp4_flashinfer_trtllm_moe.py:59-61)
+ *   afd_moe_ffn_q .............. the expert call on activations quantized before the arena
+ *                                copy (the reference's TODO, scripts/run_asap.sh:110-111)
  *   afd_finalize ............... the finalize (top-k weighted sum, do_finalize=True,
  *                                mxfp4_flashinfer_trtllm_moe.py:97)
  *   afd_combine ................ AsapBuffer.recv's sum of partial outputs
@@ -168,6 +170,22 @@ int afd_route(const int32_t* ids, int32_t n, const afd_moe_cfg* cfg, void* ws,
 int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint16_t* x,
                 const int32_t* ids, const float* w, int32_t n, void* ws, uint64_t ws_bytes,
                 uint16_t* out, afd_stream_t stream);
+
+/* The expert call on activations already quantized by afd_quant_act (fp8 activations on
+ * the wire: A quantizes before the arena copy, the arena carries xq and xs, F reads them in
+ * place). Same output as afd_moe_ffn on the bf16 x that afd_quant_act was given, bit for bit.
+ * The activation format on the wire is the reference's TODO (scripts/run_asap.sh:110-111,
+ * P/transport/layout.py:64 ACT_BYTES = 2). */
+int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint8_t* xq,
+                  const void* xs, const int32_t* ids, const float* w, int32_t n, void* ws,
+                  uint64_t ws_bytes, uint16_t* out, afd_stream_t stream);
+
+/* The activation quantizer of the expert call (quantize_routed_input,
+ * mxfp4_flashinfer_trtllm_moe.py:59-61) on its own: x bf16 [n][H] -> q e4m3 [n][H] and s:
+ * MXFP4 weights: u8 [n][H/32] UE8M0, the 4 of each 128-wide K stage as blocks 0, 2, 1, 3
+ * (block j at byte 2(j & 1) | (j >> 1) of its group); FP8 block weights: f32 [n][H/128]. */
+int afd_quant_act(const afd_moe_cfg* cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
+                  afd_stream_t stream);
 
 /* afd_moe_ffn with hipEvent_t handles recorded on `stream` around its stages:
  * stage_events[0] before routing, [1] after the launch that histograms the pairs and

@@ -503,11 +503,12 @@ static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws
 }  // namespace fp8
 
 int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                       const afd_ws_layout& L, int32_t n, hipStream_t stream) {
+                       const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
+                       hipStream_t stream) {
   (void)n;
   fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
-  p.a = ws + L.xq;
-  p.as = reinterpret_cast<const float*>(ws + L.xs);
+  p.a = xq;
+  p.as = static_cast<const float*>(xs);
   p.b = static_cast<const uint8_t*>(wt.w13);
   p.bs = static_cast<const float*>(wt.s13);
   p.K = cfg.hidden;

@@ -475,12 +475,13 @@ static int launch_mx_any(const MxGemmArgs& p, int max_row_tiles, hipStream_t str
 }
 
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                      const afd_ws_layout& L, int32_t n, hipStream_t stream) {
+                      const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
+                      hipStream_t stream) {
   (void)n;
   MxGemmArgs p;
   p.a_img = nullptr;
-  p.a_rows = ws + L.xq;
-  p.a_scales = ws + L.xs;
+  p.a_rows = xq;
+  p.a_scales = static_cast<const uint8_t*>(xs);
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
   p.act = act_params(cfg);

@@ -237,16 +237,18 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   return AFD_OK;
 }
 
+// x: bf16 activations, quantized here; or (x == NULL) xq / xs: activations the caller
+// quantized with afd_quant_act.
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
-                        const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
-                        void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream,
-                        void* const* ev) {
+                        const uint16_t* x, const uint8_t* xq, const void* xs, const int32_t* ids,
+                        const float* w, int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
+                        afd_stream_t stream, void* const* ev) {
   afd_ws_layout L;
   int st = afd_workspace_layout(cfg, n, &L);
   if (st != AFD_OK) return st;
   if (!weights || !weights->w13 || !weights->w2) return AFD_ERR_ARG;
   if (cfg->weight_fmt == AFD_W_FP8_BLOCK && (!weights->s13 || !weights->s2)) return AFD_ERR_ARG;
-  if (n > 0 && (!x || !ids || !w || !out)) return AFD_ERR_ARG;
+  if (n > 0 && ((!x && !(xq && xs)) || !ids || !w || !out)) return AFD_ERR_ARG;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
   // the gate_up GEMMs address token rows with 32-bit byte offsets
@@ -266,8 +268,10 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
                             ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
     if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
-    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, n, s)
-            : launch_fp8_gate_up(*cfg, *weights, wsb, L, n, s);
+    const uint8_t* aq = x ? wsb + L.xq : xq;
+    const void* as = x ? static_cast<const void*>(wsb + L.xs) : xs;
+    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, aq, as, n, s)
+            : launch_fp8_gate_up(*cfg, *weights, wsb, L, aq, as, n, s);
     if (st != AFD_OK || (st = mark(3)) != AFD_OK) return st;
     st = mx ? launch_mx_down(*cfg, *weights, wsb, L, n, s)
             : launch_fp8_down(*cfg, *weights, wsb, L, n, s);
@@ -286,14 +290,36 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
 extern "C" int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                            const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
                            void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream) {
-  return moe_ffn_impl(cfg, weights, x, ids, w, n, ws, ws_bytes, out, stream, nullptr);
+  if (!x && n > 0) return AFD_ERR_ARG;
+  return moe_ffn_impl(cfg, weights, x, nullptr, nullptr, ids, w, n, ws, ws_bytes, out, stream,
+                      nullptr);
+}
+
+extern "C" int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                             const uint8_t* xq, const void* xs, const int32_t* ids,
+                             const float* w, int32_t n, void* ws, uint64_t ws_bytes,
+                             uint16_t* out, afd_stream_t stream) {
+  if ((!xq || !xs) && n > 0) return AFD_ERR_ARG;
+  return moe_ffn_impl(cfg, weights, nullptr, xq, xs, ids, w, n, ws, ws_bytes, out, stream,
+                      nullptr);
+}
+
+extern "C" int afd_quant_act(const afd_moe_cfg* cfg, const uint16_t* x, int32_t n, uint8_t* q,
+                             void* s, afd_stream_t stream) {
+  int st = check_cfg(cfg);
+  if (st != AFD_OK) return st;
+  if (n < 0 || n > 0x1ffff) return AFD_ERR_ARG;
+  if (n > 0 && (!x || !q || !s)) return AFD_ERR_ARG;
+  return launch_quant_act(*cfg, x, n, q, s, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int afd_moe_ffn_profiled(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                                     const uint16_t* x, const int32_t* ids, const float* w,
                                     int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
                                     afd_stream_t stream, void* const* stage_events) {
-  return moe_ffn_impl(cfg, weights, x, ids, w, n, ws, ws_bytes, out, stream, stage_events);
+  if (!x && n > 0) return AFD_ERR_ARG;
+  return moe_ffn_impl(cfg, weights, x, nullptr, nullptr, ids, w, n, ws, ws_bytes, out, stream,
+                      stage_events);
 }
 
 extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w,

@@ -142,6 +142,20 @@ __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
   if (t == 0) s[(mat * rbs + rb) * cbs + cb] = sc;
 }
 
+int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
+                     hipStream_t stream) {
+  if (n == 0) return AFD_OK;
+  const int64_t items = int64_t(n) * (cfg.hidden / kMxBlock);
+  if (cfg.weight_fmt == AFD_W_MXFP4)
+    hipLaunchKernelGGL(quant_mxfp8_kernel<true>, dim3(grid_for(items)), dim3(kQuantThreads), 0,
+                       stream, x, items, cfg.hidden, q, static_cast<uint8_t*>(s));
+  else
+    hipLaunchKernelGGL(quant_fp8_1x128_kernel, dim3(grid_for(items)), dim3(kQuantThreads), 0,
+                       stream, x, items, cfg.hidden, q, static_cast<float*>(s));
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
 }  // namespace afd
 
 using namespace afd;

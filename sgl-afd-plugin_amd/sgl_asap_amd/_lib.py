@@ -40,8 +40,10 @@ EXPORTED = (
     "afd_pack_fp8_block",
     "afd_quant_mxfp8",
     "afd_quant_fp8_1x128",
+    "afd_quant_act",
     "afd_route",
     "afd_moe_ffn",
+    "afd_moe_ffn_q",
     "afd_moe_ffn_profiled",
     "afd_finalize",
     "afd_combine",
@@ -120,6 +122,11 @@ _SIGS = {
     "afd_route": ([_P, _I32, ctypes.POINTER(AfdMoeCfg), _P, _U64, _P], _I32),
     "afd_moe_ffn": (
         [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _I32, _P, _U64, _P, _P],
+        _I32,
+    ),
+    "afd_quant_act": ([ctypes.POINTER(AfdMoeCfg), _P, _I32, _P, _P, _P], _I32),
+    "afd_moe_ffn_q": (
+        [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _P, _I32, _P, _U64, _P, _P],
         _I32,
     ),
     "afd_moe_ffn_profiled": (

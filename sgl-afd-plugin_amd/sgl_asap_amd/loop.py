@@ -30,20 +30,25 @@ from .transport.server import FfnServer
 
 
 class OneGpuAfd:
-    """``replicas`` A ranks (one replica each, group 1) and one F rank on one GPU. A rank 0's
-    channel is installed as this process's ``AsapBuffer``; the others are driven through
-    ``channels[a]`` directly (``AttnChannel.send`` / ``wait``, pump with ``serve_pending``)."""
+    """``replicas`` x ``group`` A ranks (``group`` A ranks per replica, whose rows form one F
+    job) and one F rank on one GPU. A rank 0's channel is installed as this process's
+    ``AsapBuffer``; the others are driven through ``channels[a]`` directly (``AttnChannel.send`` / ``wait``, pump with ``serve_pending``).
+    ``act``: the activation format on the wire ("bf16", or the experts' "mxfp8" /
+    "fp8_1x128": A quantizes before the copy)."""
 
     def __init__(self, experts: Dict[int, torch.nn.Module], *, n_max: int, slots: int = 2,
-                 replicas: int = 1, seq_base: int = 0, graph_max_tokens: int = 0,
-                 timeout_s: float = 60.0, device: int = 0, reply_stream: bool = True,
+                 replicas: int = 1, group: int = 1, seq_base: int = 0, graph_max_tokens: int = 0,
+                 timeout_s: float = 60.0, device: int = 0, reply_stream: bool = True, act: str = "bf16",
                  timing: bool = False, _backpressure: bool = True,
                  _epoch_override: Optional[int] = None):
         first = next(iter(experts.values()))
         if first.n_max < n_max:
             raise ValueError(f"experts hold workspaces for {first.n_max} tokens, the loop carries up to {n_max}")
-        self.geometry = Geometry(num_a=replicas, group=1, slots=slots, n_max=n_max,
-                                 hidden=first.hidden_size, topk=first.top_k, num_f=1)
+        self.geometry = Geometry(num_a=replicas * group, group=group, slots=slots, n_max=n_max,
+                                 hidden=first.hidden_size, topk=first.top_k, num_f=1, act=act)
+        reads = {str(getattr(layer, "act_format", None)) for layer in experts.values()}
+        if act != "bf16" and reads != {act}:
+            raise ValueError(f"activations on the wire as {act}, but the experts read {sorted(reads)}")
         self.server = FfnServer(0, self.geometry, device=device, seq_base=seq_base).start()
         self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens,
                                       reply_stream=reply_stream, timing=timing)
@@ -51,7 +56,7 @@ class OneGpuAfd:
             AttnChannel(a, self.geometry, [self.server], device=device, seq_base=seq_base,
                         timeout_s=timeout_s, _backpressure=_backpressure,
                         _epoch_override=_epoch_override).connect()
-            for a in range(replicas)
+            for a in range(replicas * group)
         ]
         self.channel = self.channels[0]
         self.buffer = AsapBuffer.install(self.channel, device, pump=self.scheduler.serve_pending)

@@ -14,6 +14,10 @@ The sum is one gfx950 kernel (``afd_combine``) that can also add the shared expe
 roundings as the reference's recv followed by SGLang's plain shared add
 (``srt/layers/moe/ep_moe/layer.py:29-33``).
 
+With fp8 activations on the wire (the channel geometry's ``act``) ``send`` quantizes the
+rows on the send stream first (``quant_act``, the expert call's own quantizer) and copies the
+e4m3 codes and their scales: half the bytes of bf16, and the F rank skips its quantizer.
+
 On one GPU the F rank is in-process: ``AsapBuffer.pump`` (if set) is called before a wait
 is enqueued so the F side has enqueued its job first, which keeps host order equal to causal
 order on the device (no stream can ever wait on work that is enqueued after it).
@@ -27,6 +31,7 @@ from typing import Callable, NamedTuple, Optional
 import torch
 
 from .. import _lib
+from .experts import act_scale_shape, quant_act
 from .topk import format_is_standard
 
 # The slot of a whole batch; micro-batch i of two-batch overlap uses slot i.
@@ -94,6 +99,18 @@ class AsapBuffer:
         self.hidden = channel.g.hidden
         self.send_stream = torch.cuda.Stream(device)
         self.pump = pump
+        self.act = channel.g.act
+        self.stage = []
+        if self.act != "bf16":
+            # fp8 on the wire: one staging pair per slot; the send stream quantizes a message's
+            # rows here, then copies them to the arena. The slot's next message quantizes after
+            # those copies (same stream), so one pair per slot suffices.
+            shape, dtype = act_scale_shape(self.act, self.n_max, self.hidden)
+            self.stage = [
+                (torch.empty(self.n_max, self.hidden, dtype=torch.uint8, device=device),
+                 torch.empty(shape, dtype=dtype, device=device))
+                for _ in range(channel.g.slots)
+            ]
 
     @classmethod
     def get(cls) -> "AsapBuffer":
@@ -119,8 +136,17 @@ class AsapBuffer:
         ids = ids.to(torch.int32).contiguous()
         weights = weights.to(torch.float32).contiguous()
         slot = SLOT if micro_batch is None else micro_batch
+        n = x.shape[0]
         self.send_stream.wait_stream(torch.cuda.current_stream())
-        ticket = self.channel.send(layer_id, slot, x.data_ptr(), ids.data_ptr(), weights.data_ptr(), x.shape[0], self.send_stream)
+        x_ptr, xs_ptr = x.data_ptr(), 0
+        if self.stage:
+            if not (0 <= slot < len(self.stage) and 1 <= n <= self.n_max):
+                raise ValueError(f"slot {slot} / n_tokens {n} outside the geometry {self.channel.g}")
+            q, s = self.stage[slot]
+            quant_act(self.act, x, q[:n], s[:n], stream=self.send_stream)
+            x_ptr, xs_ptr = q.data_ptr(), s.data_ptr()
+        ticket = self.channel.send(layer_id, slot, x_ptr, ids.data_ptr(), weights.data_ptr(), n, self.send_stream,
+                                   xs_ptr=xs_ptr)
         for t in (x, ids, weights):  # the caching allocator must not hand them out before the copies ran
             t.record_stream(self.send_stream)
         return ticket, (x, ids, weights)

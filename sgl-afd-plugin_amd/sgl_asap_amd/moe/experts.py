@@ -141,6 +141,52 @@ def moe_cfg(
     )
 
 
+# activation formats of the expert call's input -> the weight format whose GEMMs read them
+ACT_FORMATS = {"mxfp8": "mxfp4", "fp8_1x128": "fp8_block"}
+
+
+def act_scale_shape(act: str, n: int, hidden: int):
+    """Shape and dtype of the scales of n tokens in activation format ``act``: "mxfp8" has
+    hidden/32 UE8M0 bytes per token (each 128-wide K stage's four as blocks 0, 2, 1, 3),
+    "fp8_1x128" hidden/128 fp32."""
+    if act == "mxfp8":
+        return (n, hidden // 32), torch.uint8
+    if act == "fp8_1x128":
+        return (n, hidden // 128), torch.float32
+    raise ValueError(f"activation format {act!r} (supported: {sorted(ACT_FORMATS)})")
+
+
+def quant_act(act: str, x: torch.Tensor, q: Optional[torch.Tensor] = None, s: Optional[torch.Tensor] = None,
+              stream: Optional[torch.cuda.Stream] = None):
+    """afd_quant_act without a layer: bf16 x [n, H] -> (e4m3 codes uint8 [n, H], scales), the
+    input of afd_moe_ffn_q for experts of the matching weight format. The quantizer reads only
+    the hidden size and the weight format of its configuration, so an attention rank, which
+    holds no expert weights, quantizes its rows before the arena copy with this."""
+    if act not in ACT_FORMATS:
+        raise ValueError(f"activation format {act!r} (supported: {sorted(ACT_FORMATS)})")
+    if x.dtype != torch.bfloat16 or x.dim() != 2:
+        raise TypeError(f"quant_act takes bf16 [n, H] activations, got {x.dtype} {tuple(x.shape)}")
+    n, hidden = x.shape
+    cfg = _lib.AfdMoeCfg(hidden, 128, 1, 0, 1, WEIGHT_FORMATS[ACT_FORMATS[act]], ACTIVATIONS["silu"], 0.0, 0.0)
+    return _quant_act(cfg, act, x, q, s, stream)
+
+
+def _quant_act(cfg, act, x, q, s, stream):
+    x = x.contiguous()
+    n, hidden = x.shape
+    shape, dtype = act_scale_shape(act, n, hidden)
+    q = torch.empty(n, hidden, dtype=torch.uint8, device=x.device) if q is None else q
+    s = torch.empty(shape, dtype=dtype, device=x.device) if s is None else s
+    if q.dtype != torch.uint8 or tuple(q.shape) != (n, hidden) or not q.is_contiguous():
+        raise ValueError(f"q must be contiguous uint8 [{n}, {hidden}], got {q.dtype} {tuple(q.shape)}")
+    if s.dtype != dtype or tuple(s.shape) != shape or not s.is_contiguous():
+        raise ValueError(f"s must be contiguous {dtype} {shape}, got {s.dtype} {tuple(s.shape)}")
+    if n > 0:
+        _lib.call("afd_quant_act", ctypes.byref(cfg), x.data_ptr(), n, q.data_ptr(), s.data_ptr(),
+                  _stream_handle(stream))
+    return q, s
+
+
 def workspace_layout(cfg: _lib.AfdMoeCfg, n: int) -> dict:
     """afd_workspace_layout as a dict of byte offsets (plus np_max, block_m, max_tiles)."""
     out = _lib.AfdWsLayout()
@@ -195,22 +241,24 @@ class AfdExperts(torch.nn.Module):
             self._ws[s.cuda_stream] = ws
         return ws
 
-    def forward(self, hidden_states: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):
+    def _topk(self, n: int, topk_output):
         if not format_is_standard(topk_output):
             raise RuntimeError(f"expected explicit top-k ids and weights, got {type(topk_output).__name__}")
-        x = hidden_states
-        if x.dtype != torch.bfloat16:
-            raise TypeError(f"the expert path takes bf16 activations, got {x.dtype}")
-        n = x.shape[0]
         if n > self.n_max:
             raise ValueError(f"{n} tokens exceed n_max={self.n_max}")
         ids = topk_output.topk_ids
         w = topk_output.topk_weights
         if ids.shape != (n, self.top_k) or w.shape != (n, self.top_k):
             raise ValueError(f"top-k shapes {tuple(ids.shape)} / {tuple(w.shape)} for {n} tokens, k={self.top_k}")
+        return ids.to(torch.int32).contiguous(), w.to(torch.float32).contiguous()
+
+    def forward(self, hidden_states: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):
+        x = hidden_states
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"the expert path takes bf16 activations, got {x.dtype}")
+        n = x.shape[0]
+        ids, w = self._topk(n, topk_output)
         x = x.contiguous()
-        ids = ids.to(torch.int32).contiguous()
-        w = w.to(torch.float32).contiguous()
         if out is None:
             out = torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=x.device)
         if n == 0:
@@ -221,6 +269,55 @@ class AfdExperts(torch.nn.Module):
             ctypes.byref(self.cfg),
             ctypes.byref(self._wstruct),
             x.data_ptr(),
+            ids.data_ptr(),
+            w.data_ptr(),
+            n,
+            ws.data_ptr(),
+            ws.numel(),
+            out.data_ptr(),
+            _stream_handle(),
+        )
+        return out
+
+    # ---- fp8 activations on the wire: A quantizes, F runs on the quantized rows ----
+    @property
+    def act_format(self) -> str:
+        """The activation format of this layer's expert call: "mxfp8" (e4m3 + UE8M0 per 32,
+        MXFP4 weights) or "fp8_1x128" (e4m3 + fp32 per 128, FP8 block weights)."""
+        return "mxfp8" if self.weights.fmt == "mxfp4" else "fp8_1x128"
+
+    def act_scale_shape(self, n: int):
+        """Shape and dtype of the activation scales of n tokens."""
+        return act_scale_shape(self.act_format, n, self.hidden_size)
+
+    def quant_act(self, x: torch.Tensor, q: Optional[torch.Tensor] = None, s: Optional[torch.Tensor] = None):
+        """The expert call's activation quantization on its own (afd_quant_act), on the current
+        stream: bf16 x [n, H] -> (q e4m3 codes uint8 [n, H], s scales)."""
+        if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.hidden_size:
+            raise TypeError(f"the expert path takes bf16 [n, {self.hidden_size}] activations, got {x.dtype} {tuple(x.shape)}")
+        return _quant_act(self.cfg, self.act_format, x, q, s, None)
+
+    def forward_q(self, xq: torch.Tensor, xs: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):
+        """The expert call on activations quant_act (or the A side) already quantized
+        (afd_moe_ffn_q); bit-identical to ``forward`` on the bf16 rows they came from."""
+        n = xq.shape[0]
+        shape, dtype = self.act_scale_shape(n)
+        if xq.dtype != torch.uint8 or tuple(xq.shape) != (n, self.hidden_size):
+            raise ValueError(f"xq must be uint8 [{n}, {self.hidden_size}], got {xq.dtype} {tuple(xq.shape)}")
+        if xs.dtype != dtype or tuple(xs.shape) != shape:
+            raise ValueError(f"xs must be {dtype} {shape}, got {xs.dtype} {tuple(xs.shape)}")
+        ids, w = self._topk(n, topk_output)
+        if out is None:
+            out = torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=xq.device)
+        if n == 0:
+            return out
+        ws = self.workspace()
+        _lib.call(
+            "afd_moe_ffn_q",
+            ctypes.byref(self.cfg),
+            ctypes.byref(self._wstruct),
+            xq.contiguous().data_ptr(),
+            xs.contiguous().data_ptr(),
             ids.data_ptr(),
             w.data_ptr(),
             n,

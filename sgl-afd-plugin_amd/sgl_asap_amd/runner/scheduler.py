@@ -11,6 +11,8 @@ bucket, from events read lazily).
 Differences on one GPU: the experts run on the scheduler's own stream, which first parks
 on the job's doorbells (``FfnServer.wait_rows``), so the host never waits; an eager job
 writes its output straight into A's result segment, so its reply is the done flag alone.
+With fp8 activations on the wire (``Geometry.act``) the rows arrive as e4m3 codes plus
+scales and the job runs the expert call on them as they are (``forward_q``).
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ from typing import Dict, Optional
 
 import torch
 
+from ..moe.experts import act_scale_shape
 from ..moe.topk import StandardTopKOutput
 from .graph_runner import FfnGraphRunner, graph_buckets
 
@@ -96,7 +99,7 @@ class FfnScheduler:
         self.graph_runner: Optional[FfnGraphRunner] = None
         if graph_max_tokens:
             with torch.cuda.stream(self.stream):
-                self.graph_runner = FfnGraphRunner(experts, graph_max_tokens, self.local)
+                self.graph_runner = FfnGraphRunner(experts, graph_max_tokens, self.local, act=self.g.act)
 
     @torch.no_grad()
     def warmup(self, n_max: int) -> list:
@@ -120,10 +123,17 @@ class FfnScheduler:
         return buckets
 
     def rows_of(self, row):
-        """x, topk_ids and topk_weights of one row: views into the RecvArena."""
+        """x, topk_ids and topk_weights of one row: views into the RecvArena. x is a tuple:
+        (bf16 [n, H],) or, with fp8 activations on the wire, (e4m3 codes, scales)."""
         g, arena = self.g, self.server.recv
         n, off = row.n_tokens, row.x_ptr - self.server.recv_base
-        x = arena[off : off + n * g.hidden * 2].view(torch.bfloat16).view(n, g.hidden)
+        if g.act == "bf16":
+            x = (arena[off : off + n * g.hidden * 2].view(torch.bfloat16).view(n, g.hidden),)
+        else:
+            shape, dtype = act_scale_shape(g.act, n, g.hidden)
+            xs_off = off + g.xs_off
+            x = (arena[off : off + n * g.hidden].view(n, g.hidden),
+                 arena[xs_off : xs_off + n * g.xs_bytes_per_token].view(dtype).view(shape))
         ids_off, w_off = off + g.ids_off, off + g.w_off
         topk_ids = arena[ids_off : ids_off + n * g.topk * 4].view(torch.int32).view(n, g.topk)
         topk_weights = arena[w_off : w_off + n * g.topk * 4].view(torch.float32).view(n, g.topk)
@@ -141,10 +151,12 @@ class FfnScheduler:
             if len(rows) == 1:
                 x, topk_ids, topk_weights = rows[0]
             else:
-                x, topk_ids, topk_weights = (torch.cat(part) for part in zip(*rows))
+                x = tuple(torch.cat(part) for part in zip(*(r[0] for r in rows)))
+                topk_ids, topk_weights = (torch.cat(part) for part in zip(*(r[1:] for r in rows)))
+            n = topk_ids.shape[0]
             output, buffer = None, 0
             reply = self.reply_stream
-            if self.graph_runner is not None and x.shape[0] <= self.graph_runner.buckets[-1]:
+            if self.graph_runner is not None and n <= self.graph_runner.buckets[-1]:
                 if reply is not None:
                     buffer = self.reply_turn
                     # the reply that last read this buffer, before the replay overwrites it
@@ -156,7 +168,11 @@ class FfnScheduler:
                 out = None
                 if len(job.rows) == 1:  # write the partial sum straight into A's segment
                     out = self.server.seg_view(job.rows[0])
-                output = self.experts[job.layer_id](x, topk_output, out=out)
+                layer = self.experts[job.layer_id]
+                if len(x) == 1:
+                    output = layer(x[0], topk_output, out=out)
+                else:  # fp8 on the wire: the rows are quantized already
+                    output = layer.forward_q(*x, topk_output, out=out)
             experts_done = timer.event(stream) if timer else None
         if reply is None:
             rstream = stream
@@ -174,7 +190,7 @@ class FfnScheduler:
             self.reply_free[buffer].record(reply)
             self.reply_turn = 1 - buffer
         if timer:
-            timer.add(x.shape[0], started, experts_done, timer.event(rstream), time.perf_counter() - tic)
+            timer.add(n, started, experts_done, timer.event(rstream), time.perf_counter() - tic)
 
     def serve_pending(self) -> int:
         """Poll once and run every complete job (the one-GPU form of serve_forever)."""

@@ -25,7 +25,6 @@ from typing import Callable, List, Optional, Sequence, Tuple
 
 from . import hip
 from .layout import (
-    ACT_BYTES,
     ID_BYTES,
     SEQ_MASK,
     ChannelPoisoned,
@@ -206,16 +205,22 @@ class AttnChannel:
     def seg_ptr(self, f: int, slot: int) -> int:
         return self.segments.data_ptr() + self.g.seg_off(f, slot) - self.g.flags_bytes
 
-    def send(self, layer_id: int, slot: int, x_ptr: int, ids_ptr: int, w_ptr: int, n_tokens: int, stream) -> Ticket:
+    def send(self, layer_id: int, slot: int, x_ptr: int, ids_ptr: int, w_ptr: int, n_tokens: int, stream,
+             xs_ptr: int = 0) -> Ticket:
         """Enqueue one message on ``stream`` (a torch stream): ``n_tokens`` rows of x (bf16
-        [n, hidden]), top-k ids (int32 [n, topk]) and weights (fp32 [n, topk]) to every F rank."""
+        [n, hidden]), top-k ids (int32 [n, topk]) and weights (fp32 [n, topk]) to every F rank.
+        With fp8 activations on the wire (``g.act`` != "bf16") x_ptr holds the e4m3 codes
+        [n, hidden] and xs_ptr their scales [n, g.xs_bytes_per_token bytes]."""
         self.check()
         g = self.g
         if not (0 <= slot < g.slots and 1 <= n_tokens <= g.n_max):
             raise ValueError(f"slot {slot} / n_tokens {n_tokens} outside the geometry {g}")
+        if (g.act != "bf16") != bool(xs_ptr):
+            raise ValueError(f"activation format {g.act} {'needs' if xs_ptr == 0 else 'takes no'} scales")
         seq = self._seq[slot] = (self._seq[slot] + 1) & SEQ_MASK
         sh = stream.cuda_stream
-        x_n, k_n = n_tokens * g.hidden * ACT_BYTES, n_tokens * g.topk * ID_BYTES
+        x_n, k_n = n_tokens * g.x_bytes_per_token, n_tokens * g.topk * ID_BYTES
+        xs_n = n_tokens * g.xs_bytes_per_token
         if self._backpressure:  # the previous message of this slot must be answered first
             for f in range(g.num_f):
                 hip.wait64(sh, self.flags.addr(g.done_off(f, slot)), (seq - 1) & SEQ_MASK)
@@ -223,6 +228,8 @@ class AttnChannel:
             epoch = self._epoch[f] if self._epoch_override is None else self._epoch_override
             dst = self._recv[f] + g.region_off(self.a, slot)
             hip.copy_async(dst, x_ptr, x_n, sh)
+            if xs_n:
+                hip.copy_async(dst + g.xs_off, xs_ptr, xs_n, sh)
             hip.copy_async(dst + g.ids_off, ids_ptr, k_n, sh)
             hip.copy_async(dst + g.w_off, w_ptr, k_n, sh)  # fp32 weights: the size of the int32 ids
             word = pack_doorbell(seq, n_tokens, layer_id, epoch)

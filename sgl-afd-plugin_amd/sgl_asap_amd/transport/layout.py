@@ -18,6 +18,13 @@ RecvArena (device memory, F owns), one region per (a, s):
     | x [n_max, hidden] bf16 | ids [n_max, topk] i32 | w [n_max, topk] f32 |
     0                      ids_off                 w_off            region_bytes
 
+With ``act`` = "mxfp8" or "fp8_1x128" (fp8 activations on the wire, the reference's TODO at
+scripts/run_asap.sh:110-111) A quantizes before the copy and the x field becomes
+    | xq [n_max, hidden] e4m3 | xs [n_max, scale_bytes/token] | ids ... | w ... |
+    0                        xs_off                          ids_off
+where a token's scales are hidden/32 UE8M0 bytes ("mxfp8", the MXFP4 experts' input) or
+hidden/128 fp32 ("fp8_1x128", the FP8 block experts' input). Results stay bf16.
+
 Flags (doorbells of F, done flags of A): one 64-byte line per flag. This build keeps
 them in pinned host memory so a host thread can always release a parked stream wait
 with a plain store; the offsets are the reference's.
@@ -38,6 +45,7 @@ FLAG_STRIDE = 64
 FLAGS_PAGE = 2 << 20
 BELL_STRIDE = 64
 ACT_BYTES = 2  # bf16 activations on the wire
+ACT_FORMATS = ("bf16", "mxfp8", "fp8_1x128")
 ID_BYTES = 4  # int32 global expert ids
 W_BYTES = 4  # fp32 top-k weights
 
@@ -105,7 +113,9 @@ def seq_ahead(new: int, last: int) -> int:
 
 @dataclass(frozen=True)
 class Geometry:
-    """Sizes of one deployment (layout.py:116-198). Every field is a positive int."""
+    """Sizes of one deployment (layout.py:116-198). Every field but ``act`` is a positive
+    int; ``act`` is the activation format on the wire (one of ACT_FORMATS, default bf16,
+    which keeps the reference's layout byte for byte)."""
 
     num_a: int  # A ranks (replicas x group)
     group: int  # A ranks of one replica; their rows form one F job
@@ -114,24 +124,50 @@ class Geometry:
     hidden: int
     topk: int
     num_f: int  # F ranks
+    act: str = "bf16"
 
     def __post_init__(self):
         bad = []
         for f in fields(self):
+            if f.name == "act":
+                continue
             v = getattr(self, f.name)
             if not isinstance(v, int) or isinstance(v, bool) or v < 1:
                 bad.append(f"{f.name}={v!r}")
+        if self.act not in ACT_FORMATS:
+            bad.append(f"act={self.act!r} is not one of {ACT_FORMATS}")
         if not bad and self.num_a % self.group:
             bad.append(f"num_a={self.num_a} is not a multiple of group={self.group}")
         if not bad and self.n_max > MAX_TOKENS:
             bad.append(f"n_max={self.n_max} exceeds the {MAX_TOKENS} tokens a doorbell can announce")
+        if not bad and self.act != "bf16" and self.hidden % 128:
+            bad.append(f"act={self.act} needs hidden={self.hidden} to be a multiple of 128")
         if bad:
             raise ValueError("invalid transport geometry: " + ", ".join(bad))
 
+    # activations on the wire
+    @property
+    def x_bytes_per_token(self) -> int:
+        """Bytes of one token's codes in the x field (bf16: 2 per element, fp8: 1)."""
+        return self.hidden * (ACT_BYTES if self.act == "bf16" else 1)
+
+    @property
+    def xs_bytes_per_token(self) -> int:
+        """Bytes of one token's activation scales (0 for bf16)."""
+        if self.act == "mxfp8":
+            return self.hidden // 32
+        if self.act == "fp8_1x128":
+            return self.hidden // 128 * 4
+        return 0
+
     # RecvArena of an F rank
     @property
+    def xs_off(self) -> int:
+        return align_up(self.n_max * self.x_bytes_per_token)
+
+    @property
     def ids_off(self) -> int:
-        return align_up(self.n_max * self.hidden * ACT_BYTES)
+        return self.xs_off + align_up(self.n_max * self.xs_bytes_per_token)
 
     @property
     def w_off(self) -> int:
@@ -180,4 +216,4 @@ class Geometry:
 
     @classmethod
     def from_dict(cls, d: dict) -> "Geometry":
-        return cls(**{f.name: d[f.name] for f in fields(cls)})
+        return cls(**{f.name: d[f.name] for f in fields(cls) if f.name in d or f.name != "act"})

@@ -92,6 +92,40 @@ def test_geometry_matches_oracle_restatement():
             assert getattr(g, name) == o[name], name
 
 
+def test_geometry_bf16_default_is_the_reference_layout():
+    g = L.Geometry(num_a=1, group=1, slots=2, n_max=8192, hidden=4096, topk=8, num_f=1)
+    assert g.act == "bf16" and g.xs_bytes_per_token == 0
+    assert g.xs_off == g.ids_off == 8192 * 4096 * 2
+    d = g.as_dict()
+    del d["act"]  # a peer that predates the field
+    assert L.Geometry.from_dict(d) == g
+
+
+@pytest.mark.parametrize("act", ["mxfp8", "fp8_1x128"])
+def test_geometry_fp8_on_the_wire(act):
+    # n_max 8192, hidden 4096, topk 8: codes 32 MiB, scales 128 B/token (4096/32 UE8M0 bytes,
+    # or 4096/128 fp32) = 1 MiB, ids and weights 256 KiB each
+    g = L.Geometry(num_a=1, group=1, slots=2, n_max=8192, hidden=4096, topk=8, num_f=1, act=act)
+    assert g.x_bytes_per_token == 4096 and g.xs_bytes_per_token == 128
+    assert g.xs_off == 33_554_432
+    assert g.ids_off == 34_603_008
+    assert g.w_off == 34_865_152
+    assert g.region_bytes == 35_127_296
+    assert g.seg_bytes == 67_108_864  # results stay bf16
+    assert L.Geometry.from_dict(g.as_dict()) == g
+    # odd sizes: every field starts on a 256-byte boundary
+    g = L.Geometry(num_a=1, group=1, slots=1, n_max=3, hidden=384, topk=3, num_f=1, act=act)
+    assert g.xs_bytes_per_token == 12  # 384/32 bytes, or 3 fp32
+    assert (g.xs_off, g.ids_off) == (1280, 1280 + 256)
+
+
+@pytest.mark.parametrize("kw", [dict(act="fp16"), dict(act="mxfp8", hidden=200), dict(act=None)])
+def test_geometry_rejects_act(kw):
+    base = dict(num_a=1, group=1, slots=1, n_max=4, hidden=256, topk=1, num_f=1)
+    with pytest.raises(ValueError):
+        L.Geometry(**{**base, **kw})
+
+
 def test_seq_ahead_cyclic():
     assert L.seq_ahead(5, 0xFFFFFFFE) == 7
     assert L.seq_ahead(0xFFFFFFFE, 5) == -7
@@ -208,6 +242,9 @@ def test_hello_rejects_geometry_mismatch():
         s.hello(0, None, None, other)
     with pytest.raises(L.HandshakeError):
         s.hello(5, None, None, g)
+    fp8 = L.Geometry(**{**g.as_dict(), "act": "mxfp8"})  # same sizes, other wire format
+    with pytest.raises(L.HandshakeError):
+        s.hello(0, None, None, fp8)
 
 
 def test_server_matches_oracle_poll_on_random_streams():
