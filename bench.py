@@ -77,21 +77,26 @@ def _short(name: str) -> str:
 def pmc_summary(fetch_csv: str, write_csv: str, copy_mib: int, out_path) -> dict:
     """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled so that the
     plain copy kernel of the same run reads and writes exactly ``copy_mib`` MiB."""
-    per = {}
+    per, copy_kib = {}, {}
+    copy_grid = copy_mib * (1 << 20) // 4 // 4  # fp32 elements, 4 per lane of the copy kernel
     for which, path in (("fetch", fetch_csv), ("write", write_csv)):
-        acc = {}
+        acc, cal = {}, []
         for r in _csv_rows(path):
             acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+            # the calibration copy: torch's neg over copy_mib MiB (other, smaller neg launches of
+            # the input generators share its name, so it is told apart by its grid)
+            if "neg_kernel" in r["Kernel_Name"] and int(r["Grid_Size"]) == copy_grid:
+                cal.append(float(r["Counter_Value"]))
+        if not cal:
+            raise SystemExit(f"no {copy_mib} MiB copy kernel (torch neg, grid {copy_grid}) in {path}")
         per[which] = {k: sum(v) / len(v) for k, v in acc.items()}
-    copy = [k for k in per["fetch"] if "neg_kernel" in k]
-    if len(copy) != 1:
-        raise SystemExit(f"expected exactly one copy kernel (torch neg) in {fetch_csv}, found {copy}")
+        copy_kib[which] = sum(cal) / len(cal)
     known_kib = copy_mib * 1024.0
-    f_fetch = known_kib / per["fetch"][copy[0]]
-    f_write = known_kib / per["write"][copy[0]]
+    f_fetch = known_kib / copy_kib["fetch"]
+    f_write = known_kib / copy_kib["write"]
     kernels = {}
     for k in per["fetch"]:
-        if "afd::" not in k and k != copy[0]:
+        if "afd::" not in k:
             continue
         fb = per["fetch"][k] * f_fetch * 1024
         wb = per["write"].get(k, 0.0) * f_write * 1024

@@ -26,6 +26,9 @@
  *                                operations_strategy.py:106-111)
  *   afd_pack_mxfp4 / _fp8_block  the quant methods' weight repack at load time
  *                                (FlashInfer layout, mxfp4_flashinfer_trtllm_moe.py:11-13)
+ *   afd_repack_mxfp4 / ......... the checkpoint expert load (P/srt/model_loader/weight_utils.py
+ *   _fp8_block                   :27-54 selects the tensors, SGLang's FusedMoE weight_loader
+ *                                stores them; MXFP4 layout of P/srt/configs/model_config.py:3-7)
  *   afd_copy_async ............. cu.memcpy_async (P/transport/cuda_wrapper.py, used at
  *                                P/transport/channel.py:345-349, P/transport/server.py:347)
  *   afd_stream_write64 ......... cu.write64 / write32 (cuda_wrapper.py:258-270; doorbell at
@@ -147,6 +150,19 @@ int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols, int
                    uint8_t* out, afd_stream_t stream);
 int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
                        int32_t gate_up, uint8_t* q, float* s, afd_stream_t stream);
+
+/* ---- checkpoint repack (load time): already-quantized experts, bytes moved unchanged -----
+ * afd_repack_mxfp4: codes u8 [mats][rows][cols/2] int8-packed e2m1 (element 2i in the low
+ * nibble) + scales u8 [mats][rows][cols/32] E8M0, the checkpoint layout -> the tile images
+ * afd_pack_mxfp4 writes (same size, same limits), holding the checkpoint's codes and scales
+ * exactly. afd_repack_fp8_block: codes e4m3 [mats][rows][cols] -> the kernel's row order
+ * (with gate_up = 1 the 32-row gate/up interleave, else a copy; rows a multiple of 128, of
+ * 256 with gate_up; cols of 128); the fp32 128x128 block scales keep their logical order and
+ * are used as they are. Pointers 16-byte aligned. */
+int afd_repack_mxfp4(const uint8_t* codes, const uint8_t* scales, int64_t mats, int32_t rows,
+                     int32_t cols, int32_t gate_up, uint8_t* out, afd_stream_t stream);
+int afd_repack_fp8_block(const uint8_t* q, int64_t mats, int32_t rows, int32_t cols,
+                         int32_t gate_up, uint8_t* out, afd_stream_t stream);
 
 /* ---- activation quantizers -------------------------------------------------------------
  * x: bf16 [rows][cols]. MXFP8: q e4m3 [rows][cols], s u8 [rows][cols/32].

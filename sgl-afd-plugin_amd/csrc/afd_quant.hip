@@ -142,6 +142,50 @@ __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
   if (t == 0) s[(mat * rbs + rb) * cbs + cb] = sc;
 }
 
+// ---------------------------------------------------------------- checkpoint repack
+// Checkpoint MXFP4 experts are already e2m1 codes (two per byte, element 2i in the low
+// nibble) with one E8M0 scale per 32: a 32-element block is 16 contiguous code bytes, i.e.
+// one 16-byte chunk of a B image. One lane per block of a physical row moves the chunk and
+// its scale byte to where afd_pack_mxfp4 would have written them; nothing is requantized.
+__global__ __launch_bounds__(kQuantThreads) void repack_mxfp4_kernel(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales, int64_t blocks,
+    int rows, int cols, int gate_up, uint8_t* __restrict__ out) {
+  const int bpr = cols / kMxBlock;
+  const int kstages = cols / kImgK, ntiles = rows / kImgBRows;
+  for (int64_t b = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; b < blocks;
+       b += int64_t(gridDim.x) * kQuantThreads) {
+    int64_t prow = b / bpr;
+    int cb = static_cast<int>(b % bpr);
+    int64_t mat = prow / rows;
+    int r = static_cast<int>(prow % rows);
+    int64_t src = mat * rows + (gate_up ? gate_up_source_row(r, rows, 32) : r);
+    v4i chunk = *reinterpret_cast<const v4i*>(codes + src * (cols / 2) + cb * 16);
+    uint8_t code = scales[src * bpr + cb];
+    const int nt = r / kImgBRows, n = r % kImgBRows;
+    const int ks = cb / 4, j = cb % 4;
+    uint8_t* img = out + ((mat * ntiles + nt) * kstages + ks) * int64_t(kImgB);
+    *reinterpret_cast<v4i*>(img + img_b_off(n, j)) = chunk;
+    img[kImgData + n * 4 + scale_byte(j)] = code;
+  }
+}
+
+// Checkpoint FP8 block experts: e4m3 rows moved into the kernel's row order, 16 bytes a lane.
+__global__ __launch_bounds__(kQuantThreads) void repack_fp8_rows_kernel(
+    const uint8_t* __restrict__ q, int64_t chunks, int rows, int cols, int gate_up,
+    uint8_t* __restrict__ out) {
+  const int cpr = cols / 16;
+  for (int64_t c = blockIdx.x * int64_t(kQuantThreads) + threadIdx.x; c < chunks;
+       c += int64_t(gridDim.x) * kQuantThreads) {
+    int64_t prow = c / cpr;
+    int j = static_cast<int>(c % cpr);
+    int64_t mat = prow / rows;
+    int r = static_cast<int>(prow % rows);
+    int64_t src = mat * rows + (gate_up ? gate_up_source_row(r, rows, 32) : r);
+    *reinterpret_cast<v4i*>(out + prow * cols + j * 16) =
+        *reinterpret_cast<const v4i*>(q + src * cols + j * 16);
+  }
+}
+
 int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
                      hipStream_t stream) {
   if (n == 0) return AFD_OK;
@@ -208,6 +252,38 @@ extern "C" int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, in
   hipLaunchKernelGGL(pack_fp8_block_kernel, dim3(static_cast<unsigned>(blocks)),
                      dim3(kQuantThreads), 0, static_cast<hipStream_t>(stream), w, rows, cols,
                      gate_up ? 1 : 0, q, s);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+extern "C" int afd_repack_mxfp4(const uint8_t* codes, const uint8_t* scales, int64_t mats,
+                                int32_t rows, int32_t cols, int32_t gate_up, uint8_t* out,
+                                afd_stream_t stream) {
+  if (!codes || !scales || !out || mats < 0) return AFD_ERR_ARG;
+  if (!aligned16(codes) || !aligned16(out)) return AFD_ERR_ARG;
+  if (rows <= 0 || cols <= 0 || rows % kImgBRows || cols % kImgK) return AFD_ERR_SHAPE;
+  if (mats == 0) return AFD_OK;
+  int64_t blocks = mats * rows * (cols / kMxBlock);
+  hipLaunchKernelGGL(repack_mxfp4_kernel, dim3(grid_for(blocks)), dim3(kQuantThreads), 0,
+                     static_cast<hipStream_t>(stream), codes, scales, blocks, rows, cols,
+                     gate_up ? 1 : 0, out);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+extern "C" int afd_repack_fp8_block(const uint8_t* q, int64_t mats, int32_t rows, int32_t cols,
+                                    int32_t gate_up, uint8_t* out, afd_stream_t stream) {
+  if (!q || !out || mats < 0) return AFD_ERR_ARG;
+  if (!aligned16(q) || !aligned16(out)) return AFD_ERR_ARG;
+  if (rows <= 0 || cols <= 0 || rows % kFp8Block || cols % kFp8Block) return AFD_ERR_SHAPE;
+  if (gate_up && rows % 256) return AFD_ERR_SHAPE;
+  if (mats == 0) return AFD_OK;
+  int64_t chunks = mats * rows * (cols / 16);
+  hipLaunchKernelGGL(repack_fp8_rows_kernel, dim3(grid_for(chunks)), dim3(kQuantThreads), 0,
+                     static_cast<hipStream_t>(stream), q, chunks, rows, cols, gate_up ? 1 : 0,
+                     out);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }

@@ -38,6 +38,8 @@ EXPORTED = (
     "afd_workspace_layout",
     "afd_pack_mxfp4",
     "afd_pack_fp8_block",
+    "afd_repack_mxfp4",
+    "afd_repack_fp8_block",
     "afd_quant_mxfp8",
     "afd_quant_fp8_1x128",
     "afd_quant_act",
@@ -117,6 +119,8 @@ _SIGS = {
     "afd_workspace_layout": ([ctypes.POINTER(AfdMoeCfg), _I32, ctypes.POINTER(AfdWsLayout)], _I32),
     "afd_pack_mxfp4": ([_P, _I64, _I32, _I32, _I32, _P, _P], _I32),
     "afd_pack_fp8_block": ([_P, _I64, _I32, _I32, _I32, _P, _P, _P], _I32),
+    "afd_repack_mxfp4": ([_P, _P, _I64, _I32, _I32, _I32, _P, _P], _I32),
+    "afd_repack_fp8_block": ([_P, _I64, _I32, _I32, _I32, _P, _P], _I32),
     "afd_quant_mxfp8": ([_P, _I64, _I32, _P, _P, _P], _I32),
     "afd_quant_fp8_1x128": ([_P, _I64, _I32, _P, _P, _P], _I32),
     "afd_route": ([_P, _I32, ctypes.POINTER(AfdMoeCfg), _P, _U64, _P], _I32),

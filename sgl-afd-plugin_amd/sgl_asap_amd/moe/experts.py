@@ -109,6 +109,65 @@ def pack_fp8_block_experts(w13: torch.Tensor, w2: torch.Tensor, device=None) -> 
     return ExpertWeights("fp8_block", e, h, inter, q13, s13, q2, s2)
 
 
+def _bytes_on(t: torch.Tensor, device) -> torch.Tensor:
+    """A 1-byte-element tensor (uint8 / int8 / float8 codes) as contiguous uint8 on device."""
+    if t.element_size() != 1:
+        raise TypeError(f"expected 1-byte codes, got {t.dtype}")
+    return t.contiguous().view(torch.uint8).to(device)
+
+
+def repack_mxfp4_experts(w13: torch.Tensor, s13: torch.Tensor, w2: torch.Tensor, s2: torch.Tensor,
+                         device=None) -> ExpertWeights:
+    """Already-quantized MXFP4 experts (a checkpoint's int8-packed e2m1 codes and E8M0 scales,
+    ``srt/configs/model_config.py:3-7``) into the kernel's tile images, bytes unchanged.
+
+    w13: [E, 2I, H/2] codes with rows [gate; up], s13: [E, 2I, H/32]; w2: [E, H, I/2],
+    s2: [E, H, I/32]. Any 1-byte dtypes (uint8, int8, float8_e8m0fnu)."""
+    device = torch.device(device or "cuda")
+    e, two_i, hb = w13.shape
+    h, inter = hb * 2, two_i // 2
+    want = {"s13": (e, two_i, h // MX_BLOCK), "w2": (e, h, inter // 2), "s2": (e, h, inter // MX_BLOCK)}
+    for name, t in (("s13", s13), ("w2", w2), ("s2", s2)):
+        if tuple(t.shape) != want[name]:
+            raise ValueError(f"{name} shape {tuple(t.shape)}, expected {want[name]} for w13 {tuple(w13.shape)}")
+    c13, c2 = _bytes_on(w13, device), _bytes_on(w2, device)
+    sc13, sc2 = _bytes_on(s13, device), _bytes_on(s2, device)
+    img13 = torch.empty(e, two_i * (h // 2 + h // MX_BLOCK), dtype=torch.uint8, device=device)
+    img2 = torch.empty(e, h * (inter // 2 + inter // MX_BLOCK), dtype=torch.uint8, device=device)
+    none = torch.empty(0, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        st = _stream_handle()
+        _lib.call("afd_repack_mxfp4", c13.data_ptr(), sc13.data_ptr(), e, two_i, h, 1, img13.data_ptr(), st)
+        _lib.call("afd_repack_mxfp4", c2.data_ptr(), sc2.data_ptr(), e, h, inter, 0, img2.data_ptr(), st)
+    return ExpertWeights("mxfp4", e, h, inter, img13, none, img2, none)
+
+
+def repack_fp8_block_experts(w13: torch.Tensor, s13: torch.Tensor, w2: torch.Tensor, s2: torch.Tensor,
+                             device=None) -> ExpertWeights:
+    """Already-quantized FP8 block experts (e4m3 codes, fp32 128x128 block scales as
+    checkpoints store them: the dequantized weight is code x scale) into the kernel's row
+    order, bytes unchanged. w13: [E, 2I, H] rows [gate; up], s13: [E, 2I/128, H/128];
+    w2: [E, H, I], s2: [E, H/128, I/128]."""
+    device = torch.device(device or "cuda")
+    e, two_i, h = w13.shape
+    inter = two_i // 2
+    want = {"s13": (e, two_i // FP8_BLOCK, h // FP8_BLOCK), "w2": (e, h, inter),
+            "s2": (e, h // FP8_BLOCK, inter // FP8_BLOCK)}
+    for name, t in (("s13", s13), ("w2", w2), ("s2", s2)):
+        if tuple(t.shape) != want[name]:
+            raise ValueError(f"{name} shape {tuple(t.shape)}, expected {want[name]} for w13 {tuple(w13.shape)}")
+    c13, c2 = _bytes_on(w13, device), _bytes_on(w2, device)
+    q13 = torch.empty(e, two_i, h, dtype=torch.uint8, device=device)
+    q2 = torch.empty(e, h, inter, dtype=torch.uint8, device=device)
+    with torch.cuda.device(device):
+        st = _stream_handle()
+        _lib.call("afd_repack_fp8_block", c13.data_ptr(), e, two_i, h, 1, q13.data_ptr(), st)
+        _lib.call("afd_repack_fp8_block", c2.data_ptr(), e, h, inter, 0, q2.data_ptr(), st)
+    s13 = s13.to(device=device, dtype=torch.float32).contiguous()
+    s2 = s2.to(device=device, dtype=torch.float32).contiguous()
+    return ExpertWeights("fp8_block", e, h, inter, q13, s13, q2, s2)
+
+
 ACTIVATIONS = {"silu": _lib.AFD_ACT_SWIGLU, "situ": _lib.AFD_ACT_SITU}
 
 

@@ -50,6 +50,7 @@ ID_BYTES = 4  # int32 global expert ids
 W_BYTES = 4  # fp32 top-k weights
 
 PROTO_VERSION = 4
+PROTO_VERSION_FP8_WIRE = 5  # the x field carries e4m3 codes + scales (Geometry.act != "bf16")
 SEQ_MASK = 0xFFFFFFFF
 MAX_TOKENS = (1 << 17) - 1
 MAX_LAYER = (1 << 10) - 1
@@ -144,6 +145,12 @@ class Geometry:
             bad.append(f"act={self.act} needs hidden={self.hidden} to be a multiple of 128")
         if bad:
             raise ValueError("invalid transport geometry: " + ", ".join(bad))
+
+    @property
+    def proto_version(self) -> int:
+        """The wire protocol of this geometry: the reference's for bf16 activations, the next
+        one when fp8 activations change the x field."""
+        return PROTO_VERSION if self.act == "bf16" else PROTO_VERSION_FP8_WIRE
 
     # activations on the wire
     @property

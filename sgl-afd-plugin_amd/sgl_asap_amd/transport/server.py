@@ -124,6 +124,8 @@ class FfnServer:
     def hello(self, a: int, flags: Optional[hip.HostPage], segments, geometry: Geometry) -> dict:
         """Admit A rank ``a``: check the geometry field by field, hand out a new epoch, reset
         its doorbells' last-seen sequence. Returns what A maps: recv base, doorbell page."""
+        if geometry.proto_version != self.g.proto_version:
+            raise HandshakeError(f"protocol version A={geometry.proto_version} F={self.g.proto_version}")
         if geometry != self.g:
             diff = {k: (v, getattr(self.g, k)) for k, v in geometry.as_dict().items() if getattr(self.g, k) != v}
             raise HandshakeError(f"geometry mismatch (A, F): {diff}")

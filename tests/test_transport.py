@@ -243,7 +243,8 @@ def test_hello_rejects_geometry_mismatch():
     with pytest.raises(L.HandshakeError):
         s.hello(5, None, None, g)
     fp8 = L.Geometry(**{**g.as_dict(), "act": "mxfp8"})  # same sizes, other wire format
-    with pytest.raises(L.HandshakeError):
+    assert (g.proto_version, fp8.proto_version) == (L.PROTO_VERSION, L.PROTO_VERSION + 1)
+    with pytest.raises(L.HandshakeError, match="protocol version"):
         s.hello(0, None, None, fp8)
 
 
