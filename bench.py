@@ -324,29 +324,38 @@ def bench_loop(args) -> dict:
     pairs = sum(W.pair_count(t.topk_ids, shape.local) for _, t in mbs)
     routed_flops = W.flops(shape.hidden, shape.inter, pairs)
     shared_flops = 2 * 6 * shape.hidden * shared_i * n
-    afd = OneGpuAfd(experts, n_max=n, slots=2, graph_max_tokens=n)
     layer = AsapMoE(shape.num_experts, shape.hidden, shape.inter, 0, top_k=shape.top_k)
     main = torch.cuda.current_stream()
 
-    def step():
-        d = [layer.dispatcher.dispatch(x, t, micro_batch=m) for m, (x, t) in enumerate(mbs)]
-        afd.scheduler.serve_pending()
-        s = [shared(x) for x, _ in mbs]
-        return [layer.dispatcher.combine(d[m], s[m]) for m in range(2)]
+    def measure(act):
+        afd = OneGpuAfd(experts, n_max=n, slots=2, graph_max_tokens=n, act=act)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    lat = []
-    for _ in range(args.steps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(main)
-        step()
-        e1.record(main)
+        def step():
+            d = [layer.dispatcher.dispatch(x, t, micro_batch=m) for m, (x, t) in enumerate(mbs)]
+            afd.scheduler.serve_pending()
+            s = [shared(x) for x, _ in mbs]
+            return [layer.dispatcher.combine(d[m], s[m]) for m in range(2)]
+
+        for _ in range(args.warmup):
+            step()
         torch.cuda.synchronize()
-        lat.append(e0.elapsed_time(e1))
-    afd.close()
+        lat = []
+        for _ in range(args.steps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(main)
+            step()
+            e1.record(main)
+            torch.cuda.synchronize()
+            lat.append(e0.elapsed_time(e1))
+        afd.close()
+        return lat
+
+    # activations on the wire: bf16 (the reference's layout), then MXFP8 (A quantizes before
+    # the copy; bit-identical outputs, half the copy bytes, no quantizer on the F side)
+    lat_fp8 = measure("mxfp8")
+    lat = measure("bf16")
     ms = statistics.median(lat)
+    ms_fp8 = statistics.median(lat_fp8)
     return {
         "metric": "per-layer latency of the one-GPU AFD loop (W4A8 + bf16 shared expert), 1 MI355X",
         "value": round(ms, 4),
@@ -367,6 +376,10 @@ def bench_loop(args) -> dict:
         "layer_latency_ms_min": round(min(lat), 4),
         "tokens_per_s": round(2 * n / (ms * 1e-3), 1),
         "tflops_routed_plus_shared": round((routed_flops + shared_flops) / (ms * 1e-3) / 1e12, 2),
+        "wire": "bf16",
+        "fp8_wire": {"act": "mxfp8", "layer_latency_ms": round(ms_fp8, 4),
+                     "layer_latency_ms_min": round(min(lat_fp8), 4),
+                     "tokens_per_s": round(2 * n / (ms_fp8 * 1e-3), 1)},
     }
 
 
@@ -491,6 +504,15 @@ def main():
         del src, dst
 
     tflops = flops / (ms * 1e-3) / 1e12
+    # algorithmic bytes of the streaming phases (their own tensors' reads + writes)
+    k, h = shape.top_k, shape.hidden
+    xs_bytes = n * h // 32 if shape.fmt == "mxfp4" else n * h // 128 * 4
+    phase_bytes = {
+        "hist_quant": n * k * 4 + n * h * 2 + n * h + xs_bytes,  # ids; x in; codes + scales out
+        "scatter": n * k * 4 + n * k * 4 + np_pairs * 4,  # ids in; pair_pos, sorted pairs out
+        "finalize": np_pairs * h * 2 + n * k * 8 + n * h * 2,  # y rows, pair_pos + w; out
+    }
+    phase_gbps = {s: round(b / (stage_avg[s] * 1e-3) / 1e9, 1) for s, b in phase_bytes.items()}
     gu_tflops = gate_up_flops / (gu_ms * 1e-3) / 1e12
     issued = "fp8" if shape.fmt in ("mxfp4", "fp8_block") else "bf16"
     result = {
@@ -519,6 +541,8 @@ def main():
         "mfma_util_vs_fp4_peak": round(tflops / PEAK_TFLOPS["fp4"], 4),
         "mfma_util_vs_issued_peak": round(tflops / PEAK_TFLOPS[issued], 4),
         "stages_ms": stage_avg,
+        "phase_bytes": phase_bytes,
+        "phase_hbm_gbps": phase_gbps,
         "stages_note": "from a second pass of the same steps through afd_moe_ffn_profiled with all "
         "six stage events; the timed steps record only the two events around gate_up (its duration "
         "in roofline). hist_quant: the expert histogram and the activation quantization in one "

@@ -16,6 +16,9 @@
  *                                P/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:87-93)
  *   afd_quant_mxfp8 / _fp8_1x128 the activation quantizer quantize_routed_input
  *   / afd_quant_act              (mxfp4_flashinfer_trtllm_moe.py:59-61)
+ *   afd_moe_ffn_job / .......... the graph runner's replay (P/srt/model_executor/runner/
+ *   afd_job_set                  ffn_cuda_graph_runner.py:75-92) with the job read from a
+ *                                device descriptor instead of copied into static inputs
  *   afd_moe_ffn_q .............. the expert call on activations quantized before the arena
  *                                copy (the reference's TODO, scripts/run_asap.sh:110-111)
  *   afd_finalize ............... the finalize (top-k weighted sum, do_finalize=True,
@@ -195,6 +198,35 @@ int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const
 int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint8_t* xq,
                   const void* xs, const int32_t* ids, const float* w, int32_t n, void* ws,
                   uint64_t ws_bytes, uint16_t* out, afd_stream_t stream);
+
+/* A job described in device memory, for callers that replay captured HIP graphs: the
+ * launches of afd_moe_ffn_job read the descriptor when they run, so one capture serves every
+ * job written into the descriptor afterwards (no copies into static buffers, no padding of
+ * the job to the captured size). x: bf16 [n][H], or NULL with xq / xs as afd_quant_act
+ * writes them; ids i32 [n][k]; w f32 [n][k]; out bf16 [n][H]. */
+typedef struct afd_job {
+  const uint16_t* x;
+  const uint8_t* xq;
+  const void* xs;
+  const int32_t* ids;
+  const float* w;
+  uint16_t* out;
+  int64_t n;
+} afd_job;
+
+/* The expert call on the job that `job` (device memory) holds when the launches run, with
+ * n_cap the largest n it will hold: grids and the workspace are sized for n_cap (ws_bytes from
+ * afd_workspace_layout(cfg, n_cap)); a descriptor n outside [0, n_cap] is clamped into it.
+ * quantized = 0 reads job->x, 1 reads job->xq / job->xs. Results equal afd_moe_ffn's (or
+ * afd_moe_ffn_q's) on the same job, bit for bit. Replaces the copy-in / pad / replay / copy-out
+ * of the FFN rank's graph runner (P/srt/model_executor/runner/ffn_cuda_graph_runner.py:75-92). */
+int afd_moe_ffn_job(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                    const afd_job* job, int32_t n_cap, int32_t quantized, void* ws,
+                    uint64_t ws_bytes, afd_stream_t stream);
+
+/* Enqueue on `stream` a write of *value (read now, on the host) into the device descriptor
+ * `job`: ordered with the stream's launches, so a graph replayed after it sees the new job. */
+int afd_job_set(afd_job* job, const afd_job* value, afd_stream_t stream);
 
 /* The activation quantizer of the expert call (quantize_routed_input,
  * mxfp4_flashinfer_trtllm_moe.py:59-61) on its own: x bf16 [n][H] -> q e4m3 [n][H] and s:

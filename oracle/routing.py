@@ -92,12 +92,6 @@ def local_experts(ep_rank: int, ep_size: int, num_experts: int) -> range:
     return range(ep_rank * per, (ep_rank + 1) * per)
 
 
-def graph_pad_id(local: range, num_experts: int) -> int:
-    """``FfnCudaGraphRunner.pad_id`` (ffn_cuda_graph_runner.py:40-42): an expert of
-    another rank when the rank is partial, else the first local expert (weight 0)."""
-    return local.stop % num_experts if len(local) < num_experts else local.start
-
-
 def graph_buckets(max_tokens: int) -> list:
     """Powers of two below max_tokens, then max_tokens (ffn_cuda_graph_runner.py:36-39)."""
     b = [1 << i for i in range(max_tokens.bit_length()) if 1 << i < max_tokens]

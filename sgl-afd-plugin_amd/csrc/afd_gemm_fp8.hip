@@ -76,6 +76,7 @@ static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
 struct Fp8GemmArgs {
   const uint8_t* a;   // gate_up: token rows xq [n][K]; down: hq [np][K]
   const float* as;    // their scales: xs [n][K/128]; hs [np][K/128]
+  const afd_job* rows_desc;  // gate_up: if set, a / as are its xq / xs
   int topk;
   uint32_t topk_magic;  // div_magic(topk)
   uint32_t ncb_magic;   // div_magic(walk_col_blocks<kWalkRows>(N / 256))
@@ -167,9 +168,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   const uint8_t* w_tile = nullptr;
   int blk0 = 0, blk1 = 0;
   int64_t e_copy = 0;
+  const uint8_t* a_rows = p.a;
+  const float* a_scales = p.as;
+  if (MODE != kDown && p.rows_desc != nullptr) {
+    a_rows = p.rows_desc->xq;
+    a_scales = static_cast<const float*>(p.rows_desc->xs);
+  }
   auto copy_tile = [&](int mt, int nt, int64_t e) {
-    x_tile = MODE != kDown ? p.a : p.a + int64_t(mt) * kBM * p.K;
-    s_tile = MODE != kDown ? p.as : p.as + int64_t(mt) * kBM * KT;
+    x_tile = MODE != kDown ? a_rows : a_rows + int64_t(mt) * kBM * p.K;
+    s_tile = MODE != kDown ? a_scales : a_scales + int64_t(mt) * kBM * KT;
     w_tile = p.b + (e * p.N + int64_t(nt) * kBN) * int64_t(p.K);
     // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
     // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
@@ -503,12 +510,12 @@ static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws
 }  // namespace fp8
 
 int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                       const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
-                       hipStream_t stream) {
-  (void)n;
+                       const afd_ws_layout& L, const uint8_t* xq, const void* xs,
+                       const afd_job* rows_desc, hipStream_t stream) {
   fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
   p.a = xq;
   p.as = static_cast<const float*>(xs);
+  p.rows_desc = rows_desc;
   p.b = static_cast<const uint8_t*>(wt.w13);
   p.bs = static_cast<const float*>(wt.s13);
   p.K = cfg.hidden;
@@ -525,6 +532,7 @@ int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_
   fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
   p.a = ws + L.hq;
   p.as = reinterpret_cast<const float*>(ws + L.hs);
+  p.rows_desc = nullptr;
   p.b = static_cast<const uint8_t*>(wt.w2);
   p.bs = static_cast<const float*>(wt.s2);
   p.K = cfg.inter;

@@ -39,6 +39,7 @@ struct MxGemmArgs {
   const uint8_t* a_img;         // down: A images [row tiles][K/128]
   const uint8_t* a_rows;        // gate_up: e4m3 token rows [n][K], gathered by sorted_pairs
   const uint8_t* a_scales;      // gate_up: their UE8M0 scales [n][K/32] in stage order
+  const afd_job* rows_desc;     // gate_up: if set, a_rows / a_scales are its xq / xs
   int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
   uint32_t topk_magic;          // div_magic(topk)
   uint32_t ncb_magic;           // div_magic(walk_col_blocks<kMxWalkRows>(N / BN)), for the tile walk
@@ -104,6 +105,12 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   const uint32_t voff = static_cast<uint32_t>(lane) * 16;
+  const uint8_t* a_rows = p.a_rows;
+  const uint8_t* a_scales = p.a_scales;
+  if (MODE != kDown && p.rows_desc != nullptr) {
+    a_rows = p.rows_desc->xq;
+    a_scales = static_cast<const uint8_t*>(p.rows_desc->xs);
+  }
   // this wavefront's B operand: image wn/2 of the stage, rows (wn%2)*128 + j*32 + lr
   const int bimg = wn / 2, brow = (wn % 2) * 128;
 
@@ -166,7 +173,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int step16 = img16 == 0 ? kImgA : kImgB;
   const uint32_t dst16 = img16 == 0 ? kImgData : T::kLdsA + (img16 - 1) * kImgB + kImgData;
   auto copy_tile = [&](int mt, int nt, int64_t e) {
-    a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : p.a_rows;
+    a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA : a_rows;
     b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
     src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
   };
@@ -175,14 +182,14 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
     if constexpr (q == T::kImgs * T::kQP) {
       if (MODE != kDown && img16 == 0)  // 64 rows' scale words, gathered
-        lds_dma4(st + kImgData + s_half * 256, p.a_scales + int64_t(kt) * 4, s_voff);
+        lds_dma4(st + kImgData + s_half * 256, a_scales + int64_t(kt) * 4, s_voff);
       else
         lds_dma16(st + dst16, src16 + int64_t(kt) * step16, voff);
     } else {
       constexpr int img = q / T::kQP;
       const int off = (w_u * T::kQP + q % T::kQP) * 1024;
       if constexpr (img == 0 && MODE != kDown)
-        lds_dma16(st + off, p.a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
+        lds_dma16(st + off, a_rows + int64_t(kt) * kImgK, a_voff[q % T::kQP]);
       else if constexpr (img == 0)
         lds_dma16(st + off, a_tile + int64_t(kt) * kImgA + off, voff);
       else
@@ -475,13 +482,13 @@ static int launch_mx_any(const MxGemmArgs& p, int max_row_tiles, hipStream_t str
 }
 
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                      const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
-                      hipStream_t stream) {
-  (void)n;
+                      const afd_ws_layout& L, const uint8_t* xq, const void* xs,
+                      const afd_job* rows_desc, hipStream_t stream) {
   MxGemmArgs p;
   p.a_img = nullptr;
   p.a_rows = xq;
   p.a_scales = static_cast<const uint8_t*>(xs);
+  p.rows_desc = rows_desc;
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
   p.act = act_params(cfg);
@@ -507,6 +514,7 @@ int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t
   p.a_img = ws + L.hq;
   p.a_rows = nullptr;
   p.a_scales = nullptr;
+  p.rows_desc = nullptr;
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
   p.b_img = static_cast<const uint8_t*>(wt.w2);

@@ -13,6 +13,30 @@ constexpr int kMaxTopk = 32;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
 
 
+// Where a launch finds its job: the fields by value, or (desc != nullptr) read from the job
+// descriptor in device memory when the kernel runs, n then clamped to [0, n] as given here
+// (the n_cap the grids and the workspace were sized for).
+struct JobIn {
+  const afd_job* desc;
+  const uint16_t* x;
+  const int32_t* ids;
+  const float* w;
+  uint16_t* out;
+  int64_t n;
+};
+
+__device__ __forceinline__ JobIn resolve_job(JobIn j) {
+  if (j.desc != nullptr) {
+    const afd_job d = *j.desc;
+    j.x = d.x;
+    j.ids = d.ids;
+    j.w = d.w;
+    j.out = d.out;
+    j.n = d.n < 0 ? 0 : d.n < j.n ? d.n : j.n;
+  }
+  return j;
+}
+
 // Routing of the job's pairs into the workspace; with x, the activation quantization into
 // ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs beside the
 // expert histogram. `mid` (optional) is recorded between the two launches.
@@ -21,23 +45,24 @@ constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments 
 int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
                      hipStream_t stream);
 
-int launch_route_quant(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
-                       const afd_ws_layout& L, const uint16_t* x, hipStream_t stream,
-                       hipEvent_t mid);
+// With quantize = false the launch only routes (the rows are quantized already).
+int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
+                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid);
 
 // Grouped MXFP4 GEMMs (afd_gemm_mx.hip).
 // xq / xs: the quantized activation rows [n][H] and their scales (the workspace's, or the
-// caller's for afd_moe_ffn_q)
+// caller's for afd_moe_ffn_q); with rows_desc != nullptr they are read from that job
+// descriptor's xq / xs when the kernel runs.
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                      const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
-                      hipStream_t stream);
+                      const afd_ws_layout& L, const uint8_t* xq, const void* xs,
+                      const afd_job* rows_desc, hipStream_t stream);
 int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                    const afd_ws_layout& L, int32_t n, hipStream_t stream);
 
 // Grouped FP8 128x128-block GEMMs (afd_gemm_fp8.hip).
 int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
-                       const afd_ws_layout& L, const uint8_t* xq, const void* xs, int32_t n,
-                       hipStream_t stream);
+                       const afd_ws_layout& L, const uint8_t* xq, const void* xs,
+                       const afd_job* rows_desc, hipStream_t stream);
 int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                     const afd_ws_layout& L, int32_t n, hipStream_t stream);
 

@@ -46,10 +46,14 @@ constexpr int kFinThreads = 256;
 constexpr int kFinElems = 8;  // bf16 per lane = one 16-byte vector
 
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
-    const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos,
-    const float* __restrict__ w, int k, int hidden, int col_blocks, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos, JobIn jin, int k,
+    int hidden, int col_blocks) {
   // products and sums round separately: no contraction of w * y + acc into an fma
 #pragma clang fp contract(off)
+  const JobIn job = resolve_job(jin);
+  if (int64_t(blockIdx.x) >= job.n * col_blocks) return;  // past a descriptor's job
+  const float* __restrict__ w = job.w;
+  uint16_t* __restrict__ out = job.out;
   const int64_t tok = blockIdx.x / col_blocks;
   const int col = ((blockIdx.x % col_blocks) * kFinThreads + threadIdx.x) * kFinElems;
   if (col >= hidden) return;
@@ -93,13 +97,14 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
 }
 
-static int launch_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w,
-                           int32_t n, int32_t k, int32_t hidden, uint16_t* out,
-                           hipStream_t stream) {
-  if (n == 0) return AFD_OK;
+// one workgroup per (token, column block) of job.n tokens (with a descriptor: of n_cap, the
+// ones past the job's tokens return at once)
+static int launch_finalize(const uint16_t* y, const int32_t* pair_pos, const JobIn& job,
+                           int32_t k, int32_t hidden, hipStream_t stream) {
+  if (job.n == 0) return AFD_OK;
   const int col_blocks = (hidden / kFinElems + kFinThreads - 1) / kFinThreads;
-  hipLaunchKernelGGL(finalize_kernel, dim3(col_blocks * n), dim3(kFinThreads), 0, stream, y,
-                     pair_pos, w, k, hidden, col_blocks, out);
+  hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>(col_blocks * job.n)),
+                     dim3(kFinThreads), 0, stream, y, pair_pos, job, k, hidden, col_blocks);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }
@@ -237,18 +242,21 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   return AFD_OK;
 }
 
-// x: bf16 activations, quantized here; or (x == NULL) xq / xs: activations the caller
-// quantized with afd_quant_act.
+// job: the job's pointers and n by value, or its descriptor with job.n = n_cap. quantized:
+// the rows come quantized by afd_quant_act (xq / xs, or the descriptor's) instead of as bf16
+// x, which is quantized here.
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
-                        const uint16_t* x, const uint8_t* xq, const void* xs, const int32_t* ids,
-                        const float* w, int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
-                        afd_stream_t stream, void* const* ev) {
+                        const JobIn& job, bool quantized, const uint8_t* xq, const void* xs,
+                        void* ws, uint64_t ws_bytes, afd_stream_t stream, void* const* ev) {
+  if (job.n < 0 || job.n > 0x1ffff) return AFD_ERR_ARG;
+  const int32_t n = static_cast<int32_t>(job.n);
   afd_ws_layout L;
   int st = afd_workspace_layout(cfg, n, &L);
   if (st != AFD_OK) return st;
   if (!weights || !weights->w13 || !weights->w2) return AFD_ERR_ARG;
   if (cfg->weight_fmt == AFD_W_FP8_BLOCK && (!weights->s13 || !weights->s2)) return AFD_ERR_ARG;
-  if (n > 0 && ((!x && !(xq && xs)) || !ids || !w || !out)) return AFD_ERR_ARG;
+  const bool rows_ok = quantized ? (xq && xs) : job.x != nullptr;
+  if (!job.desc && n > 0 && (!rows_ok || !job.ids || !job.w || !job.out)) return AFD_ERR_ARG;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
   // the gate_up GEMMs address token rows with 32-bit byte offsets
@@ -264,21 +272,22 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
     // routing and the activation quantization (one launch beside the expert histogram), then
     // the pair scatter; stage mark 1 falls between the two launches
-    st = launch_route_quant(ids, n, *cfg, wsb, L, x, s,
+    st = launch_route_quant(job, !quantized, *cfg, wsb, L, s,
                             ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
     if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
-    const uint8_t* aq = x ? wsb + L.xq : xq;
-    const void* as = x ? static_cast<const void*>(wsb + L.xs) : xs;
-    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, aq, as, n, s)
-            : launch_fp8_gate_up(*cfg, *weights, wsb, L, aq, as, n, s);
+    const uint8_t* aq = quantized ? xq : wsb + L.xq;
+    const void* as = quantized ? xs : static_cast<const void*>(wsb + L.xs);
+    const afd_job* rows_desc = quantized ? job.desc : nullptr;
+    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s)
+            : launch_fp8_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s);
     if (st != AFD_OK || (st = mark(3)) != AFD_OK) return st;
     st = mx ? launch_mx_down(*cfg, *weights, wsb, L, n, s)
             : launch_fp8_down(*cfg, *weights, wsb, L, n, s);
     if (st != AFD_OK || (st = mark(4)) != AFD_OK) return st;
     st = launch_finalize(reinterpret_cast<const uint16_t*>(wsb + L.y),
-                         reinterpret_cast<const int32_t*>(wsb + L.pair_pos), w, n, cfg->topk,
-                         cfg->hidden, out, s);
+                         reinterpret_cast<const int32_t*>(wsb + L.pair_pos), job, cfg->topk,
+                         cfg->hidden, s);
     if (st != AFD_OK) return st;
   } else {
     for (int i = 1; i < 5; ++i)
@@ -290,18 +299,38 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
 extern "C" int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                            const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
                            void* ws, uint64_t ws_bytes, uint16_t* out, afd_stream_t stream) {
-  if (!x && n > 0) return AFD_ERR_ARG;
-  return moe_ffn_impl(cfg, weights, x, nullptr, nullptr, ids, w, n, ws, ws_bytes, out, stream,
-                      nullptr);
+  const JobIn job{nullptr, x, ids, w, out, n};
+  return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream, nullptr);
 }
 
 extern "C" int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                              const uint8_t* xq, const void* xs, const int32_t* ids,
                              const float* w, int32_t n, void* ws, uint64_t ws_bytes,
                              uint16_t* out, afd_stream_t stream) {
-  if ((!xq || !xs) && n > 0) return AFD_ERR_ARG;
-  return moe_ffn_impl(cfg, weights, nullptr, xq, xs, ids, w, n, ws, ws_bytes, out, stream,
+  const JobIn job{nullptr, nullptr, ids, w, out, n};
+  return moe_ffn_impl(cfg, weights, job, true, xq, xs, ws, ws_bytes, stream, nullptr);
+}
+
+extern "C" int afd_moe_ffn_job(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                               const afd_job* job, int32_t n_cap, int32_t quantized, void* ws,
+                               uint64_t ws_bytes, afd_stream_t stream) {
+  if (!job) return AFD_ERR_ARG;
+  const JobIn jin{job, nullptr, nullptr, nullptr, nullptr, n_cap};
+  return moe_ffn_impl(cfg, weights, jin, quantized != 0, nullptr, nullptr, ws, ws_bytes, stream,
                       nullptr);
+}
+
+__global__ void job_set_kernel(afd_job* __restrict__ job, afd_job value) {
+  if (threadIdx.x == 0) *job = value;
+}
+
+extern "C" int afd_job_set(afd_job* job, const afd_job* value, afd_stream_t stream) {
+  if (!job || !value) return AFD_ERR_ARG;
+  if ((reinterpret_cast<uintptr_t>(job) & 7) != 0) return AFD_ERR_ARG;
+  hipLaunchKernelGGL(job_set_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), job,
+                     *value);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
 }
 
 extern "C" int afd_quant_act(const afd_moe_cfg* cfg, const uint16_t* x, int32_t n, uint8_t* q,
@@ -317,8 +346,8 @@ extern "C" int afd_moe_ffn_profiled(const afd_moe_cfg* cfg, const afd_expert_wei
                                     const uint16_t* x, const int32_t* ids, const float* w,
                                     int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
                                     afd_stream_t stream, void* const* stage_events) {
-  if (!x && n > 0) return AFD_ERR_ARG;
-  return moe_ffn_impl(cfg, weights, x, nullptr, nullptr, ids, w, n, ws, ws_bytes, out, stream,
+  const JobIn job{nullptr, x, ids, w, out, n};
+  return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream,
                       stage_events);
 }
 
@@ -328,7 +357,8 @@ extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const fl
   if (n < 0 || k < 1 || k > kMaxTopk) return AFD_ERR_ARG;
   if (n > 0 && (!y || !pair_pos || !w || !out)) return AFD_ERR_ARG;
   if (hidden <= 0 || hidden % kFinElems) return AFD_ERR_SHAPE;
-  return launch_finalize(y, pair_pos, w, n, k, hidden, out, static_cast<hipStream_t>(stream));
+  const JobIn job{nullptr, nullptr, nullptr, w, out, n};
+  return launch_finalize(y, pair_pos, job, k, hidden, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int afd_combine(const uint16_t* const* parts, int32_t num_parts,

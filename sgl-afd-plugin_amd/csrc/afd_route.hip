@@ -32,28 +32,30 @@ __device__ __forceinline__ int pair_key(int id, int e_lo, int num_local) {
 // activation quantization run by the prep kernel beside the histogram
 enum { kPrepNone = 0, kPrepMxfp8 = 1, kPrepFp8 = 2 };
 struct PrepQuant {
-  const uint16_t* x;
-  int64_t items;  // MX blocks of 32 (MXFP8) or quarter groups of 32 (FP8 1x128)
-  int cols;
+  int cols;  // items: n * cols / 32 MX blocks (MXFP8) or quarter groups (FP8 1x128)
   uint8_t* q;
   void* s;
 };
 
 template <int QUANT>
 __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
-    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int chunks, int e_lo,
-    int num_local, int32_t* __restrict__ hist, PrepQuant pq) {
+    JobIn jin, int topk, int chunk, int chunks, int e_lo, int num_local,
+    int32_t* __restrict__ hist, PrepQuant pq) {
+  const JobIn job = resolve_job(jin);
   if (static_cast<int>(blockIdx.x) >= chunks) {
     const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
     const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;
+    const int64_t items = job.n * (pq.cols / kMxBlock);
     if constexpr (QUANT == kPrepMxfp8)
-      quant_mxfp8_items<true>(pq.x, pq.items, pq.cols, pq.q, static_cast<uint8_t*>(pq.s), first,
+      quant_mxfp8_items<true>(job.x, items, pq.cols, pq.q, static_cast<uint8_t*>(pq.s), first,
                               stride);
     else if constexpr (QUANT == kPrepFp8)
-      quant_fp8_1x128_items(pq.x, pq.items, pq.cols, pq.q, static_cast<float*>(pq.s), first,
+      quant_fp8_1x128_items(job.x, items, pq.cols, pq.q, static_cast<float*>(pq.s), first,
                             stride);
     return;
   }
+  const int32_t* __restrict__ ids = job.ids;
+  const int64_t pairs = job.n * topk;
   __shared__ int cnt[kMaxLocalExperts];
   for (int e = threadIdx.x; e < num_local; e += kRouteThreads) cnt[e] = 0;
   __syncthreads();
@@ -69,11 +71,14 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
 }
 
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
-    const int32_t* __restrict__ ids, int64_t pairs, int chunk, int chunks, int e_lo,
-    int num_local, int block_m, const int32_t* __restrict__ hist, int32_t* __restrict__ counts,
+    JobIn jin, int topk, int chunk, int chunks, int e_lo, int num_local, int block_m,
+    const int32_t* __restrict__ hist, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ poff, int32_t* __restrict__ sorted_pairs,
     int32_t* __restrict__ pair_pos, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ num_tiles) {
+  const JobIn job = resolve_job(jin);
+  const int32_t* __restrict__ ids = job.ids;
+  const int64_t pairs = job.n * topk;
   constexpr int kWaves = kRouteThreads / 64;
   constexpr int kMaxPer = kMaxChunks / (kRouteThreads / kMaxLocalExperts);
   __shared__ int run[kMaxLocalExperts + 1];
@@ -216,38 +221,35 @@ void route_chunking(int64_t pairs, int* chunks, int* chunk) {
   *chunks = pairs == 0 ? 0 : static_cast<int>((pairs + c - 1) / c);
 }
 
-int launch_route_quant(const int32_t* ids, int32_t n, const afd_moe_cfg& cfg, uint8_t* ws,
-                       const afd_ws_layout& L, const uint16_t* x, hipStream_t stream,
-                       hipEvent_t mid) {
-  const int64_t pairs = int64_t(n) * cfg.topk;
+int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
+                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid) {
+  // grids for job.n tokens (with a descriptor: n_cap; chunks past the job's pairs are empty)
+  const int64_t pairs = job.n * cfg.topk;
   int chunks, chunk;
   route_chunking(pairs, &chunks, &chunk);
   int32_t* hist = reinterpret_cast<int32_t*>(ws + L.hist);
-  PrepQuant pq{x, 0, cfg.hidden, ws + L.xq, ws + L.xs};
+  PrepQuant pq{cfg.hidden, ws + L.xq, ws + L.xs};
   int quant_grid = 0;
-  const int fmt = x == nullptr ? kPrepNone : cfg.weight_fmt == AFD_W_MXFP4 ? kPrepMxfp8 : kPrepFp8;
-  if (fmt != kPrepNone) {
-    pq.items = int64_t(n) * (cfg.hidden / kMxBlock);
-    quant_grid = grid_for(pq.items);
-  }
-  if (chunks + quant_grid > 0) {
+  const int fmt = !quantize ? kPrepNone : cfg.weight_fmt == AFD_W_MXFP4 ? kPrepMxfp8 : kPrepFp8;
+  if (fmt != kPrepNone) quant_grid = grid_for(job.n * (cfg.hidden / kMxBlock));
+  if (job.n > 0 && chunks + quant_grid > 0) {
     const dim3 grid(chunks + quant_grid);
     if (fmt == kPrepMxfp8)
-      hipLaunchKernelGGL(route_prep_kernel<kPrepMxfp8>, grid, dim3(kRouteThreads), 0, stream, ids,
-                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
+      hipLaunchKernelGGL(route_prep_kernel<kPrepMxfp8>, grid, dim3(kRouteThreads), 0, stream, job,
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
     else if (fmt == kPrepFp8)
-      hipLaunchKernelGGL(route_prep_kernel<kPrepFp8>, grid, dim3(kRouteThreads), 0, stream, ids,
-                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
+      hipLaunchKernelGGL(route_prep_kernel<kPrepFp8>, grid, dim3(kRouteThreads), 0, stream, job,
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
     else
-      hipLaunchKernelGGL(route_prep_kernel<kPrepNone>, grid, dim3(kRouteThreads), 0, stream, ids,
-                         pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
+      hipLaunchKernelGGL(route_prep_kernel<kPrepNone>, grid, dim3(kRouteThreads), 0, stream, job,
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq);
     AFD_CHECK_LAUNCH();
   }
   if (mid) AFD_CHECK_HIP(hipEventRecord(mid, stream));
   // at least one workgroup, which writes the (empty) tables when there are no pairs
   hipLaunchKernelGGL(route_scatter_kernel, dim3(chunks > 0 ? chunks : 1), dim3(kRouteThreads), 0,
-                     stream, ids, pairs, chunk, chunks, cfg.expert_lo, cfg.num_local, L.block_m,
-                     hist, reinterpret_cast<int32_t*>(ws + L.counts),
+                     stream, job, cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local,
+                     L.block_m, hist, reinterpret_cast<int32_t*>(ws + L.counts),
                      reinterpret_cast<int32_t*>(ws + L.offsets),
                      reinterpret_cast<int32_t*>(ws + L.padded_offsets),
                      reinterpret_cast<int32_t*>(ws + L.sorted_pairs),
@@ -267,6 +269,7 @@ extern "C" int afd_route(const int32_t* ids, int32_t n, const afd_moe_cfg* cfg, 
   if (st != AFD_OK) return st;
   if ((!ids && n > 0) || !ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
-  return afd::launch_route_quant(ids, n, *cfg, static_cast<uint8_t*>(ws), L, nullptr,
+  const afd::JobIn job{nullptr, nullptr, ids, nullptr, nullptr, n};
+  return afd::launch_route_quant(job, false, *cfg, static_cast<uint8_t*>(ws), L,
                                  static_cast<hipStream_t>(stream), nullptr);
 }

@@ -46,6 +46,8 @@ EXPORTED = (
     "afd_route",
     "afd_moe_ffn",
     "afd_moe_ffn_q",
+    "afd_moe_ffn_job",
+    "afd_job_set",
     "afd_moe_ffn_profiled",
     "afd_finalize",
     "afd_combine",
@@ -85,6 +87,20 @@ class AfdExpertWeights(ctypes.Structure):
         ("s13", ctypes.c_void_p),
         ("w2", ctypes.c_void_p),
         ("s2", ctypes.c_void_p),
+    ]
+
+
+class AfdJob(ctypes.Structure):
+    """afd_job: a job described in device memory (afd_moe_ffn_job reads it when it runs)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("xq", ctypes.c_void_p),
+        ("xs", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("n", ctypes.c_int64),
     ]
 
 
@@ -129,6 +145,8 @@ _SIGS = {
         _I32,
     ),
     "afd_quant_act": ([ctypes.POINTER(AfdMoeCfg), _P, _I32, _P, _P, _P], _I32),
+    "afd_moe_ffn_job": ([ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _I32, _I32, _P, _U64, _P], _I32),
+    "afd_job_set": ([_P, ctypes.POINTER(AfdJob), _P], _I32),
     "afd_moe_ffn_q": (
         [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _P, _I32, _P, _U64, _P, _P],
         _I32,

@@ -246,6 +246,37 @@ def _quant_act(cfg, act, x, q, s, stream):
     return q, s
 
 
+JOB_BYTES = ctypes.sizeof(_lib.AfdJob)
+
+
+def new_job_desc(device=None) -> torch.Tensor:
+    """A zeroed device job descriptor (afd_job) for ``AfdExperts.call_job`` / ``set_job``."""
+    return torch.zeros(JOB_BYTES, dtype=torch.uint8, device=device or "cuda")
+
+
+def set_job(desc: torch.Tensor, *, ids: torch.Tensor, w: torch.Tensor, out: torch.Tensor,
+            x: Optional[torch.Tensor] = None, xq: Optional[torch.Tensor] = None,
+            xs: Optional[torch.Tensor] = None, stream: Optional[torch.cuda.Stream] = None) -> None:
+    """Enqueue on ``stream`` (default: current) the write of one job into the descriptor
+    (afd_job_set): bf16 ``x`` [n, H], or ``xq`` / ``xs`` from quant_act; int32 ``ids`` and fp32
+    ``w`` [n, k]; bf16 ``out`` [n, H]. The tensors must stay alive until the calls that read
+    the descriptor have run."""
+    n = ids.shape[0]
+    for name, t in (("ids", ids), ("w", w), ("out", out), ("x", x), ("xq", xq), ("xs", xs)):
+        if t is not None and (not t.is_contiguous() or (t.dim() > 0 and t.shape[0] != n)):
+            raise ValueError(f"{name} must be contiguous with {n} rows")
+    if ids.dtype != torch.int32 or w.dtype != torch.float32 or out.dtype != torch.bfloat16:
+        raise TypeError("ids int32, w float32 and out bf16 expected")
+    if (x is None) == (xq is None or xs is None):
+        raise ValueError("give either x or both xq and xs")
+
+    def ptr(t):
+        return t.data_ptr() if t is not None else None
+
+    value = _lib.AfdJob(ptr(x), ptr(xq), ptr(xs), ptr(ids), ptr(w), ptr(out), n)
+    _lib.call("afd_job_set", desc.data_ptr(), ctypes.byref(value), _stream_handle(stream))
+
+
 def workspace_layout(cfg: _lib.AfdMoeCfg, n: int) -> dict:
     """afd_workspace_layout as a dict of byte offsets (plus np_max, block_m, max_tiles)."""
     out = _lib.AfdWsLayout()
@@ -337,6 +368,29 @@ class AfdExperts(torch.nn.Module):
             _stream_handle(),
         )
         return out
+
+    # ---- graph replay: the job is read from a device descriptor when the calls run ----
+    def call_job(self, desc: torch.Tensor, n_cap: int, quantized: bool = False) -> None:
+        """Enqueue the expert call on whatever job ``desc`` (from ``new_job_desc``) holds when
+        it runs, up to ``n_cap`` tokens (afd_moe_ffn_job): bf16 rows, or with ``quantized``
+        the xq / xs of ``quant_act``. Capture it in a HIP graph once, then ``set_job`` +
+        replay per job: no copies into static buffers, no work for tokens the job lacks."""
+        if not 0 <= n_cap <= self.n_max:
+            raise ValueError(f"n_cap {n_cap} outside [0, n_max={self.n_max}]")
+        if desc.dtype != torch.uint8 or desc.numel() != JOB_BYTES or not desc.is_cuda:
+            raise ValueError(f"desc must be a device uint8 tensor of {JOB_BYTES} bytes")
+        ws = self.workspace()
+        _lib.call(
+            "afd_moe_ffn_job",
+            ctypes.byref(self.cfg),
+            ctypes.byref(self._wstruct),
+            desc.data_ptr(),
+            n_cap,
+            int(bool(quantized)),
+            ws.data_ptr(),
+            ws.numel(),
+            _stream_handle(),
+        )
 
     # ---- fp8 activations on the wire: A quantizes, F runs on the quantized rows ----
     @property

@@ -1,20 +1,24 @@
-"""HIP graphs of the expert calls of an FFN rank, per (layer, token bucket, output buffer).
+"""HIP graphs of the expert calls of an FFN rank, one per (layer, token bucket).
 
-Same rules as ``python/sgl_asap_plugin/srt/model_executor/runner/ffn_cuda_graph_runner.py``:
-buckets are the powers of two below ``max_tokens`` plus ``max_tokens`` (:36-39); padding rows
-route to ``pad_id`` = an expert of another rank when the rank is partial, else the first
-local expert with weight 0 (:40-42, :88-90); two static output buffers, one graph per
-(layer, bucket, buffer) (:48-66); ``run`` copies the job's rows into the static inputs, pads
-them to the bucket, replays, and returns a view of the output buffer, or None when the job
-is larger than the largest bucket (:75-92).
+Replaces ``python/sgl_asap_plugin/srt/model_executor/runner/ffn_cuda_graph_runner.py``. The
+buckets are the reference's: the powers of two below ``max_tokens`` plus ``max_tokens``
+(:36-39), and a job larger than the largest bucket runs eagerly (``run`` returns None,
+:75-92). The reference copies a job's rows into static input buffers, pads them to the
+bucket with a pad expert (:40-42, :88-90), replays into one of two static output buffers
+(:48-66) and copies the result out. Here each graph captures ``afd_moe_ffn_job``, whose
+launches read the job from a device descriptor when they run: ``run`` writes the job's
+pointers and size into the descriptor (one small launch) and replays. The kernels then read
+the rows in place (the RecvArena), do no work for the tokens the job lacks, and write the
+output where the caller says (A's result segment), so nothing is copied in or out; the bucket
+only bounds the grids. Jobs of several rows (a TP group) are concatenated first, and without
+an ``out`` their output lands in one of two internal buffers used in turn, as in the
+reference.
 
-With fp8 activations on the wire (``act`` "mxfp8" / "fp8_1x128") the static inputs are the
-e4m3 codes and their scales and the graphs capture ``forward_q``.
+With fp8 activations on the wire (``act`` "mxfp8" / "fp8_1x128") the descriptor carries the
+e4m3 codes and their scales instead of bf16 rows.
 
-A graph replay removes the per-job host cost of the eager call (argument checks, the
-ctypes call and its kernel launches). Our kernels read the device-side row-tile count the
-router writes, so a bucket's graph serves any job size up to the bucket. The stream memops
-of the transport stay outside the graphs: their values are fixed at capture time.
+The stream memops of the transport stay outside the graphs: their values are fixed at
+capture time.
 """
 
 from __future__ import annotations
@@ -25,8 +29,7 @@ from typing import Dict, Optional
 
 import torch
 
-from ..moe.experts import act_scale_shape
-from ..moe.topk import StandardTopKOutput
+from ..moe.experts import new_job_desc, set_job
 
 
 def graph_buckets(max_tokens: int) -> list:
@@ -34,67 +37,54 @@ def graph_buckets(max_tokens: int) -> list:
     return b + [max_tokens]
 
 
-def pad_id_for(local: range, num_experts: int) -> int:
-    return local.stop % num_experts if len(local) < num_experts else local.start
-
-
 class FfnGraphRunner:
     def __init__(self, experts: Dict[int, torch.nn.Module], max_tokens: int, local: range, act: str = "bf16"):
         first = next(iter(experts.values()))
-        hidden, topk, num_experts = first.hidden_size, first.top_k, first.num_experts
+        hidden = first.hidden_size
         self.buckets = graph_buckets(max_tokens)
-        self.pad_id = pad_id_for(local, num_experts)
+        self.local = local
+        self.quantized = act != "bf16"
         device = torch.cuda.current_device()
-        n = self.buckets[-1]
-        if act == "bf16":
-            self.x = (torch.zeros(n, hidden, dtype=torch.bfloat16, device=device),)
-        else:
-            shape, dtype = act_scale_shape(act, n, hidden)
-            # zero codes with scale 1.0 (UE8M0 127): padding rows stay finite
-            self.x = (torch.zeros(n, hidden, dtype=torch.uint8, device=device),
-                      torch.full(shape, 127 if act == "mxfp8" else 1.0, dtype=dtype, device=device))
-        self.ids = torch.full((n, topk), self.pad_id, dtype=torch.int32, device=device)
-        self.w = torch.zeros(n, topk, dtype=torch.float32, device=device)
-        self.outs = [torch.zeros(n, hidden, dtype=torch.bfloat16, device=device) for _ in range(2)]
+        self.desc = new_job_desc(device)  # n = 0 until the first job: a replay then does nothing
+        self.outs = [torch.zeros(max_tokens, hidden, dtype=torch.bfloat16, device=device) for _ in range(2)]
         self.graphs: Dict[tuple, torch.cuda.CUDAGraph] = {}
         tic = time.perf_counter()
         pool = torch.cuda.graph_pool_handle()
         stream = torch.cuda.Stream()
         for b in reversed(self.buckets):
-            topk_output = StandardTopKOutput(self.w[:b], self.ids[:b], None)
-            x = tuple(t[:b] for t in self.x)
             for layer_id, layer in experts.items():
-                call = layer if act == "bf16" else layer.forward_q
                 stream.wait_stream(torch.cuda.current_stream())
                 with torch.cuda.stream(stream):  # first call outside the capture
-                    call(*x, topk_output, out=self.outs[0][:b])
+                    layer.call_job(self.desc, b, self.quantized)
                 torch.cuda.current_stream().wait_stream(stream)
-                for k, out in enumerate(self.outs):
-                    graph = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(graph, pool=pool, stream=stream):
-                        call(*x, topk_output, out=out[:b])
-                    self.graphs[(layer_id, b, k)] = graph
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=pool, stream=stream):
+                    layer.call_job(self.desc, b, self.quantized)
+                self.graphs[(layer_id, b)] = graph
         torch.cuda.synchronize()
         self.capture_s = time.perf_counter() - tic
 
-    def run(self, layer_id: int, x, topk_ids, topk_weights, buffer: int = 0) -> Optional[torch.Tensor]:
-        """The expert output of the job's rows in output buffer ``buffer`` (0 or 1), or None
-        if the job is larger than the largest bucket (the caller runs it eagerly). ``x`` is a
-        bf16 tensor, or a tuple of the rows' tensors in the runner's activation format."""
+    def run(self, layer_id: int, x, topk_ids, topk_weights, buffer: int = 0,
+            out: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+        """Enqueue the expert call of the job's rows on the current stream and return its
+        output: ``out`` if given (bf16 [n, H]), else output buffer ``buffer`` (0 or 1). None if
+        the job is larger than the largest bucket (the caller runs it eagerly). ``x`` is a bf16
+        tensor, or the tuple of the rows' tensors in the runner's activation format. The
+        inputs must stay alive until the replay has run (stream order)."""
         x = x if isinstance(x, tuple) else (x,)
-        if len(x) != len(self.x):
-            raise ValueError(f"the graphs take {len(self.x)} activation tensors, got {len(x)}")
+        if len(x) != (2 if self.quantized else 1):
+            raise ValueError(f"the graphs take {2 if self.quantized else 1} activation tensors, got {len(x)}")
         n = topk_ids.shape[0]
         i = bisect.bisect_left(self.buckets, n)
         if i == len(self.buckets):
             return None
-        b = self.buckets[i]
-        for dst, src in zip(self.x, x):
-            dst[:n].copy_(src)
-        self.ids[:n].copy_(topk_ids)
-        self.w[:n].copy_(topk_weights)
-        if n < b:
-            self.ids[n:b].fill_(self.pad_id)
-            self.w[n:b].zero_()
-        self.graphs[(layer_id, b, buffer)].replay()
-        return self.outs[buffer][:n]
+        if out is None:
+            out = self.outs[buffer][:n]
+        ids = topk_ids.to(torch.int32).contiguous()
+        w = topk_weights.to(torch.float32).contiguous()
+        if self.quantized:
+            set_job(self.desc, xq=x[0].contiguous(), xs=x[1].contiguous(), ids=ids, w=w, out=out)
+        else:
+            set_job(self.desc, x=x[0].contiguous(), ids=ids, w=w, out=out)
+        self.graphs[(layer_id, self.buckets[i])].replay()
+        return out

@@ -154,20 +154,19 @@ class FfnScheduler:
                 x = tuple(torch.cat(part) for part in zip(*(r[0] for r in rows)))
                 topk_ids, topk_weights = (torch.cat(part) for part in zip(*(r[1:] for r in rows)))
             n = topk_ids.shape[0]
-            output, buffer = None, 0
+            output, buffer, used_buffer = None, 0, False
             reply = self.reply_stream
+            out = None
+            if len(job.rows) == 1:  # write the partial sum straight into A's segment
+                out = self.server.seg_view(job.rows[0])
             if self.graph_runner is not None and n <= self.graph_runner.buckets[-1]:
-                if reply is not None:
-                    buffer = self.reply_turn
+                if out is None and reply is not None:
+                    buffer, used_buffer = self.reply_turn, True
                     # the reply that last read this buffer, before the replay overwrites it
                     stream.wait_event(self.reply_free[buffer])
-                output = self.graph_runner.run(job.layer_id, x, topk_ids, topk_weights, buffer)
-            from_graph = output is not None
+                output = self.graph_runner.run(job.layer_id, x, topk_ids, topk_weights, buffer, out=out)
             if output is None:
                 topk_output = StandardTopKOutput(topk_weights, topk_ids, None)
-                out = None
-                if len(job.rows) == 1:  # write the partial sum straight into A's segment
-                    out = self.server.seg_view(job.rows[0])
                 layer = self.experts[job.layer_id]
                 if len(x) == 1:
                     output = layer(x[0], topk_output, out=out)
@@ -186,7 +185,7 @@ class FfnScheduler:
             self.server.reply(row, output[start].data_ptr(), nbytes, rstream.cuda_stream)
             start += row.n_tokens
         self.layer_calls[job.layer_id] += 1
-        if reply is not None and from_graph:
+        if used_buffer:
             self.reply_free[buffer].record(reply)
             self.reply_turn = 1 - buffer
         if timer:

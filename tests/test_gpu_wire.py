@@ -116,12 +116,13 @@ def test_loop_fp8_on_the_wire(act, graphs):
 
 
 @pytest.mark.parametrize("act", ["mxfp8", "fp8_1x128"])
-def test_grouped_rows_fp8_on_the_wire(act):
+@pytest.mark.parametrize("graphs", [0, 64])
+def test_grouped_rows_fp8_on_the_wire(act, graphs):
     """Two A ranks of one replica: their rows form one F job (the codes and the scales are
     concatenated row by row); each rank's answer equals the expert call on its own rows."""
-    say(f"loop: {act} on the wire, a group of 2 A ranks")
+    say(f"loop: {act} on the wire, a group of 2 A ranks, graph_max_tokens={graphs}")
     experts = make_experts(act, 64)
-    with OneGpuAfd(experts, n_max=64, act=act, group=2) as afd:
+    with OneGpuAfd(experts, n_max=64, act=act, group=2, graph_max_tokens=graphs) as afd:
         sends = [torch.cuda.Stream() for _ in range(2)]
         main = torch.cuda.current_stream()
         keep, tickets = [], []

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from oracle import routing as R
-from sgl_asap_amd.runner.graph_runner import graph_buckets, pad_id_for
+from sgl_asap_amd.runner.graph_runner import graph_buckets
 from sgl_asap_amd.runner.scheduler import local_experts
 
 CASES = [
@@ -71,13 +71,8 @@ def test_graph_and_ep_rules_known_answers():
     assert R.graph_buckets(16384) == [1 << i for i in range(15)]
     assert R.graph_buckets(48) == [1, 2, 4, 8, 16, 32, 48]
     assert R.graph_buckets(1) == [1]
-    assert R.graph_pad_id(range(0, 64), 256) == 64
-    assert R.graph_pad_id(range(192, 256), 256) == 0
-    assert R.graph_pad_id(range(0, 64), 64) == 0
     assert R.local_experts(1, 4, 256) == range(64, 128)
     for m in (1, 2, 3, 48, 64, 100, 16384):
         assert graph_buckets(m) == R.graph_buckets(m)
-    for lo, hi, ne in ((0, 64, 256), (192, 256, 256), (0, 64, 64), (8, 16, 32)):
-        assert pad_id_for(range(lo, hi), ne) == R.graph_pad_id(range(lo, hi), ne)
     for f in range(4):
         assert local_experts(f, 4, 256) == R.local_experts(f, 4, 256)
