@@ -105,6 +105,17 @@ __device__ __forceinline__ uint32_t pk_e4m3(float lo, float hi) {
          0xffffu;
 }
 
+// Exchange between the lane halves of a wavefront: lane l < 32 receives hi_sends of lane
+// l + 32, lane l >= 32 receives lo_sends of lane l - 32 (lk = l / 32). One
+// v_permlane32_swap (VALU) instead of a ds_bpermute through the LDS crossbar.
+__device__ __forceinline__ uint32_t swap_halves(uint32_t lo_sends, uint32_t hi_sends, int lk) {
+  const auto r = __builtin_amdgcn_permlane32_swap(hi_sends, lo_sends, false, false);
+  return lk ? r[0] : r[1];
+}
+__device__ __forceinline__ float xor32(float v, int lk) {
+  return __uint_as_float(swap_halves(__float_as_uint(v), __float_as_uint(v), lk));
+}
+
 // Four clamped fp32 -> four e4m3fn bytes (element i in byte i).
 __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d) {
   int lo = __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(a), clamp_e4m3(b), 0, false);

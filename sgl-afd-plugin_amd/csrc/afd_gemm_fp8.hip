@@ -404,7 +404,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
             h[i2][q] = fn(acc[i2][0][q], acc[i2][1][q]);
             m = fmaxf(m, fabsf(h[i2][q]));
           }
-          m = fmaxf(m, __shfl_xor(m, 32));
+          m = fmaxf(m, xor32(m, lk));
           if (lk == 0) amax_l[(wm * 64 + i2 * 32 + lr) * 4 + wn] = m;
         }
         __syncthreads();
@@ -421,8 +421,8 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
                              h[i2][4 * q4 + 3] / sc);
           // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
           // 16-31 (the partner's d2, d3 and its own)
-          const uint32_t p0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[0] : d[2]), 32));
-          const uint32_t p1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[1] : d[3]), 32));
+          const uint32_t p0 = swap_halves(d[2], d[0], lk);
+          const uint32_t p1 = swap_halves(d[3], d[1], lk);
           v4i chunk;
           chunk[0] = static_cast<int>(lk ? p0 : d[0]);
           chunk[1] = static_cast<int>(lk ? d[2] : p0);
@@ -461,8 +461,9 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
         const int idx = q * kThreads + t;
         const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
         if (row < nvalid)
-          *reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8) =
-              *reinterpret_cast<const v4i*>(yl + row * kYStride + c * 8);
+          __builtin_nontemporal_store(
+              *reinterpret_cast<const v4i*>(yl + row * kYStride + c * 8),
+              reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
       }
       __syncthreads();
     }

@@ -384,7 +384,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
               h[q] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
               amax = fmaxf(amax, fabsf(h[q]));
             }
-            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            amax = fmaxf(amax, xor32(amax, lk));
             const uint32_t code = mx_scale_code(amax, 8);
             const float inv = mx_inv_scale(code);
             uint32_t d[4];  // h columns 8 q4 + 4 lk .. + 3
@@ -394,8 +394,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
                                h[4 * q4 + 3] * inv);
             // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
             // 16-31 (the partner's d2, d3 and its own)
-            const uint32_t p0 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[0] : d[2]), 32));
-            const uint32_t p1 = static_cast<uint32_t>(__shfl_xor(static_cast<int>(lk ? d[1] : d[3]), 32));
+            const uint32_t p0 = swap_halves(d[2], d[0], lk);
+            const uint32_t p1 = swap_halves(d[3], d[1], lk);
             v4i chunk;
             chunk[0] = static_cast<int>(lk ? p0 : d[0]);
             chunk[1] = static_cast<int>(lk ? d[2] : p0);
@@ -421,7 +421,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
       // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
       // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile: one 8-byte LDS write per
-      // group of four. Rows [0, nvalid) of this tile are real.
+      // group of four. Rows [0, nvalid) of this tile are real. The stores are non-temporal:
+      // y (np x H bf16) is read once, by the finalize, and does not fit in L2 anyway.
       const int nvalid = min(kBM, row_end - m0);
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
       static_for<2>([&](auto ic) {
@@ -445,8 +446,9 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         const int idx = q * T::kThreads + t;
         const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
         if (row < nvalid)
-          *reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8) =
-              *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8);
+          __builtin_nontemporal_store(
+              *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8),
+              reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
       }
       __syncthreads();
     }
