@@ -14,8 +14,8 @@ constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments 
 
 
 // Where a launch finds its job: the fields by value, or (desc != nullptr) read from the job
-// descriptor in device memory when the kernel runs, n then clamped to [0, n] as given here
-// (the n_cap the grids and the workspace were sized for).
+// descriptor in device memory when the kernel runs, its n then clamped to [0, n], n being
+// here the n_cap the grids and the workspace were sized for.
 struct JobIn {
   const afd_job* desc;
   const uint16_t* x;
@@ -37,15 +37,15 @@ __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   return j;
 }
 
-// Routing of the job's pairs into the workspace; with x, the activation quantization into
-// ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs beside the
-// expert histogram. `mid` (optional) is recorded between the two launches.
 // Activation quantization as the expert call applies it (MXFP8 with stage-order scales, or
 // FP8 1x128, by cfg.weight_fmt) into q / s.
 int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
                      hipStream_t stream);
 
-// With quantize = false the launch only routes (the rows are quantized already).
+// Routing of the job's pairs into the workspace; with quantize, the activation quantization
+// of job.x into ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs
+// beside the expert histogram (without, the rows are quantized already). `mid` (optional)
+// is recorded between the two launches.
 int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
                        const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid);
 
