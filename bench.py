@@ -201,6 +201,39 @@ def _mxfp4_layer(W, shape, dev, n_max, seed=1):
     return AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n_max)
 
 
+def small_jobs(W, shape, dev, sizes=(256, 512, 1024, 2048)) -> list:
+    """Single small jobs of the stream's shape through the eager expert call: at these sizes
+    the layer is bound by streaming the touched experts' weights from HBM. Compulsory bytes =
+    weights of the local experts with at least one pair + x + out + ids + w."""
+    import torch
+
+    from sgl_asap_amd.moe.topk import StandardTopKOutput
+
+    experts = _mxfp4_layer(W, shape, dev, max(sizes))
+    per_expert = (experts.weights.w13.numel() + experts.weights.w2.numel()) // shape.num_local
+    rows = []
+    for n in sizes:
+        x, ids, w = W.job(shape, n=n, seed=900 + n, device=dev)
+        topk = StandardTopKOutput(w.to(torch.float32), ids.to(torch.int32))
+        rel = ids - shape.local.start
+        touched = int(torch.unique(rel[(rel >= 0) & (rel < shape.num_local)]).numel())
+        nbytes = touched * per_expert + n * shape.hidden * 4 + n * shape.top_k * 8
+        for _ in range(20):
+            experts(x, topk)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            experts(x, topk)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        rows.append({"tokens": n, "experts_touched": touched, "ms": round(ms, 4),
+                     "compulsory_bytes": nbytes, "hbm_gbps": round(nbytes / (ms * 1e-3) / 1e9, 1)})
+    del experts
+    torch.cuda.empty_cache()
+    return rows
+
+
 def bench_stream(args) -> dict:
     """The skewed job stream: Zipf(1.2) routing, job sizes log-uniform in [256, 16384], jobs
     arriving from 2 A replicas x 2 micro-batches (round robin) through the one-GPU transport
@@ -284,6 +317,7 @@ def bench_stream(args) -> dict:
         afd.close()
         del experts, afd
         torch.cuda.empty_cache()
+    out["small_jobs"] = small_jobs(W, shape, dev)
     out["value"] = out["graphs"]["tflops"]
     out["ms_per_step"] = out["graphs"]["ms"]
     out["tokens_per_s"] = out["graphs"]["tokens_per_s"]
@@ -354,6 +388,21 @@ def bench_loop(args) -> dict:
     # the copy; bit-identical outputs, half the copy bytes, no quantizer on the F side)
     lat_fp8 = measure("mxfp8")
     lat = measure("bf16")
+    # the A-side combine alone at this size: 1 F part + the shared output -> bf16
+    from sgl_asap_amd.moe.dispatcher import combine_parts
+
+    part = torch.randn(n, shape.hidden, device=dev).to(torch.bfloat16)
+    sh = torch.randn(n, shape.hidden, device=dev).to(torch.bfloat16)
+    for _ in range(5):
+        combine_parts([part.data_ptr()], sh, n, shape.hidden, dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        combine_parts([part.data_ptr()], sh, n, shape.hidden, dev)
+    e1.record()
+    torch.cuda.synchronize()
+    comb_ms = e0.elapsed_time(e1) / 20
+    comb_bytes = 3 * n * shape.hidden * 2
     ms = statistics.median(lat)
     ms_fp8 = statistics.median(lat_fp8)
     return {
@@ -376,6 +425,8 @@ def bench_loop(args) -> dict:
         "layer_latency_ms_min": round(min(lat), 4),
         "tokens_per_s": round(2 * n / (ms * 1e-3), 1),
         "tflops_routed_plus_shared": round((routed_flops + shared_flops) / (ms * 1e-3) / 1e12, 2),
+        "combine": {"ms": round(comb_ms, 4), "bytes": comb_bytes,
+                    "hbm_gbps": round(comb_bytes / (comb_ms * 1e-3) / 1e9, 1)},
         "wire": "bf16",
         "fp8_wire": {"act": "mxfp8", "layer_latency_ms": round(ms_fp8, 4),
                      "layer_latency_ms_min": round(min(lat_fp8), 4),
