@@ -122,11 +122,15 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   // scale half h, at offsets given by the pair indices of those rows. Padding rows (-1) read
   // token 0; their results are never stored.
   const int s_half = (w_u / T::kImgs) & 1;
-  int sp_next[T::kQP + 1], e_next = 0;
+  // Each wavefront also loads the pair indices of its group's 64 rows: an expert's padding
+  // rows (-1) come last in its segment, so a ballot counts the group's real rows, and MFMAs
+  // of 32-row blocks with no real row are skipped (their rows are never stored).
+  int sp_next[T::kQP + 1], e_next = 0, own_next = -1;
   auto load_next = [&](int ii) {
     int m, nn;
     walk.at(ii, m, nn);
     e_next = p.tile_expert[m];
+    own_next = p.sorted_pairs[m * kBM + 64 * wm + lane];
     if constexpr (MODE != kDown) {
 #pragma unroll
       for (int q = 0; q < T::kQP; ++q)
@@ -134,10 +138,11 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       sp_next[T::kQP] = p.sorted_pairs[m * kBM + 64 * s_half + lane];
     }
   };
-  int e_cur = 0;
+  int e_cur = 0, live_cur = 0;
   uint32_t a_voff[T::kQP] = {}, s_voff = 0;
   auto decode_next = [&]() {
     e_cur = __builtin_amdgcn_readfirstlane(e_next);
+    live_cur = __popcll(__ballot(own_next >= 0));  // real rows of this group, a scalar
     if constexpr (MODE != kDown) {
       auto token = [&](int sp) {
         return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
@@ -225,6 +230,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
     const bool has_next = i_next < walk.count;
+    // 32-row blocks i of this group with a real row
+    const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
     if (has_next) load_next(i_next);
     if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
@@ -284,9 +291,10 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
           static_for<4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
             // D[weight row][activation row]; op_sel ks: byte ks of the lane's scale half-word
-            acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
-                                          0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
-                                          static_cast<int>(f.sa[i2]));
+            if (i2 == 0 ? live_i0 : live_i1)
+              acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
+                                            0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
+                                            static_cast<int>(f.sa[i2]));
             if constexpr (Copy) {
               constexpr int m = ks * 8 + i2 * 4 + j;
               if constexpr ((m & 1) && m / 2 < T::kPieces)
