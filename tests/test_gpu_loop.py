@@ -187,3 +187,32 @@ def test_graph_replays_match_eager_every_time():
             got_bits = bits16(got)
             want = direct(experts, 0, x, topk)  # eager work between the replays
             assert np.array_equal(got_bits, want), (rep, n)
+
+
+@pytest.mark.parametrize("graphs", [0, 64])
+def test_group_of_two_a_ranks(graphs):
+    """Two A ranks of one replica (a TP group): their rows form one F job, concatenated row
+    by row; each rank's answer equals the expert call on its own rows (eager and graphs)."""
+    say(f"loop: a group of 2 A ranks, bf16, graph_max_tokens={graphs}")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, group=2, graph_max_tokens=graphs) as afd:
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        main = torch.cuda.current_stream()
+        for rnd in range(2):
+            keep, tickets = [], []
+            for r in range(2):
+                x, topk = job(13 + 17 * r + rnd, 700 + 10 * rnd + r)
+                ids = topk.topk_ids.to(torch.int32).contiguous()
+                w = topk.topk_weights.to(torch.float32).contiguous()
+                sends[r].wait_stream(main)
+                tickets.append(afd.channels[r].send(0, 0, x.data_ptr(), ids.data_ptr(), w.data_ptr(), x.shape[0],
+                                                    sends[r]))
+                keep.append((x, topk, ids, w))
+            assert afd.scheduler.serve_pending() == 1
+            for r, (t, (x, topk, _, _)) in enumerate(zip(tickets, keep)):
+                ptr = afd.channels[r].wait(t, main)[0]
+                got = torch.empty(x.shape[0], H, dtype=torch.bfloat16, device=dev())
+                _lib_copy(got, ptr)
+                torch.cuda.synchronize()
+                assert np.array_equal(bits16(got), direct(experts, 0, x, topk)), (rnd, r)
+        assert afd.server.stats["jobs"] == 2
