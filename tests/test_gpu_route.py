@@ -64,6 +64,8 @@ CASES = [
     (16384, 8, 256, 0, 64, 6),
     (2048, 6, 64, 0, 64, 7),
     (777, 32, 256, 0, 256, 8),
+    (131071, 8, 256, 0, 64, 9),  # the largest job a doorbell announces: 1M pairs, 128 chunks
+    (131071, 1, 256, 0, 256, 10),
 ]
 
 
