@@ -104,3 +104,23 @@ def test_subset_against_oracle(layer):
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
     assert err <= 1e-2
     assert not got[~has_kept[sub]].any()  # tokens with no local expert are exactly 0
+
+
+def test_largest_job_rows_match_a_subset():
+    """131071 tokens (the most a doorbell announces; token rows addressed with 32-bit byte
+    offsets up to 2^29): the rows of a 2000-token subset equal the full job's bit for bit."""
+    shape = W.SHAPES["dsv4_rank"]
+    n = 131071
+    say(f"largest job: {n} tokens, {shape.name} shape")
+    gen = W.generator("cpu", 2)
+    w13, w2 = W.expert_weights(shape.num_local, shape.hidden, shape.inter, gen, "cpu")
+    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, pack_mxfp4_experts(w13, w2, device=dev()),
+                         n_max=n)
+    del w13, w2
+    x, ids, w = W.job(shape, n=n, seed=3, device=dev())
+    ids, w = ids.to(torch.int32), w.to(torch.float32)
+    full = bits16(call(experts, x, ids, w))
+    sub = torch.cat([torch.arange(0, 1000), torch.arange(n - 1000, n)]).to(dev())
+    assert np.array_equal(bits16(call(experts, x[sub], ids[sub], w[sub])), full[sub.cpu().numpy()])
+    del experts
+    torch.cuda.empty_cache()
