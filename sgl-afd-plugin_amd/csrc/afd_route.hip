@@ -80,7 +80,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   const int32_t* __restrict__ ids = job.ids;
   const int64_t pairs = job.n * topk;
   constexpr int kWaves = kRouteThreads / 64;
-  constexpr int kMaxPer = kMaxChunks / (kRouteThreads / kMaxLocalExperts);
   __shared__ int run[kMaxLocalExperts + 1];
   __shared__ int wcnt[kWaves][kMaxLocalExperts + 1];
   __shared__ int part_all[kRouteThreads], part_before[kRouteThreads];
@@ -88,20 +87,23 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   __shared__ int pof[kMaxLocalExperts + 1];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int c = blockIdx.x;
-  // Expert e's chunks are split over G = kRouteThreads / num_local threads (e, g), each a
-  // contiguous run of at most kMaxPer chunks loaded at once: the counts in all chunks and in
-  // the chunks before this one.
+  const int64_t lo = int64_t(c) * chunk;
+  const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
+  // the chunk's first 256 ids are loaded now, so their latency overlaps the histogram pass
+  const int id_first = lo + t < hi ? ids[lo + t] : 0;
+  // Expert e's chunks are split over G = kRouteThreads / num_local threads (e, g), each summing
+  // a contiguous run of them: the counts in all chunks and in the chunks before this one.
   const int G = kRouteThreads / num_local;
   const int per = (chunks + G - 1) / G;
   const int e = t % num_local, g = t / num_local;
   const bool active = g < G;
   const int c0 = active ? g * per : 0, c1 = active ? min(c0 + per, chunks) : 0;
   int all = 0, before = 0;
-#pragma unroll
-  for (int k = 0; k < kMaxPer; ++k) {
-    const int h = c0 + k < c1 ? hist[int64_t(c0 + k) * num_local + e] : 0;
+#pragma unroll 4
+  for (int k = c0; k < c1; ++k) {
+    const int h = hist[int64_t(k) * num_local + e];
     all += h;
-    before += c0 + k < c ? h : 0;
+    before += k < c ? h : 0;
   }
   part_all[t] = all;
   part_before[t] = before;
@@ -171,13 +173,12 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
       for (int r = pof[e] + tot[e] + g; r < pof[e + 1]; r += G) sorted_pairs[r] = -1;
   }
   __syncthreads();
-  const int64_t lo = int64_t(blockIdx.x) * chunk;
-  const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
   const uint64_t below = (uint64_t(1) << lane) - 1;
   for (int64_t base = lo; base < hi; base += kRouteThreads) {
     const int64_t i = base + t;
     const bool live = i < hi;
-    const int key = live ? pair_key(ids[i], e_lo, num_local) : num_local;
+    const int id = base == lo ? id_first : live ? ids[i] : 0;
+    const int key = live ? pair_key(id, e_lo, num_local) : num_local;
     // lanes with the same key (dead lanes join the "not local" key and are ignored)
     uint64_t peers = __ballot(1);
 #pragma unroll
