@@ -279,11 +279,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
 #pragma unroll
       for (int j = 0; j < 4; ++j) f.sb[j] = sb[2 * (brow + j * 32 + lr)];
     };
-    // the 16 MFMAs of a stage; with Copy, this wavefront's pieces of stage copy_kt are issued
-    // one after every second MFMA (copy instructions are ordering points for the compiler,
-    // so the interleave holds)
-    auto mma_stage = [&](auto copy, int copy_kt) {
-      constexpr bool Copy = decltype(copy)::value;
+    // the 16 MFMAs of a stage (blocks of padding rows skipped)
+    auto mma_stage = [&]() {
       static_for<2>([&](auto ksc) {
         constexpr int ks = decltype(ksc)::value;
         static_for<2>([&](auto i2c) {
@@ -295,11 +292,6 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
               acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
                                             0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
                                             static_cast<int>(f.sa[i2]));
-            if constexpr (Copy) {
-              constexpr int m = ks * 8 + i2 * 4 + j;
-              if constexpr ((m & 1) && m / 2 < T::kPieces)
-                issue_piece(copy_kt, std::integral_constant<int, m / 2>{});
-            }
           });
         });
       });
@@ -335,7 +327,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage(std::false_type{}, 0);
+        mma_stage();
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         wait_vmcnt<T::kPieces>();  // own pieces of stage kt+1 landed
@@ -351,7 +343,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage(std::false_type{}, 0);
+        mma_stage();
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
