@@ -473,15 +473,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
 template <int MODE>
 static int launch(Fp8GemmArgs p, int max_row_tiles, hipStream_t stream) {
   if (p.K % kBK || p.N % kBN || p.K / kBK > kMaxKT) return AFD_ERR_SHAPE;
-  static int per_cu = 0;  // resident workgroups per CU (registers and LDS decide)
-  if (per_cu == 0) {
+  // resident workgroups per CU (registers and LDS decide); initialized once, thread-safely
+  static const int per_cu = [] {
     int b = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fp8_gemm_kernel<MODE>, kThreads, 0) !=
             hipSuccess ||
         b < 1)
       b = 1;
-    per_cu = b;
-  }
+    return b;
+  }();
   const int max_tiles = max_row_tiles * (p.N / kBN);
   p.ncb_magic = div_magic(walk_col_blocks<kWalkRows>(p.N / kBN));
   int grid = device_cu_count() * per_cu;

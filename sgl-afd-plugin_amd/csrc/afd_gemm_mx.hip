@@ -458,15 +458,15 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
 template <int MODE, int WN>
 static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream) {
   using T = MxTile<WN>;
-  static int per_cu = 0;  // resident workgroups per CU (registers and LDS decide)
-  if (per_cu == 0) {
+  // resident workgroups per CU (registers and LDS decide); initialized once, thread-safely
+  static const int per_cu = [] {
     int b = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE, WN>, T::kThreads,
                                                      0) != hipSuccess ||
         b < 1)
       b = 1;
-    per_cu = b;
-  }
+    return b;
+  }();
   const int max_tiles = max_row_tiles * (p.N / T::kBN);
   MxGemmArgs a = p;
   a.ncb_magic = div_magic(walk_col_blocks<kMxWalkRows>(p.N / T::kBN));
