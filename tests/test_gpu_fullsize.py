@@ -8,8 +8,11 @@ the oracle to run the whole job:
 * weights: doubling w doubles every output exactly (products, fp32 sums and the bf16
   rounding all scale by 2);
 * the job read from a device descriptor equals the by-value call;
-and, for the MXFP4 layer, the tokens of 4 of its experts against the oracle on the
-dequantized weights (rel-L2 1e-2)."""
+and tokens of a few experts against the oracle on the dequantized weights (rel-L2 1e-2):
+for the MXFP4 layer the tokens of 4 of its experts, for the FP8 block layer (every expert
+local, 8 per token) the tokens whose 8 experts are all among its 16 most used."""
+
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -81,11 +84,10 @@ def test_descriptor_call_equals_by_value(layer):
 def test_subset_against_oracle(layer):
     """Tokens whose local experts all lie in [e_lo, e_lo + 4) (plus tokens with no local
     expert), against the oracle run with those 4 experts only: the oracle's weight
-    quantization of all 64 experts would take minutes on the CPU. The FP8 layer's shape is
-    covered against the oracle at reduced size (test_gpu_moe)."""
+    quantization of all 64 experts would take minutes on the CPU."""
     shape, experts, (w13, w2), (xc, idsc, wc), _, out = layer
     if shape.fmt != "mxfp4":
-        pytest.skip("FP8 block layer: oracle comparison at reduced size in test_gpu_moe")
+        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
     say(f"{shape.name}: tokens of 4 experts against the oracle")
     lo, keep = shape.local.start, 4
     ids = idsc.numpy()
@@ -104,6 +106,40 @@ def test_subset_against_oracle(layer):
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
     assert err <= 1e-2
     assert not got[~has_kept[sub]].any()  # tokens with no local expert are exactly 0
+
+
+def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
+    """The FP8 block layer has every expert local and 8 per token, so no token stays within
+    4 experts: take the tokens whose 8 experts are all among the ``keep`` most used, renumber
+    those experts 0..keep-1 (a token's result does not depend on the numbering: its pairs,
+    their k order and the finalize sum are unchanged) and run the oracle with them only,
+    quantizing the experts on a thread pool."""
+    w13, w2 = weights
+    xc, idsc, wc = job
+    lo = shape.local.start
+    rel = idsc.numpy() - lo
+    counts = np.bincount(rel.ravel(), minlength=len(shape.local))
+    chosen = np.argsort(-counts, kind="stable")[:keep]
+    table = np.full(len(shape.local), -1, dtype=np.int64)
+    table[chosen] = np.arange(keep)
+    sub = np.nonzero((table[rel] >= 0).all(axis=1))[0][:256]
+    say(f"{shape.name}: {len(sub)} tokens of the {keep} most used experts against the oracle")
+    assert len(sub) >= 128
+
+    def deq(e):
+        c13, s13 = F.fp8_block_quantize_2d(w13[e:e + 1].numpy())
+        c2, s2 = F.fp8_block_quantize_2d(w2[e:e + 1].numpy())
+        return F.fp8_block_dequantize_2d(c13, s13)[0], F.fp8_block_dequantize_2d(c2, s2)[0]
+
+    with ThreadPoolExecutor(8) as pool:
+        parts = list(pool.map(deq, chosen.tolist()))
+    w13d = np.stack([p[0] for p in parts])
+    w2d = np.stack([p[1] for p in parts])
+    ids = table[rel[sub]].astype(np.int32)
+    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="fp8_1x128")
+    err = rel_l2(F.bf16_to_f32(bits16(out)[sub]), F.bf16_to_f32(ref))
+    say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
+    assert err <= 1e-2
 
 
 def test_largest_job_rows_match_a_subset():
