@@ -76,11 +76,14 @@ enum afd_wait_cond { AFD_WAIT_GEQ = 0, AFD_WAIT_EQ = 1, AFD_WAIT_AND = 2, AFD_WA
 /* Activation of the gate_up output (FusedMoE's moe_runner_config.activation). */
 enum afd_activation {
   AFD_ACT_SWIGLU = 0, /* h = silu(gate) * up ("silu") */
-  AFD_ACT_SITU = 1    /* h = L tanh(up / L) * A tanh(gate / A) * sigmoid(gate) ("situ"), with
+  AFD_ACT_SITU = 1,   /* h = L tanh(up / L) * A tanh(gate / A) * sigmoid(gate) ("situ"), with
                          A = act_alpha (SiTU's beta, FusedMoE gemm1_alpha) and L = act_limit
                          (its linear_beta, gemm1_clamp_limit): the function the reference's
                          SiTU hook runs, python/sgl_asap_plugin/srt/layers/quantization/
                          mxfp4_flashinfer_trtllm_moe.py:13-16 */
+  AFD_ACT_SWIGLU_LIMIT = 2 /* h = silu(min(gate, L)) * clamp(up, -L, L), L = act_limit: SwiGLU
+                              with DeepSeek-V4's swiglu_limit, which the reference hands to
+                              FusedMoE (python/sgl_asap_plugin/srt/models/deepseek_v4.py:63) */
 };
 
 /* Shape of one MoE layer on one F rank. Experts [expert_lo, expert_lo + num_local) are
@@ -95,8 +98,8 @@ typedef struct afd_moe_cfg {
   int32_t num_local;
   int32_t weight_fmt; /* enum afd_weight_fmt */
   int32_t activation; /* enum afd_activation (0: SwiGLU) */
-  float act_alpha;    /* SiTU: A > 0 (unused for SwiGLU) */
-  float act_limit;    /* SiTU: L > 0 (unused for SwiGLU) */
+  float act_alpha;    /* SiTU: A > 0 (unused otherwise) */
+  float act_limit;    /* SiTU, SwiGLU with limit: L > 0 and finite (unused for SwiGLU) */
 } afd_moe_cfg;
 
 /* Packed expert weights of one layer (device pointers), as afd_pack_* writes them.

@@ -56,10 +56,27 @@ def situ(g: torch.Tensor, u: torch.Tensor, alpha: float, limit: float) -> torch.
     return (limit * torch.tanh(u / limit)) * (alpha * torch.tanh(g / alpha)) * torch.sigmoid(g)
 
 
+def swiglu_limit(g: torch.Tensor, u: torch.Tensor, limit: float) -> torch.Tensor:
+    """SwiGLU with a limit: ``silu(min(g, limit)) * clamp(u, -limit, limit)``, DeepSeek-V4's
+    ``swiglu_limit``, which the reference passes to FusedMoE
+    (python/sgl_asap_plugin/srt/models/deepseek_v4.py:63) and SGLang hands to the MoE kernel
+    as gemm1_clamp_limit; the clamped-SwiGLU form of the public DeepSeek-V4 and TRT-LLM
+    expert code (gate clamped above only, up on both sides). fp32 torch.
+
+    Pinned (tests/test_oracle_experts.py): equal to SwiGLU wherever no clamp binds and for an
+    infinite limit, values against an independent math-module evaluation of the clamped form,
+    saturation in g above the limit, odd symmetry in u and the bound
+    |h| <= max(silu(limit), 0.2785) * limit."""
+    return _silu(torch.clamp(g, max=limit)) * torch.clamp(u, -limit, limit)
+
+
 def gate_up_act(g: torch.Tensor, u: torch.Tensor, activation: str = "silu", alpha=None, limit=None):
-    """h of the gate_up output: SwiGLU silu(g) * u (SGLang's default activation), or SiTU."""
+    """h of the gate_up output: SwiGLU silu(g) * u (SGLang's default activation), SwiGLU with
+    a limit ("swiglu_limit") or SiTU."""
     if activation == "silu":
         return _silu(g) * u
+    if activation == "swiglu_limit":
+        return swiglu_limit(g, u, limit)
     if activation == "situ":
         return situ(g, u, alpha, limit)
     raise NotImplementedError(activation)
@@ -120,7 +137,8 @@ def moe_ffn(
     x_bf16: torch bf16 [n, H] (CPU). ids int32 [n, k] global ids. w fp32 [n, k].
     w13_deq: fp32 [E, 2I, H] logical rows [gate; up], dequantized. w2_deq: fp32 [E, H, I].
     act: activation quantizer applied to x and to h ("mxfp8", "fp8_1x128" or "bf16").
-    activation: the gate_up activation, "silu" (SwiGLU) or "situ" with act_alpha, act_limit.
+    activation: the gate_up activation, "silu" (SwiGLU), "swiglu_limit" with act_limit, or
+    "situ" with act_alpha, act_limit.
     Returns bf16 bits uint16 [n, H] (and the intermediates when return_parts).
     """
     n, hdim = x_bf16.shape

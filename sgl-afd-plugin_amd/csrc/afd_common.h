@@ -143,6 +143,10 @@ __device__ __forceinline__ float act_swiglu(float g, float u) {
 __device__ __forceinline__ float tanh_exp(float x) {
   return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __expf(2.0f * x));
 }
+// SwiGLU with a limit: silu(min(g, L)) * clamp(u, -L, L)
+__device__ __forceinline__ float act_swiglu_limit(float g, float u, float l) {
+  return act_swiglu(fminf(g, l), fminf(fmaxf(u, -l), l));
+}
 // SiTU: L tanh(u / L) * A tanh(g / A) * sigmoid(g)
 __device__ __forceinline__ float act_situ(float g, float u, float a, float inv_a, float l,
                                           float inv_l) {

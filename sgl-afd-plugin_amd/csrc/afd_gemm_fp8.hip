@@ -36,9 +36,10 @@
 namespace afd {
 namespace fp8 {
 
-// gate_up with SwiGLU or with SiTU (separate kernels: SiTU's longer epilogue would raise
-// the register pressure of the SwiGLU kernel), down
-enum { kGateUp = 0, kDown = 1, kGateUpSitu = 2 };
+// gate_up with SwiGLU, gate_up with an activation that takes constants (SiTU, or SwiGLU with
+// a limit: SiTU's longer epilogue would raise the register pressure of the SwiGLU kernel),
+// down
+enum { kGateUp = 0, kDown = 1, kGateUpParam = 2 };
 
 // Tile walk blocks of 8 row tiles x 4 column tiles: a 1 MiB weight slice is shared 8 ways
 // (column-tile-fastest walks fetch ~3x more from beyond L2).
@@ -433,12 +434,16 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
           if (wn == 0 && lk == 0) p.hs[int64_t(m0 + row) * (inter / kBK) + n0 / 256] = sc;
         }
       };
-      if constexpr (MODE == kGateUpSitu)
-        quant_store([&](float g, float u) {
-          return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
-        });
-      else
+      if constexpr (MODE == kGateUpParam) {
+        if (p.act.act == AFD_ACT_SITU)
+          quant_store([&](float g, float u) {
+            return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+          });
+        else
+          quant_store([&](float g, float u) { return act_swiglu_limit(g, u, p.act.l); });
+      } else {
         quant_store([](float g, float u) { return act_swiglu(g, u); });
+      }
     } else {
       const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
       uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
@@ -523,7 +528,7 @@ int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uin
   p.N = 2 * cfg.inter;
   p.hq = ws + L.hq;
   p.hs = reinterpret_cast<float*>(ws + L.hs);
-  return cfg.activation == AFD_ACT_SITU ? fp8::launch<fp8::kGateUpSitu>(p, L.max_tiles, stream)
+  return cfg.activation != AFD_ACT_SWIGLU ? fp8::launch<fp8::kGateUpParam>(p, L.max_tiles, stream)
                                          : fp8::launch<fp8::kGateUp>(p, L.max_tiles, stream);
 }
 

@@ -27,9 +27,10 @@
 
 namespace afd {
 
-// gate_up with SwiGLU or with SiTU (separate kernels: SiTU's longer epilogue would raise
-// the register pressure of the SwiGLU kernel), down
-enum { kGateUp = 0, kDown = 1, kGateUpSitu = 2 };
+// gate_up with SwiGLU, gate_up with an activation that takes constants (SiTU, or SwiGLU with
+// a limit: SiTU's longer epilogue would raise the register pressure of the SwiGLU kernel),
+// down
+enum { kGateUp = 0, kDown = 1, kGateUpParam = 2 };
 
 // Tile walk blocks of 4 row tiles x 8 column tiles: a row tile's gathered activation rows are
 // shared 8 ways (measured faster than 8 x 4 blocks, whose lower HBM traffic does not pay).
@@ -411,12 +412,16 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
           });
         });
       };
-      if constexpr (MODE == kGateUpSitu)
-        quant_store([&](float g, float u) {
-          return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
-        });
-      else
+      if constexpr (MODE == kGateUpParam) {
+        if (p.act.act == AFD_ACT_SITU)
+          quant_store([&](float g, float u) {
+            return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+          });
+        else
+          quant_store([&](float g, float u) { return act_swiglu_limit(g, u, p.act.l); });
+      } else {
         quant_store([](float g, float u) { return act_swiglu(g, u); });
+      }
     } else {
       // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
       // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
@@ -504,7 +509,7 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.N = 2 * cfg.inter;
   p.h_img = ws + L.hq;
   p.y = nullptr;
-  return cfg.activation == AFD_ACT_SITU ? launch_mx_any<kGateUpSitu>(p, L.max_tiles, stream)
+  return cfg.activation != AFD_ACT_SWIGLU ? launch_mx_any<kGateUpParam>(p, L.max_tiles, stream)
                                          : launch_mx_any<kGateUp>(p, L.max_tiles, stream);
 }
 

@@ -171,12 +171,15 @@ static int check_cfg(const afd_moe_cfg* cfg) {
     return AFD_ERR_SHAPE;
   if (cfg->weight_fmt != AFD_W_MXFP4 && cfg->weight_fmt != AFD_W_FP8_BLOCK)
     return AFD_ERR_UNSUPPORTED;
-  if (cfg->activation != AFD_ACT_SWIGLU && cfg->activation != AFD_ACT_SITU)
+  if (cfg->activation != AFD_ACT_SWIGLU && cfg->activation != AFD_ACT_SITU &&
+      cfg->activation != AFD_ACT_SWIGLU_LIMIT)
     return AFD_ERR_UNSUPPORTED;
   // SiTU's two constants are positive and finite (the reference raises ValueError without them)
   if (cfg->activation == AFD_ACT_SITU &&
       !(cfg->act_alpha > 0.0f && cfg->act_alpha < INFINITY && cfg->act_limit > 0.0f &&
         cfg->act_limit < INFINITY))
+    return AFD_ERR_ARG;
+  if (cfg->activation == AFD_ACT_SWIGLU_LIMIT && !(cfg->act_limit > 0.0f && cfg->act_limit < INFINITY))
     return AFD_ERR_ARG;
   return AFD_OK;
 }

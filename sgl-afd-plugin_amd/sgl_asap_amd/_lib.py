@@ -27,6 +27,7 @@ AFD_W_FP8_BLOCK = 2
 
 AFD_ACT_SWIGLU = 0
 AFD_ACT_SITU = 1
+AFD_ACT_SWIGLU_LIMIT = 2
 
 AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 

@@ -181,10 +181,18 @@ def moe_cfg(
 ) -> _lib.AfdMoeCfg:
     """The C config of a layer. ``activation`` is FusedMoE's ("silu": SwiGLU; "situ": SiTU
     with ``gemm1_alpha`` = its beta and ``gemm1_clamp_limit`` = its linear_beta, as the
-    reference's ERNIE 5.5 experts pass them, P/srt/models/ernie55.py:43-55)."""
+    reference's ERNIE 5.5 experts pass them, P/srt/models/ernie55.py:43-55). "silu" with a
+    ``gemm1_clamp_limit`` L is SwiGLU with a limit, silu(min(gate, L)) * clamp(up, -L, L):
+    DeepSeek-V4's ``swiglu_limit`` (P/srt/models/deepseek_v4.py:63)."""
     if activation not in ACTIVATIONS:
         raise NotImplementedError(f"activation {activation!r} (supported: {sorted(ACTIVATIONS)})")
     alpha = limit = 0.0
+    code = ACTIVATIONS[activation]
+    if activation == "silu" and gemm1_clamp_limit is not None:
+        limit = float(gemm1_clamp_limit)
+        if not 0.0 < limit < float("inf"):
+            raise ValueError(f"the SwiGLU limit must be positive and finite, got {limit}")
+        code = _lib.AFD_ACT_SWIGLU_LIMIT
     if activation == "situ":
         if gemm1_alpha is None or gemm1_clamp_limit is None:
             # the reference's message (P/srt/layers/quantization/mxfp4_flashinfer_trtllm_moe.py:110-113)
@@ -196,7 +204,7 @@ def moe_cfg(
             raise ValueError(f"SiTU constants must be positive and finite, got {alpha}, {limit}")
     return _lib.AfdMoeCfg(
         weights.hidden, weights.inter, top_k, expert_lo, weights.num_local, WEIGHT_FORMATS[weights.fmt],
-        ACTIVATIONS[activation], alpha, limit,
+        code, alpha, limit,
     )
 
 
@@ -304,8 +312,13 @@ class AfdExperts(torch.nn.Module):
         activation: str = "silu",
         gemm1_alpha: Optional[float] = None,
         gemm1_clamp_limit: Optional[float] = None,
+        swiglu_limit: Optional[float] = None,
     ):
         super().__init__()
+        if swiglu_limit is not None:  # DeepSeek-V4's FusedMoE argument: the SwiGLU clamp limit
+            if activation != "silu" or (gemm1_clamp_limit is not None and gemm1_clamp_limit != swiglu_limit):
+                raise ValueError("swiglu_limit applies to SwiGLU and is its gemm1_clamp_limit")
+            gemm1_clamp_limit = swiglu_limit
         if len(local) != weights.num_local:
             raise ValueError(f"{len(local)} local experts but weights for {weights.num_local}")
         if not (0 <= local.start and local.stop <= num_experts):

@@ -69,6 +69,8 @@ def test_bad_configs_rejected_on_host():
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, 5),  # unknown activation
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 0.0, 1.0),  # SiTU without beta
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 1.0, float("inf")),
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SWIGLU_LIMIT, 0.0, 0.0),  # no limit
+        _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SWIGLU_LIMIT, 0.0, float("inf")),
     ]
     for cfg in bad:
         assert _lib.lib().afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) != 0
@@ -77,10 +79,11 @@ def test_bad_configs_rejected_on_host():
     assert _lib.lib().afd_workspace_layout(ctypes.byref(good), (1 << 17) - 1, ctypes.byref(out)) == 0
 
 
-def test_situ_config_accepted():
+def test_situ_and_limit_configs_accepted():
     out = _lib.AfdWsLayout()
-    ok = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 2.0, 3.0)
-    assert _lib.lib().afd_workspace_layout(ctypes.byref(ok), 16, ctypes.byref(out)) == 0
+    for ok in (_lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SITU, 2.0, 3.0),
+               _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 1, _lib.AFD_ACT_SWIGLU_LIMIT, 0.0, 10.0)):
+        assert _lib.lib().afd_workspace_layout(ctypes.byref(ok), 16, ctypes.byref(out)) == 0
 
 
 def test_python_activation_arguments():
@@ -96,3 +99,9 @@ def test_python_activation_arguments():
         moe_cfg(wts, 2, 0, "situ", 2.0, None)
     with pytest.raises(NotImplementedError):
         moe_cfg(wts, 2, 0, "gelu")
+    # SwiGLU with a limit: gemm1_clamp_limit on "silu", or DeepSeek-V4's swiglu_limit
+    c = moe_cfg(wts, 2, 0, "silu", None, 10.0)
+    assert (c.activation, c.act_limit) == (_lib.AFD_ACT_SWIGLU_LIMIT, 10.0)
+    for bad in (0.0, -1.0, float("inf")):
+        with pytest.raises(ValueError):
+            moe_cfg(wts, 2, 0, "silu", None, bad)

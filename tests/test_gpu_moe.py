@@ -35,9 +35,11 @@ def deq_weights(w13, w2, fmt):
     return F.fp8_block_dequantize_2d(c13, s13), F.fp8_block_dequantize_2d(c2, s2)
 
 
-def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=None, situ=None):
-    """situ: None for SwiGLU, else SiTU's (gemm1_alpha, gemm1_clamp_limit)."""
-    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed} situ={situ}")
+def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=None, situ=None,
+             swiglu_limit=None):
+    """situ: None for SwiGLU, else SiTU's (gemm1_alpha, gemm1_clamp_limit); swiglu_limit:
+    SwiGLU with that limit (DeepSeek-V4's FusedMoE argument)."""
+    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed} situ={situ} swiglu_limit={swiglu_limit}")
     gen = W.generator("cpu", seed)
     x = W.tokens(n, hidden, gen, "cpu")
     if zipf is None:
@@ -49,12 +51,16 @@ def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=
     weights = pack(w13, w2, device=dev())
     local = range(e_lo, e_lo + num_local)
     act_kw = {} if situ is None else dict(activation="situ", gemm1_alpha=situ[0], gemm1_clamp_limit=situ[1])
+    if swiglu_limit is not None:
+        act_kw = dict(swiglu_limit=swiglu_limit)
     experts = AfdExperts(num_experts, k, 0, local, weights, n_max=max(n, 1), **act_kw)
     out = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
     w13d, w2d = deq_weights(w13, w2, fmt)
     act = "mxfp8" if fmt == "mxfp4" else "fp8_1x128"
     oact = {} if situ is None else dict(activation="situ", act_alpha=situ[0], act_limit=situ[1])
+    if swiglu_limit is not None:
+        oact = dict(activation="swiglu_limit", act_limit=swiglu_limit)
     ref, parts = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13d, w2d, e_lo, act=act, return_parts=True, **oact)
     return experts, out, ref, parts, (x, ids, w)
 
@@ -149,3 +155,22 @@ def test_situ_layers(fmt, alpha, limit, seed):
         1024, 512, 32, 0, 16, 8, 384, fmt, seed, situ=(alpha, limit)
     )
     assert_close(out, ref, ids.numpy(), range(0, 16))
+
+
+@pytest.mark.parametrize(
+    "fmt,limit,seed",
+    [
+        ("mxfp4", 0.5, 31),  # binds on a large share of the gate and up values
+        ("mxfp4", 1.5, 32),  # binds on the tails
+        ("fp8_block", 0.5, 33),
+    ],
+)
+def test_swiglu_limit_layers(fmt, limit, seed):
+    """SwiGLU with DeepSeek-V4's swiglu_limit through both weight formats against the oracle;
+    the limit must change the output (the clamps bind)."""
+    experts, out, ref, parts, (x, ids, w) = run_case(1024, 512, 32, 0, 16, 8, 384, fmt, seed, swiglu_limit=limit)
+    assert_close(out, ref, ids.numpy(), range(0, 16))
+    plain = AfdExperts(32, 8, 0, range(0, 16), experts.weights, n_max=384)
+    base = plain(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
+    torch.cuda.synchronize()
+    assert not np.array_equal(bits16(base), bits16(out))

@@ -178,3 +178,58 @@ def test_situ_layer_reduces_to_swiglu_layer():
     a = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16", activation="situ", act_alpha=1e5, act_limit=1e5)
     b = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16")
     assert rel_l2(F.bf16_to_f32(a).astype(np.float64), F.bf16_to_f32(b).astype(np.float64)) < 1e-3
+
+
+# ---------------------------------------------------------------- SwiGLU with a limit
+def _swiglu_limit_math(g, u, l):
+    """silu(min(g, l)) * clamp(u, -l, l), evaluated independently in float64."""
+    gc = min(g, l)
+    uc = max(-l, min(u, l))
+    return gc / (1.0 + math.exp(-gc)) * uc
+
+
+def test_swiglu_limit_matches_an_independent_evaluation():
+    gen = torch.Generator().manual_seed(11)
+    g = torch.randn(400, generator=gen) * 4
+    u = torch.randn(400, generator=gen) * 4
+    for l in (0.5, 2.0, 7.0):
+        got = OX.swiglu_limit(g, u, l).double().numpy()
+        want = np.array([_swiglu_limit_math(float(gi), float(ui), l) for gi, ui in zip(g, u)])
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-7)
+
+
+def test_swiglu_limit_is_swiglu_where_no_clamp_binds():
+    gen = torch.Generator().manual_seed(12)
+    g, u = torch.randn(500, generator=gen), torch.randn(500, generator=gen)
+    swiglu = OX.gate_up_act(g, u, "silu")
+    assert torch.equal(OX.swiglu_limit(g, u, float("inf")), swiglu)
+    l = 1.0
+    inside = (g <= l) & (u.abs() <= l)
+    assert bool(inside.any()) and bool((~inside).any())
+    h = OX.swiglu_limit(g, u, l)
+    assert torch.equal(h[inside], swiglu[inside])
+    assert not torch.allclose(h[~inside], swiglu[~inside])
+
+
+def test_swiglu_limit_saturation_symmetry_and_bound():
+    gen = torch.Generator().manual_seed(13)
+    g, u = torch.randn(300, generator=gen) * 5, torch.randn(300, generator=gen) * 5
+    l = 1.5
+    h = OX.swiglu_limit(g, u, l)
+    # above the limit the gate saturates: any g > l gives the value at g = l
+    big = g > l
+    assert bool(big.any())
+    assert torch.equal(h[big], OX.swiglu_limit(torch.full_like(g[big], l), u[big], l))
+    # the gate is clamped above only: very negative gates still drive silu towards 0
+    assert abs(float(OX.swiglu_limit(torch.tensor([-30.0]), torch.tensor([1.0]), l))) < 1e-9
+    assert torch.equal(OX.swiglu_limit(g, -u, l), -h)  # odd in the up value
+    silu_l = l / (1.0 + math.exp(-l))
+    assert bool((h.abs() <= max(silu_l, 0.2785) * l + 1e-6).all())
+
+
+def test_swiglu_limit_layer_reduces_to_swiglu_layer():
+    """The whole expert call with a limit no value reaches equals the SwiGLU call bit for bit."""
+    x, ids, w, w13, w2 = setup(24, 2, 8, 0, 8, seed=10)
+    a = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16", activation="swiglu_limit", act_limit=1e30)
+    b = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16")
+    assert np.array_equal(a, b)
