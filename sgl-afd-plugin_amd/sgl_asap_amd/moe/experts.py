@@ -299,6 +299,10 @@ class AfdExperts(torch.nn.Module):
     rank: x bf16 [n, H], topk_output with ``topk_ids`` [n, k] (global ids) and
     ``topk_weights`` [n, k]; returns bf16 [n, H], the top-k-weighted sum over the local
     experts (rows with no local expert are 0). Enqueued on the current stream.
+
+    ``activation``, ``gemm1_alpha`` and ``gemm1_clamp_limit`` are FusedMoE's (see
+    ``moe_cfg``); ``swiglu_limit`` is DeepSeek-V4's FusedMoE argument, the clamp limit of
+    its SwiGLU (P/srt/models/deepseek_v4.py:63).
     """
 
     def __init__(
