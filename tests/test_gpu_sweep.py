@@ -1,0 +1,47 @@
+"""GPU: seeded random layer shapes against the oracle, across both weight formats and the
+three activations, with token counts at and around the 128-row tile edge (1, 2, 127, 128,
+129, ...), partial local expert ranges and top-k from 1 to 8. Same bars as test_gpu_moe."""
+
+import random
+
+import pytest
+
+from test_gpu_moe import assert_close, run_case
+
+pytestmark = pytest.mark.gpu
+
+CASES = 24
+
+
+def draw(case: int) -> dict:
+    rng = random.Random(7000 + case)
+    fmt = rng.choice(["mxfp4", "fp8_block"])
+    num_experts = rng.choice([8, 16, 32, 64])
+    num_local = rng.randint(1, min(num_experts, 24))
+    spec = dict(
+        fmt=fmt,
+        hidden=256 * rng.randint(1, 6),
+        inter=128 * rng.randint(1, 6),
+        num_experts=num_experts,
+        num_local=num_local,
+        e_lo=rng.randint(0, num_experts - num_local),
+        k=rng.randint(1, min(8, num_experts)),
+        n=rng.choice([1, 2, 31, 64, 127, 128, 129, 255, 300, 777]),
+        zipf=rng.choice([None, 1.2]) if fmt == "fp8_block" else None,
+    )
+    act = rng.choice(["silu", "situ", "limit"])
+    if act == "situ":
+        spec["situ"] = (rng.choice([0.5, 2.0]), rng.choice([0.25, 3.0]))
+    if act == "limit":
+        spec["swiglu_limit"] = rng.choice([0.3, 1.0])
+    return spec
+
+
+@pytest.mark.parametrize("case", range(CASES))
+def test_random_layer(case):
+    s = draw(case)
+    extra = {k: s[k] for k in ("situ", "swiglu_limit") if k in s}
+    experts, out, ref, parts, (x, ids, w) = run_case(
+        s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], s["fmt"],
+        9000 + case, zipf=s["zipf"], **extra)
+    assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
