@@ -89,14 +89,12 @@ __device__ __forceinline__ void quant_fp8_1x128_items(const uint16_t* __restrict
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
     if (!live) continue;
+    // hardware conversion (v_cvt_pk_fp8_f32): bit-identical to f32_to_e4m3 on the clamped range
     v4i out[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) packed |= f32_to_e4m3(clamp_e4m3(v[i * 4 + j] / sc)) << (8 * j);
-      out[i / 4][i % 4] = static_cast<int>(packed);
-    }
+    for (int i = 0; i < 8; ++i)
+      out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(v[i * 4] / sc, v[i * 4 + 1] / sc,
+                                                     v[i * 4 + 2] / sc, v[i * 4 + 3] / sc));
     v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cq * kMxBlock);
     dst[0] = out[0];
     dst[1] = out[1];
