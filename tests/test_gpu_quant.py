@@ -16,6 +16,32 @@ def _stream():
     return torch.cuda.current_stream().cuda_stream
 
 
+def _e4m3_ties():
+    """Every positive e4m3 midpoint (normal and subnormal), its bf16 neighbours and the
+    negatives: values that the quantizers see unchanged when the group's scale is 1."""
+    vals = np.array([float(F.e4m3_decode(np.array([c], dtype=np.uint8))[0]) for c in range(127)])
+    mids = (vals[:-1] + vals[1:]) / 2
+    bf = torch.tensor(mids, dtype=torch.float32).to(torch.bfloat16)
+    up = (bf.view(torch.int16) + 1).view(torch.bfloat16)
+    down = (bf.view(torch.int16) - 1).view(torch.bfloat16)
+    pos = torch.cat([bf, up, down]).float()
+    return torch.cat([pos, -pos])
+
+
+def _tie_row(cols, group, amax):
+    """A row whose every `group` elements start with `amax` (scale exactly 1: 448 for FP8
+    1x128, 256 for MXFP8) followed by e4m3 ties."""
+    ties = _e4m3_ties()
+    row = torch.empty(cols)
+    k = 0
+    for g0 in range(0, cols, group):
+        row[g0] = amax
+        for c in range(g0 + 1, g0 + group):
+            row[c] = ties[k % len(ties)]
+            k += 1
+    return row
+
+
 def _bf16_input(rows, cols, seed):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(rows, cols, generator=g) * torch.logspace(-3, 3, cols)[None, :]
@@ -23,6 +49,9 @@ def _bf16_input(rows, cols, seed):
         x[0, :] = 0.0  # an all-zero row: scale code 0
         x[1, :32] = 1e-30  # a tiny block
         x[2, :64] = torch.tensor([0.25, -0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 448.0] * 8)
+    if rows >= 5 and cols >= 128:
+        x[3] = _tie_row(cols, 128, 448.0)  # FP8 1x128 groups with scale 1: RNE ties
+        x[4] = _tie_row(cols, 32, 256.0)  # MXFP8 blocks with scale 2^0
     return x.to(torch.bfloat16)
 
 
