@@ -148,7 +148,7 @@ def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
     from oracle import formats as F
     from sgl_asap_amd import workloads as W
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = len(os.sched_getaffinity(0))  # every host core this process may run on
     torch.set_num_threads(threads)
     gen = W.generator("cpu", 1)
     x, ids, w = W.job(shape, n=sample_tokens, seed=0, device="cpu")

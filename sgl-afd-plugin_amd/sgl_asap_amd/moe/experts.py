@@ -458,6 +458,10 @@ class AfdExperts(torch.nn.Module):
         )
         return out
 
+    def layout_for(self, n: int) -> dict:
+        """Offsets of the workspace buffers of a call with ``n`` tokens (afd_workspace_layout)."""
+        return workspace_layout(self.cfg, n)
+
     def ws_view(self, name: str, dtype: torch.dtype, count: int, n: int, stream=None) -> torch.Tensor:
         """A view of an intermediate buffer of the last call with ``n`` tokens (the
         workspace layout depends on n); for parity tests and profiling."""

@@ -205,6 +205,15 @@ class AttnChannel:
     def seg_ptr(self, f: int, slot: int) -> int:
         return self.segments.data_ptr() + self.g.seg_off(f, slot) - self.g.flags_bytes
 
+    def result_view(self, f: int, slot: int, n_tokens: int):
+        """F rank f's partial sum for ``slot`` as it lies in this rank's result segment:
+        bf16 [n_tokens, hidden] (valid after the wait for the reply, until the next reply)."""
+        import torch
+
+        off = self.g.seg_off(f, slot) - self.g.flags_bytes
+        seg = self.segments[off : off + n_tokens * self.g.hidden * 2]
+        return seg.view(torch.bfloat16).view(n_tokens, self.g.hidden)
+
     def send(self, layer_id: int, slot: int, x_ptr: int, ids_ptr: int, w_ptr: int, n_tokens: int, stream,
              xs_ptr: int = 0) -> Ticket:
         """Enqueue one message on ``stream`` (a torch stream): ``n_tokens`` rows of x (bf16

@@ -1,0 +1,153 @@
+"""GPU: the skewed job stream's workload. DeepSeek-V4-Flash F-rank shape (hidden 4096,
+moe_intermediate 2048, 64 of 256 experts local, top-8), MXFP4 weights, Zipf(1.2) expert
+popularity, jobs of 256, 1000, 4097 and 16384 tokens from the stream's generator (each job
+draws its own popularity order, as the stream does), through the HIP-graph buckets of the FFN
+rank (powers of two up to 16384) and eagerly.
+
+Per job:
+* the router's tables (counts, offsets, padded offsets, sorted pairs, pair positions) equal
+  the oracle's stable routing bit for bit, at full size;
+* the graph replay (the bucket above the job: 256, 1024, 8192, 16384) equals the eager call
+  bit for bit, and so does a second replay from the other output buffer;
+* the tokens whose local experts all lie among the job's 4 most used local experts (the most
+  used one, which spans the most row tiles, included; tokens spread over the whole job) are
+  within rel-L2 1e-2 of the oracle's expert call, and tokens without a local expert are 0.
+Finally one pass of the four jobs through the one-GPU transport (2 replicas x 2 slots,
+graphs) returns the eager results bit for bit."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits16, dev, rel_l2, say
+from oracle import experts as OX
+from oracle import formats as F
+from oracle import routing as R
+from sgl_asap_amd import workloads as W
+from sgl_asap_amd.loop import OneGpuAfd
+from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts
+from sgl_asap_amd.moe.topk import StandardTopKOutput
+from sgl_asap_amd.runner.graph_runner import FfnGraphRunner
+
+pytestmark = pytest.mark.gpu
+
+SHAPE = W.SHAPES["dsv4_zipf"]
+N_MAX = 16384
+SIZES = (256, 1000, 4097, 16384)
+
+
+@pytest.fixture(scope="module")
+def stream_layer():
+    say("C3 stream workload: packing 64 MXFP4 experts (hidden 4096, inter 2048)")
+    gen = W.generator(dev(), 11)
+    w13, w2 = W.expert_weights(SHAPE.num_local, SHAPE.hidden, SHAPE.inter, gen, dev())
+    experts = {0: AfdExperts(SHAPE.num_experts, SHAPE.top_k, 0, SHAPE.local, pack_mxfp4_experts(w13, w2),
+                             n_max=N_MAX)}
+    w13, w2 = w13.cpu(), w2.cpu()
+    jobs = []
+    for j, n in enumerate(SIZES):
+        x, ids, w = W.job(SHAPE, n=n, seed=300 + j, device="cpu")
+        jobs.append((x, ids.to(torch.int32), w.to(torch.float32)))
+    torch.cuda.synchronize()
+    yield experts, (w13, w2), jobs
+    del experts
+    torch.cuda.empty_cache()
+
+
+def router_tables(layer, n):
+    L = layer.layout_for(n)
+    nl = SHAPE.num_local
+
+    def i32(name, count):
+        return layer.ws_view(name, torch.int32, count, n).cpu().numpy()
+
+    poff = i32("padded_offsets", nl + 1)
+    return {
+        "counts": i32("counts", nl),
+        "offsets": i32("offsets", nl + 1),
+        "padded_offsets": poff,
+        "sorted_pairs": i32("sorted_pairs", int(poff[-1])),
+        "pair_pos": i32("pair_pos", n * SHAPE.top_k),
+    }, L["block_m"]
+
+
+def oracle_subset(w13, w2, x, ids, w, got, keep=4, limit=320):
+    lo, nl = SHAPE.local.start, SHAPE.num_local
+    rel = ids.numpy().astype(np.int64) - lo
+    local = (rel >= 0) & (rel < nl)
+    counts = np.bincount(rel[local], minlength=nl)
+    chosen = np.argsort(-counts, kind="stable")[:keep]
+    table = np.full(nl, -1, dtype=np.int64)
+    table[chosen] = np.arange(keep)
+    relc = np.where(local, rel, 0)
+    inside = ~(local & (table[relc] < 0)).any(axis=1)
+    has = local.any(axis=1)
+    cand = np.nonzero(inside & has)[0]
+    assert len(cand) >= min(64, len(ids) // 8), len(cand)
+    pick = cand[np.linspace(0, len(cand) - 1, min(limit, len(cand))).astype(np.int64)]
+    none = np.nonzero(~has)[0][:32]
+    sub = np.concatenate([pick, none])
+    sel = torch.from_numpy(chosen)
+    c13, s13 = F.mx_quantize(w13[sel].numpy(), "e2m1")
+    c2, s2 = F.mx_quantize(w2[sel].numpy(), "e2m1")
+    sub_ids = np.where(local[sub], table[relc[sub]], -1).astype(np.int32)
+    ref = OX.moe_ffn(x[torch.from_numpy(sub)], sub_ids, w.numpy()[sub], F.mx_dequantize(c13, s13, "e2m1"),
+                     F.mx_dequantize(c2, s2, "e2m1"), 0, act="mxfp8")
+    err = rel_l2(F.bf16_to_f32(got[pick]), F.bf16_to_f32(ref[: len(pick)]))
+    say(f"  {len(pick)} tokens of experts {chosen.tolist()} (pairs {counts[chosen].tolist()}, head spans "
+        f"{(counts[chosen[0]] + 127) // 128} row tiles), rel_l2 = {err:.2e}")
+    assert err <= 1e-2
+    assert not got[none].any()
+
+
+def test_stream_jobs_graphs_eager_routing_and_oracle(stream_layer):
+    experts, (w13, w2), jobs = stream_layer
+    layer = experts[0]
+    say(f"C3: capturing graph buckets up to {N_MAX}")
+    runner = FfnGraphRunner(experts, N_MAX, SHAPE.local)
+    assert runner.buckets == [1 << i for i in range(14)] + [N_MAX]
+    for (x, ids, w), n in zip(jobs, SIZES):
+        say(f"C3 job of {n} tokens")
+        xd, idsd, wd = x.to(dev()), ids.to(dev()), w.to(dev())
+        eager = bits16(layer(xd, StandardTopKOutput(wd, idsd)))
+        torch.cuda.synchronize()
+        tables, block_m = router_tables(layer, n)
+        ref = R.route(ids.numpy(), SHAPE.local.start, SHAPE.num_local, block_m)
+        for key, val in tables.items():
+            assert np.array_equal(val, ref[key]), (n, key)
+        for buffer in (0, 1):
+            out = runner.run(0, xd, idsd, wd, buffer)
+            torch.cuda.synchronize()
+            assert out is not None and out.shape == (n, SHAPE.hidden)
+            assert np.array_equal(bits16(out), eager), (n, buffer)
+        oracle_subset(w13, w2, x, ids, w, eager)
+
+
+def test_stream_through_the_transport(stream_layer):
+    experts, _, jobs = stream_layer
+    say("C3: the four jobs through the one-GPU transport, 2 replicas x 2 slots, graphs")
+    eager = []
+    for x, ids, w in jobs:
+        eager.append(bits16(experts[0](x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))))
+    torch.cuda.synchronize()
+    order = [(r, mb) for r in range(2) for mb in range(2)]
+    with OneGpuAfd(experts, n_max=N_MAX, slots=2, replicas=2, graph_max_tokens=N_MAX) as afd:
+        main = torch.cuda.current_stream()
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        dev_jobs = [(x.to(dev()), ids.to(dev()), w.to(dev())) for x, ids, w in jobs]
+        for s in sends:
+            s.wait_stream(main)
+        tickets = []
+        for (r, mb), (x, ids, w) in zip(order, dev_jobs):
+            tickets.append((r, afd.channels[r].send(0, mb, x.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                                                    x.shape[0], sends[r])))
+        afd.scheduler.serve_pending()
+        results = []
+        for r, t in tickets:
+            ptrs = afd.channels[r].wait(t, main)
+            results.append(afd.channels[r].result_view(0, t.slot, t.n_tokens))
+        torch.cuda.synchronize()
+        got = [bits16(v) for v in results]
+        assert afd.server.stats["jobs"] == 4
+    for g, e, n in zip(got, eager, SIZES):
+        assert np.array_equal(g, e), n

@@ -233,3 +233,50 @@ def test_swiglu_limit_layer_reduces_to_swiglu_layer():
     a = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16", activation="swiglu_limit", act_limit=1e30)
     b = OX.moe_ffn(x, ids, w, w13, w2, 0, act="bf16")
     assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------- shared expert
+def _shared_float64(x, wg, wu, wd):
+    """The dense SwiGLU shared expert in float64 numpy, element formulas written out:
+    h_j = g_j / (1 + exp(-g_j)) * u_j with g = Wg x, u = Wu x; out = Wd h."""
+    xf = x.double().numpy()
+    g = np.einsum("ih,th->ti", wg.double().numpy(), xf)
+    u = np.einsum("ih,th->ti", wu.double().numpy(), xf)
+    h = g / (1.0 + np.exp(-g)) * u
+    return np.einsum("hi,ti->th", wd.double().numpy(), h)
+
+
+def _shared_case(n=24, hidden=H, inter=96, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, hidden, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(inter, hidden, generator=g) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(inter, hidden, generator=g) * 0.05).to(torch.bfloat16)
+    wd = (torch.randn(hidden, inter, generator=g) * 0.05).to(torch.bfloat16)
+    return x, wg, wu, wd
+
+
+def test_shared_mlp_matches_float64_dense_swiglu():
+    """bf16(fp32 evaluation) against bf16(float64 evaluation): equal bits except where the
+    float64 value sits within fp32 noise of a bf16 rounding boundary, never more than one
+    bf16 step apart. inter != hidden, so a transposed operand cannot pass."""
+    x, wg, wu, wd = _shared_case()
+    got = bits(OX.shared_mlp(x, wg, wu, wd)).astype(np.int32)
+    want = bits(torch.from_numpy(_shared_float64(x, wg, wu, wd)).float().to(torch.bfloat16)).astype(np.int32)
+    assert np.mean(got == want) > 0.99
+    assert np.abs(got - want).max() <= 1
+
+
+def test_shared_mlp_sensitivity_and_zeros():
+    x, wg, wu, wd = _shared_case(seed=4)
+    ref = bits(OX.shared_mlp(x, wg, wu, wd))
+    assert np.mean(bits(OX.shared_mlp(x, wu, wg, wd)) == ref) < 0.1  # gate and up swapped
+    assert not bits(OX.shared_mlp(x, wg, torch.zeros_like(wu), wd)).any()  # up = 0 -> exact zeros
+    assert not bits(OX.shared_mlp(torch.zeros_like(x), wg, wu, wd)).any()  # silu(0) * 0 = 0
+    # one token, one hidden unit: out = wd[:, 0] * silu(g) * u in closed form
+    x1 = x[:1]
+    wg1, wu1, wd1 = wg[:1], wu[:1], wd[:, :1]
+    g1 = float((wg1.double() @ x1.double().T).item())
+    u1 = float((wu1.double() @ x1.double().T).item())
+    want = wd1.double()[:, 0] * (g1 / (1 + math.exp(-g1)) * u1)
+    got = OX.shared_mlp(x1, wg1, wu1, wd1)[0].double()
+    assert torch.allclose(got, want, rtol=8e-3, atol=1e-6)
