@@ -296,7 +296,7 @@ def bench_stream(args) -> dict:
 
         run()
         torch.cuda.synchronize()
-        afd.scheduler.job_timer = type(afd.scheduler.job_timer)()  # time the measured pass only
+        afd.scheduler.clock = type(afd.scheduler.clock)()  # time the measured pass only
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         h0 = time.perf_counter()
         e0.record(main)
@@ -311,8 +311,8 @@ def bench_stream(args) -> dict:
             "tokens_per_s": round(tokens / (ms * 1e-3), 1),
             "host_enqueue_ms": round(host_ms, 3),
             "setup_s": round(setup_s, 2),
-            "jobs_per_bucket": {str(b): v["jobs"] for b, v in afd.scheduler.job_timer.summary().items()},
-            "job_timer": afd.scheduler.job_timer.summary(),
+            "jobs_per_bucket": {str(b): v["jobs"] for b, v in afd.scheduler.clock.summary().items()},
+            "job_clock": afd.scheduler.clock.summary(),
         }
         afd.close()
         del experts, afd
@@ -336,6 +336,7 @@ def bench_loop(args) -> dict:
     from sgl_asap_amd import workloads as W
     from sgl_asap_amd.loop import OneGpuAfd
     from sgl_asap_amd.moe.layer import AsapMoE
+    from sgl_asap_amd.moe.shared import SharedExpertMLP
     from sgl_asap_amd.moe.topk import StandardTopKOutput
 
     shape = W.SHAPES["dsv4_zipf"]
@@ -343,13 +344,7 @@ def bench_loop(args) -> dict:
     torch.cuda.set_device(dev)
     n, shared_i = 8192, 1536
     experts = {0: _mxfp4_layer(W, shape, dev, n)}
-    g = W.generator(dev, 2)
-    w_gu = (torch.randn(2 * shared_i, shape.hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-    w_d = (torch.randn(shape.hidden, shared_i, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-
-    def shared(x):
-        gate, up = (x @ w_gu.T).split(shared_i, dim=1)
-        return (torch.nn.functional.silu(gate) * up) @ w_d.T
+    shared = SharedExpertMLP.random(shape.hidden, shared_i, W.generator(dev, 2), dev)
 
     mbs = []
     for m in range(2):

@@ -32,6 +32,13 @@
  *   afd_repack_mxfp4 / ......... the checkpoint expert load (P/srt/model_loader/weight_utils.py
  *   _fp8_block                   :27-54 selects the tensors, SGLang's FusedMoE weight_loader
  *                                stores them; MXFP4 layout of P/srt/configs/model_config.py:3-7)
+ *   afd_send ................... AttnChannel.send (P/transport/channel.py:317-362): the
+ *                                backpressure waits, the payload copies to every F rank's
+ *                                RecvArena region and the doorbells, as one call
+ *   afd_reply .................. FfnServer.reply (P/transport/server.py:340-350): the
+ *                                partial-sum copies and the done flags of a job, as one call
+ *   afd_wait_replies ........... the reply waits of AttnChannel.wait (P/transport/channel.py
+ *                                :364-377)
  *   afd_copy_async ............. cu.memcpy_async (P/transport/cuda_wrapper.py, used at
  *                                P/transport/channel.py:345-349, P/transport/server.py:347)
  *   afd_stream_write64 ......... cu.write64 / write32 (cuda_wrapper.py:258-270; doorbell at
@@ -260,7 +267,57 @@ int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w, int
 int afd_combine(const uint16_t* const* parts, int32_t num_parts, const uint16_t* shared,
                 uint16_t* out, int64_t numel, afd_stream_t stream);
 
-/* ---- transport primitives (one GPU: producer and consumer streams) -------------------- */
+/* ---- transport (one GPU: producer and consumer streams) ---------------------------------
+ * Done flags are 64-bit message counters that only grow (a message's counter is the count of
+ * messages sent on its slot, starting from the channel's base): afd_send's backpressure and
+ * afd_wait_replies wait for counter >= value, so a later count, or a watchdog's release,
+ * satisfies every earlier wait. Doorbell words carry the low 32 bits of the count in their
+ * sequence field (the reference's bit layout, P/transport/layout.py:50-53). */
+#define AFD_MAX_F 16
+
+/* One message of an attention rank to every F rank (replaces AttnChannel.send,
+ * P/transport/channel.py:317-362). On `stream`, in this order:
+ *   1. for every F rank f with done[f] != NULL: wait until *done[f] >= done_min;
+ *   2. one copy launch: x (x_bytes), xs (xs_bytes, fp8 activations on the wire; NULL / 0 for
+ *      bf16), ids and w (ids_bytes each) to region[f] + 0 / xs_off / ids_off / w_off for every f;
+ *   3. for every f: the 64-bit store word[f] -> *bell[f].
+ * Fields must not overlap inside a region; bell and done addresses 8-byte aligned. */
+typedef struct afd_send_desc {
+  int32_t num_f; /* 1..AFD_MAX_F */
+  int32_t reserved;
+  const void* x;
+  uint64_t x_bytes;
+  const void* xs;
+  uint64_t xs_bytes;
+  const void* ids;
+  const void* w;
+  uint64_t ids_bytes;
+  uint64_t xs_off, ids_off, w_off;
+  uint64_t done_min;
+  void* region[AFD_MAX_F];
+  uint64_t* bell[AFD_MAX_F];
+  uint64_t word[AFD_MAX_F];
+  uint64_t* done[AFD_MAX_F];
+} afd_send_desc;
+int afd_send(const afd_send_desc* msg, afd_stream_t stream);
+
+/* One F-rank answer per row of a job (replaces FfnServer.reply, P/transport/server.py
+ * :340-350): one copy launch of every row's partial sum (src -> dst, bytes; none when
+ * src == dst or bytes == 0), then the 64-bit store value -> *done per row. 1..64 rows. */
+typedef struct afd_reply_desc {
+  const void* src;
+  void* dst;
+  uint64_t bytes;
+  uint64_t* done;
+  uint64_t value;
+} afd_reply_desc;
+int afd_reply(const afd_reply_desc* rows, int32_t num_rows, afd_stream_t stream);
+
+/* Park `stream` until *done[f] >= seq for f < num_f (the reply waits of AttnChannel.wait,
+ * P/transport/channel.py:364-377). */
+int afd_wait_replies(uint64_t* const* done, int32_t num_f, uint64_t seq, afd_stream_t stream);
+
+/* ---- transport primitives ---------------------------------------------------------------- */
 int afd_host_alloc(void** ptr, uint64_t bytes); /* pinned, coherent, zero-filled */
 int afd_host_free(void* ptr);
 int afd_copy_async(void* dst, const void* src, uint64_t bytes, afd_stream_t stream);

@@ -57,7 +57,12 @@ EXPORTED = (
     "afd_copy_async",
     "afd_stream_write64",
     "afd_stream_wait64",
+    "afd_send",
+    "afd_reply",
+    "afd_wait_replies",
 )
+
+AFD_MAX_F = 16
 
 
 class HIPError(RuntimeError):
@@ -127,6 +132,42 @@ class AfdWsLayout(ctypes.Structure):
     ]
 
 
+class AfdSendDesc(ctypes.Structure):
+    """afd_send_desc: one message to every F rank (afd_send)."""
+
+    _fields_ = [
+        ("num_f", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_bytes", ctypes.c_uint64),
+        ("xs", ctypes.c_void_p),
+        ("xs_bytes", ctypes.c_uint64),
+        ("ids", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("ids_bytes", ctypes.c_uint64),
+        ("xs_off", ctypes.c_uint64),
+        ("ids_off", ctypes.c_uint64),
+        ("w_off", ctypes.c_uint64),
+        ("done_min", ctypes.c_uint64),
+        ("region", ctypes.c_void_p * AFD_MAX_F),
+        ("bell", ctypes.c_void_p * AFD_MAX_F),
+        ("word", ctypes.c_uint64 * AFD_MAX_F),
+        ("done", ctypes.c_void_p * AFD_MAX_F),
+    ]
+
+
+class AfdReplyDesc(ctypes.Structure):
+    """afd_reply_desc: one row's answer (afd_reply)."""
+
+    _fields_ = [
+        ("src", ctypes.c_void_p),
+        ("dst", ctypes.c_void_p),
+        ("bytes", ctypes.c_uint64),
+        ("done", ctypes.c_void_p),
+        ("value", ctypes.c_uint64),
+    ]
+
+
 _P = ctypes.c_void_p
 _I32, _I64, _U64 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64
 _SIGS = {
@@ -164,6 +205,9 @@ _SIGS = {
     "afd_copy_async": ([_P, _P, _U64, _P], _I32),
     "afd_stream_write64": ([_P, _P, _U64], _I32),
     "afd_stream_wait64": ([_P, _P, _U64, _U64, _I32], _I32),
+    "afd_send": ([ctypes.POINTER(AfdSendDesc), _P], _I32),
+    "afd_reply": ([ctypes.POINTER(AfdReplyDesc), _I32, _P], _I32),
+    "afd_wait_replies": ([ctypes.POINTER(ctypes.c_void_p), _I32, _U64, _P], _I32),
 }
 
 _lib = None

@@ -9,8 +9,9 @@ Wires the pieces the reference runs in separate processes (``AsapBuffer.connect`
     [shared experts on the compute stream]
     AsapDispatcher.combine -> AsapBuffer.recv
         pump: FfnServer.poll -> FfnScheduler.run_job                (F stream)
-            waits on the doorbell, runs the experts into A's result segment, rings done
-        AttnChannel.wait (compute stream) -> afd_combine (+ shared)
+            gates on the doorbell, runs the experts into A's result segment, stores the
+            message's count into A's done counter (afd_reply)
+        AttnChannel.wait (compute stream: done counter >= count) -> afd_combine (+ shared)
 
 Every wait is enqueued after the work that satisfies it (host order equals causal order),
 so the loop cannot deadlock even when streams share a hardware queue.
@@ -38,7 +39,7 @@ class OneGpuAfd:
 
     def __init__(self, experts: Dict[int, torch.nn.Module], *, n_max: int, slots: int = 2,
                  replicas: int = 1, group: int = 1, seq_base: int = 0, graph_max_tokens: int = 0,
-                 timeout_s: float = 60.0, device: int = 0, reply_stream: bool = True, act: str = "bf16",
+                 timeout_s: float = 60.0, device: int = 0, act: str = "bf16",
                  timing: bool = False, _backpressure: bool = True,
                  _epoch_override: Optional[int] = None):
         first = next(iter(experts.values()))
@@ -50,8 +51,7 @@ class OneGpuAfd:
         if act != "bf16" and reads != {act}:
             raise ValueError(f"activations on the wire as {act}, but the experts read {sorted(reads)}")
         self.server = FfnServer(0, self.geometry, device=device, seq_base=seq_base).start()
-        self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens,
-                                      reply_stream=reply_stream, timing=timing)
+        self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens, timing=timing)
         self.channels = [
             AttnChannel(a, self.geometry, [self.server], device=device, seq_base=seq_base,
                         timeout_s=timeout_s, _backpressure=_backpressure,

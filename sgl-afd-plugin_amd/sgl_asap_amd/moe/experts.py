@@ -348,7 +348,7 @@ class AfdExperts(torch.nn.Module):
             self._ws[s.cuda_stream] = ws
         return ws
 
-    def _topk(self, n: int, topk_output):
+    def _topk(self, n: int, topk_output, device):
         if not format_is_standard(topk_output):
             raise RuntimeError(f"expected explicit top-k ids and weights, got {type(topk_output).__name__}")
         if n > self.n_max:
@@ -357,17 +357,32 @@ class AfdExperts(torch.nn.Module):
         w = topk_output.topk_weights
         if ids.shape != (n, self.top_k) or w.shape != (n, self.top_k):
             raise ValueError(f"top-k shapes {tuple(ids.shape)} / {tuple(w.shape)} for {n} tokens, k={self.top_k}")
+        if ids.device != device or w.device != device:
+            raise ValueError(f"top-k ids / weights on {ids.device} / {w.device}, activations on {device}")
         return ids.to(torch.int32).contiguous(), w.to(torch.float32).contiguous()
+
+    def _out(self, out: Optional[torch.Tensor], n: int, device) -> torch.Tensor:
+        """The caller's output tensor after checking it, or a new one: the kernels write
+        n * hidden bf16 values through its data pointer."""
+        if out is None:
+            return torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=device)
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (n, self.hidden_size):
+            raise ValueError(f"out must be bf16 [{n}, {self.hidden_size}], got {out.dtype} {tuple(out.shape)}")
+        if not out.is_contiguous() or out.device != torch.device(device):
+            raise ValueError(f"out must be contiguous on {device}, got {out.device} "
+                             f"{'contiguous' if out.is_contiguous() else 'strided'}")
+        return out
 
     def forward(self, hidden_states: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):
         x = hidden_states
         if x.dtype != torch.bfloat16:
             raise TypeError(f"the expert path takes bf16 activations, got {x.dtype}")
+        if x.dim() != 2 or x.shape[1] != self.hidden_size or not x.is_cuda:
+            raise ValueError(f"x must be a device tensor [n, {self.hidden_size}], got {tuple(x.shape)} on {x.device}")
         n = x.shape[0]
-        ids, w = self._topk(n, topk_output)
+        ids, w = self._topk(n, topk_output, x.device)
         x = x.contiguous()
-        if out is None:
-            out = torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=x.device)
+        out = self._out(out, n, x.device)
         if n == 0:
             return out
         ws = self.workspace()
@@ -436,9 +451,10 @@ class AfdExperts(torch.nn.Module):
             raise ValueError(f"xq must be uint8 [{n}, {self.hidden_size}], got {xq.dtype} {tuple(xq.shape)}")
         if xs.dtype != dtype or tuple(xs.shape) != shape:
             raise ValueError(f"xs must be {dtype} {shape}, got {xs.dtype} {tuple(xs.shape)}")
-        ids, w = self._topk(n, topk_output)
-        if out is None:
-            out = torch.empty(n, self.hidden_size, dtype=torch.bfloat16, device=xq.device)
+        if not xq.is_cuda or xs.device != xq.device:
+            raise ValueError(f"xq / xs must be device tensors on one device, got {xq.device} / {xs.device}")
+        ids, w = self._topk(n, topk_output, xq.device)
+        out = self._out(out, n, xq.device)
         if n == 0:
             return out
         ws = self.workspace()

@@ -1,27 +1,30 @@
 """The F rank's job handler: routed experts per MoE layer, served job by job.
 
-Follows ``FfnScheduler`` in ``python/sgl_asap_plugin/srt/managers/scheduler.py``:
-``local_experts`` (:206-218), ``warmup`` over every power of two up to n_max with the seeded
-generator (:329-351), ``run_job`` (:387-436: row views of the RecvArena, the graph runner or
-the eager expert call, a reply stream that waits for the experts, ``reply`` per row, the two
-graph output buffers reused in turn behind ``reply_free`` events), ``rows_of`` (:438-450) and
-``JobTimer`` (:109-159: host launch time and GPU expert / reply times per power-of-two
-bucket, from events read lazily).
+Plays the part of ``FfnScheduler`` in ``python/sgl_asap_plugin/srt/managers/scheduler.py``:
+``local_experts`` (:206-218), ``warmup`` (:329-351), ``run_job`` (:387-436), ``rows_of``
+(:438-450) and the per-job timing of its ``JobTimer`` (:109-159).
 
-Differences on one GPU: the experts run on the scheduler's own stream, which first parks
-on the job's doorbells (``FfnServer.wait_rows``), so the host never waits; an eager job
-writes its output straight into A's result segment, so its reply is the done flag alone.
-With fp8 activations on the wire (``Geometry.act``) the rows arrive as e4m3 codes plus
-scales and the job runs the expert call on them as they are (``forward_q``).
+Design on one GPU: everything a job does is stream-ordered on one F stream, enqueued by
+``run_job`` without any host wait:
+
+    gate on the rows' doorbells -> expert call (a HIP-graph replay, or eager above the largest
+    bucket) -> afd_reply (copies if any, then the done counters)
+
+A job of one row (the normal case, one attention rank per replica) writes its output straight
+into that rank's result segment, so its reply is only the done counter. A job of several rows
+(a group of A ranks per replica) computes into a buffer that the reply copies from on the
+same stream, so one output buffer is enough and its memory is never handed out while a copy
+still reads it. With fp8 activations on the wire (``Geometry.act``) the rows arrive as e4m3
+codes plus scales and the expert call runs on them as they are.
 """
 
 from __future__ import annotations
 
 import collections
-import statistics
 import time
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
+import numpy as np
 import torch
 
 from ..moe.experts import act_scale_shape
@@ -30,53 +33,67 @@ from .graph_runner import FfnGraphRunner, graph_buckets
 
 
 def local_experts(ep_rank: int, ep_size: int, num_experts: int) -> range:
-    """The routed experts of this EP rank: num_experts // ep_size contiguous global ids."""
-    per_rank = num_experts // ep_size
-    return range(ep_rank * per_rank, (ep_rank + 1) * per_rank)
+    """The routed experts of EP rank ``ep_rank``: a contiguous block of num_experts // ep_size
+    global ids."""
+    width = num_experts // ep_size
+    return range(ep_rank * width, ep_rank * width + width)
 
 
-class JobTimer:
-    """Per power-of-two bucket: host launch time, GPU time of the experts (split into jobs
-    that found the GPU idle, "alone", and jobs queued behind another, "queued") and of the
-    replies. CUDA-style events, read once completed, so timing adds no synchronization."""
+class JobClock:
+    """GPU and host time of every served job, grouped by the job's power-of-two size class.
+
+    ``start`` / ``stop`` bracket a job's GPU work with two timing events on the F stream and
+    note the host time spent enqueueing it; whether the F stream was idle when the job was
+    enqueued is recorded too (the previous job's end event had completed), since a job queued
+    behind another starts late. Records are resolved lazily: ``collect`` reads only those
+    whose end event the GPU has passed, so timing never synchronizes the serving loop."""
 
     def __init__(self, keep: int = 4096):
         self.keep = keep
-        self.pending = collections.deque()
-        self.samples = collections.defaultdict(lambda: collections.defaultdict(list))
+        self._open: collections.deque = collections.deque()
+        self._rows: Dict[int, List[tuple]] = collections.defaultdict(list)
+        self._last_end: Optional[torch.cuda.Event] = None
 
-    def event(self, stream=None) -> torch.cuda.Event:
-        e = torch.cuda.Event(enable_timing=True)
-        e.record(stream)
-        return e
+    @staticmethod
+    def size_class(n_tokens: int) -> int:
+        return 1 << max(0, n_tokens - 1).bit_length()
 
-    def start(self, stream=None) -> tuple:
-        alone = not self.pending or self.pending[-1][4].query()
-        return alone, self.event(stream)
+    def start(self, stream) -> tuple:
+        idle = self._last_end is None or self._last_end.query()
+        begin = torch.cuda.Event(enable_timing=True)
+        begin.record(stream)
+        return time.perf_counter(), idle, begin
 
-    def add(self, n_tokens: int, started: tuple, experts, replied, host_s: float) -> None:
-        bucket = 1 << (n_tokens - 1).bit_length()
-        self.pending.append((bucket, *started, experts, replied, host_s))
-        self.drain()
+    def stop(self, token: tuple, n_tokens: int, stream) -> None:
+        t0, idle, begin = token
+        end = torch.cuda.Event(enable_timing=True)
+        end.record(stream)
+        self._last_end = end
+        self._open.append((self.size_class(n_tokens), idle, begin, end, time.perf_counter() - t0))
+        self.collect()
 
-    def drain(self) -> None:
-        while self.pending and self.pending[0][4].query():
-            bucket, alone, start, experts, replied, host_s = self.pending.popleft()
-            rows = self.samples[bucket]
-            if len(rows["host_us"]) < self.keep:
-                rows["host_us"].append(host_s * 1e6)
-                rows["reply_ms"].append(experts.elapsed_time(replied))
-                rows[f"experts_ms_{'alone' if alone else 'queued'}"].append(start.elapsed_time(experts))
+    def collect(self) -> None:
+        while self._open and self._open[0][3].query():
+            size, idle, begin, end, host_s = self._open.popleft()
+            rows = self._rows[size]
+            if len(rows) < self.keep:
+                rows.append((begin.elapsed_time(end), host_s * 1e6, idle))
 
     def summary(self) -> dict:
+        """Per size class: job count, median / p90 GPU ms (split by whether the stream was
+        idle at enqueue) and median host enqueue µs. Synchronizes the device first."""
         torch.cuda.synchronize()
-        self.drain()
+        self.collect()
         out = {}
-        for bucket, rows in sorted(self.samples.items()):
-            out[bucket] = {"jobs": len(rows["host_us"])}
-            for name, values in sorted(rows.items()):
-                out[bucket][f"{name}_p50"] = round(statistics.median(values), 4)
-                out[bucket][f"{name}_n"] = len(values)
+        for size in sorted(self._rows):
+            gpu, host, idle = (np.asarray(c) for c in zip(*self._rows[size]))
+            entry = {"jobs": int(gpu.size), "host_us_p50": round(float(np.median(host)), 2)}
+            for name, sel in (("idle", idle), ("queued", ~idle)):
+                if sel.any():
+                    entry[f"gpu_ms_{name}_p50"] = round(float(np.median(gpu[sel])), 4)
+                    entry[f"gpu_ms_{name}_p90"] = round(float(np.percentile(gpu[sel], 90)), 4)
+                    entry[f"gpu_ms_{name}_n"] = int(sel.sum())
+            out[size] = entry
         return out
 
 
@@ -84,18 +101,13 @@ class FfnScheduler:
     """Serves the jobs an ``FfnServer`` discovers with the routed experts of every layer."""
 
     def __init__(self, server, experts: Dict[int, torch.nn.Module], *, graph_max_tokens: int = 0,
-                 reply_stream: bool = True, timing: bool = False):
+                 timing: bool = False):
         self.server, self.g = server, server.g
         self.experts = experts
-        first = next(iter(experts.values()))
-        self.local = first.local
+        self.local = next(iter(experts.values())).local
         self.stream = torch.cuda.Stream()
-        self.reply_stream = torch.cuda.Stream() if reply_stream else None
-        self.reply_ready = torch.cuda.Event()
-        self.reply_free = [torch.cuda.Event(), torch.cuda.Event()]
-        self.reply_turn = 0
         self.layer_calls: collections.Counter = collections.Counter()
-        self.job_timer = JobTimer() if timing else None
+        self.clock = JobClock() if timing else None
         self.graph_runner: Optional[FfnGraphRunner] = None
         if graph_max_tokens:
             with torch.cuda.stream(self.stream):
@@ -103,93 +115,78 @@ class FfnScheduler:
 
     @torch.no_grad()
     def warmup(self, n_max: int) -> list:
-        """Run every power-of-two token count up to n_max once (layer 0; every layer up to 256
-        tokens), so every kernel and workspace is ready before serving."""
-        layers = sorted(self.experts)
-        first = self.experts[layers[0]]
-        device = torch.cuda.current_device()
-        buckets = graph_buckets(n_max)
+        """Run the expert call once at every graph-bucket size up to ``n_max`` on seeded
+        inputs (the prefixes of one batch: x ~ N(0,1) bf16, k distinct experts per token drawn
+        uniformly over all experts, weights ~ U(0,1)), on the first layer at every size and on
+        every other layer at the smallest size, so every kernel and every workspace has been
+        used before serving. Synchronizes; returns the sizes run."""
+        order = sorted(self.experts)
+        first = self.experts[order[0]]
+        sizes = graph_buckets(n_max)
+        device = torch.device("cuda", torch.cuda.current_device())
         gen = torch.Generator(device=device).manual_seed(0)
+        n = sizes[-1]
+        x = torch.randn(n, first.hidden_size, generator=gen, device=device).to(torch.bfloat16)
+        ids = torch.multinomial(torch.ones(n, first.num_experts, device=device), first.top_k,
+                                replacement=False, generator=gen).to(torch.int32)
+        w = torch.rand(n, first.top_k, generator=gen, device=device)
         with torch.cuda.stream(self.stream):
-            for n in buckets:
-                x = torch.randn(n, first.hidden_size, device=device, dtype=torch.bfloat16, generator=gen)
-                scores = torch.rand(n, first.num_experts, device=device, generator=gen)
-                topk_ids = scores.topk(first.top_k, dim=1).indices.to(torch.int32)
-                topk_weights = torch.rand(n, first.top_k, device=device, generator=gen)
-                topk_output = StandardTopKOutput(topk_weights, topk_ids, None)
-                for layer_id in layers[:1] if n > 256 else layers:
-                    self.experts[layer_id](x, topk_output)
+            for i, size in enumerate(sizes):
+                topk = StandardTopKOutput(w[:size], ids[:size])
+                for layer_id in (order if i == 0 else order[:1]):
+                    self.experts[layer_id](x[:size], topk)
         torch.cuda.synchronize()
-        return buckets
+        return sizes
 
     def rows_of(self, row):
         """x, topk_ids and topk_weights of one row: views into the RecvArena. x is a tuple:
         (bf16 [n, H],) or, with fp8 activations on the wire, (e4m3 codes, scales)."""
         g, arena = self.g, self.server.recv
-        n, off = row.n_tokens, row.x_ptr - self.server.recv_base
+        n, base = row.n_tokens, row.x_ptr - self.server.recv_base
+
+        def view(off, nbytes, dtype, shape):
+            return arena[off : off + nbytes].view(dtype).view(shape)
+
         if g.act == "bf16":
-            x = (arena[off : off + n * g.hidden * 2].view(torch.bfloat16).view(n, g.hidden),)
+            x = (view(base, n * g.hidden * 2, torch.bfloat16, (n, g.hidden)),)
         else:
             shape, dtype = act_scale_shape(g.act, n, g.hidden)
-            xs_off = off + g.xs_off
-            x = (arena[off : off + n * g.hidden].view(n, g.hidden),
-                 arena[xs_off : xs_off + n * g.xs_bytes_per_token].view(dtype).view(shape))
-        ids_off, w_off = off + g.ids_off, off + g.w_off
-        topk_ids = arena[ids_off : ids_off + n * g.topk * 4].view(torch.int32).view(n, g.topk)
-        topk_weights = arena[w_off : w_off + n * g.topk * 4].view(torch.float32).view(n, g.topk)
+            x = (view(base, n * g.hidden, torch.uint8, (n, g.hidden)),
+                 view(base + g.xs_off, n * g.xs_bytes_per_token, dtype, shape))
+        topk_ids = view(base + g.ids_off, n * g.topk * 4, torch.int32, (n, g.topk))
+        topk_weights = view(base + g.w_off, n * g.topk * 4, torch.float32, (n, g.topk))
         return x, topk_ids, topk_weights
+
+    def _inputs(self, job):
+        parts = [self.rows_of(row) for row in job.rows]
+        if len(parts) == 1:
+            return parts[0]
+        x = tuple(torch.cat([p[0][i] for p in parts]) for i in range(len(parts[0][0])))
+        return x, torch.cat([p[1] for p in parts]), torch.cat([p[2] for p in parts])
+
+    def _experts(self, layer_id: int, x: tuple, ids, w, out):
+        if self.graph_runner is not None:
+            result = self.graph_runner.run(layer_id, x, ids, w, 0, out=out)
+            if result is not None:
+                return result
+        layer = self.experts[layer_id]
+        topk = StandardTopKOutput(w, ids)
+        return layer(x[0], topk, out=out) if len(x) == 1 else layer.forward_q(*x, topk, out=out)
 
     @torch.no_grad()
     def run_job(self, job) -> None:
-        """One expert call for the job's rows, then one reply per row. Only enqueues."""
-        tic, timer = time.perf_counter(), self.job_timer
+        """Gate, expert call and reply of one job, all enqueued on the F stream."""
         stream = self.stream
-        self.server.wait_rows(job, stream.cuda_stream)
+        self.server.gate(job, stream.cuda_stream)
+        token = self.clock.start(stream) if self.clock is not None else None
         with torch.cuda.stream(stream):
-            started = timer.start(stream) if timer else None
-            rows = [self.rows_of(row) for row in job.rows]
-            if len(rows) == 1:
-                x, topk_ids, topk_weights = rows[0]
-            else:
-                x = tuple(torch.cat(part) for part in zip(*(r[0] for r in rows)))
-                topk_ids, topk_weights = (torch.cat(part) for part in zip(*(r[1:] for r in rows)))
-            n = topk_ids.shape[0]
-            output, buffer, used_buffer = None, 0, False
-            reply = self.reply_stream
-            out = None
-            if len(job.rows) == 1:  # write the partial sum straight into A's segment
-                out = self.server.seg_view(job.rows[0])
-            if self.graph_runner is not None and n <= self.graph_runner.buckets[-1]:
-                if out is None and reply is not None:
-                    buffer, used_buffer = self.reply_turn, True
-                    # the reply that last read this buffer, before the replay overwrites it
-                    stream.wait_event(self.reply_free[buffer])
-                output = self.graph_runner.run(job.layer_id, x, topk_ids, topk_weights, buffer, out=out)
-            if output is None:
-                topk_output = StandardTopKOutput(topk_weights, topk_ids, None)
-                layer = self.experts[job.layer_id]
-                if len(x) == 1:
-                    output = layer(x[0], topk_output, out=out)
-                else:  # fp8 on the wire: the rows are quantized already
-                    output = layer.forward_q(*x, topk_output, out=out)
-            experts_done = timer.event(stream) if timer else None
-        if reply is None:
-            rstream = stream
-        else:
-            self.reply_ready.record(stream)
-            reply.wait_event(self.reply_ready)
-            rstream = reply
-        start = 0
-        for row in job.rows:
-            nbytes = row.n_tokens * self.g.hidden * 2
-            self.server.reply(row, output[start].data_ptr(), nbytes, rstream.cuda_stream)
-            start += row.n_tokens
+            x, ids, w = self._inputs(job)
+            out = self.server.seg_view(job.rows[0]) if len(job.rows) == 1 else None
+            output = self._experts(job.layer_id, x, ids, w, out)
+            self.server.reply_job(job, output.data_ptr(), stream.cuda_stream)
         self.layer_calls[job.layer_id] += 1
-        if used_buffer:
-            self.reply_free[buffer].record(reply)
-            self.reply_turn = 1 - buffer
-        if timer:
-            timer.add(n, started, experts_done, timer.event(rstream), time.perf_counter() - tic)
+        if token is not None:
+            self.clock.stop(token, ids.shape[0], stream)
 
     def serve_pending(self) -> int:
         """Poll once and run every complete job (the one-GPU form of serve_forever)."""

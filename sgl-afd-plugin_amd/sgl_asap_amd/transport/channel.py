@@ -1,126 +1,119 @@
-"""A side of the transport on one MI355X: ``AttnChannel`` and its ``Watchdog``.
+"""A side of the transport on one MI355X: ``AttnChannel`` and its ``StallWatch``.
 
-Follows ``python/sgl_asap_plugin/transport/channel.py``: ``send`` (:317-362) enqueues, on
-the caller's stream, the backpressure waits on every F rank's done flag, the three payload
-copies into the F rank's RecvArena region and the 64-bit doorbell; ``wait`` (:364-377)
-enqueues the waits for the replies and returns the result segment addresses; a
-``Watchdog`` (:100-167) times the oldest unfinished group of waits and, on timeout, writes
-every awaited value so the parked streams are released, after which ``check``/``send``
-raise ``ChannelPoisoned`` until ``reconnect``. ``_backpressure`` / ``_epoch_override``
-exist, as in the reference (:198-203), only for tests that provoke protocol violations.
+The attention rank's end of the connection to every F rank (the role of
+``python/sgl_asap_plugin/transport/channel.py``): ``send`` enqueues one message of a slot
+(the reference's :317-362) as one ``afd_send`` call, ``wait`` enqueues the waits for the F
+ranks' answers (:364-377) as one ``afd_wait_replies`` call and returns the result segments,
+``check`` raises ``ChannelPoisoned`` once a wait had to be released, and ``reconnect`` is the
+way out (:301-311). ``_backpressure`` / ``_epoch_override`` are for tests that provoke
+protocol violations (:198-203).
 
-On one GPU the done flags live in pinned host memory (``hip.HostPage``) rather than in
-the ResultArena's device flag page, so the watchdog releases a parked wait with a plain
-host store, independent of any GPU queue; the segments stay in device memory at the
-reference's offsets (``Geometry.seg_off`` minus the flag page).
+Design on one GPU:
+* Every (F rank, slot) has a 64-bit done counter in a pinned host page. Message m of a slot
+  has count ``base + m``; F's reply stores that count, A's streams wait for ``counter >= m``
+  (backpressure before overwriting the slot's region: ``>= m - 1``). Counts only grow, so the
+  32-bit sequence field of the doorbell word may wrap while no wait ever compares across it.
+* The per-slot part of the send descriptor (regions, doorbell and counter addresses) is
+  built once at connect; a send fills in the payload pointers, sizes and doorbell words and
+  makes one C call, so the host enqueue of a message is a single ctypes call.
+* Liveness: ``StallWatch`` reads the done counters straight from the pinned page. A counter
+  that some stream waits on and that has not moved for ``timeout_s`` means the F side is dead
+  or stuck; the watch then stores every awaited count (which releases every parked wait, the
+  counters being compared with >=) and poisons the channel. It needs no events and no GPU
+  calls, so a scan is a few loads.
 """
 
 from __future__ import annotations
 
-import collections
 import threading
 import time
-from dataclasses import dataclass, field
-from typing import Callable, List, Optional, Sequence, Tuple
+from dataclasses import dataclass
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
+from .. import _lib
 from . import hip
-from .layout import (
-    ID_BYTES,
-    SEQ_MASK,
-    ChannelPoisoned,
-    Geometry,
-    HandshakeError,
-    pack_doorbell,
-)
+from .layout import ID_BYTES, ChannelPoisoned, Geometry, HandshakeError, pack_doorbell
+
+COUNT_LIMIT = 1 << 63  # the largest base a channel accepts: counts never reach 2^64
 
 
-class _Phase:
-    """A group of stream waits plus the event recorded right after them; ``release`` lists
-    (page, offset, value) stores that satisfy every wait of the group."""
+class StallWatch:
+    """Detects a dead F side from the done counters an attention rank waits on.
 
-    __slots__ = ("event", "release", "what", "state", "t_head")
+    ``expect(offset, value, what)`` records that a stream will wait for the counter at
+    ``offset`` of ``page`` to reach ``value``. ``scan(now)`` forgets satisfied expectations,
+    restarts the quiet clock of every outstanding counter that moved, and if one has stayed
+    unchanged for more than ``timeout_s`` stores every outstanding expected value (releasing
+    all parked waits) and returns the description of the wait that stalled. ``start`` runs
+    ``scan`` every ``period_s`` on a daemon thread and calls ``on_stall`` with the result."""
 
-    def __init__(self, event, release: List[Tuple[hip.HostPage, int, int]], what: str):
-        self.event, self.release, self.what = event, release, what
-        self.state = "pending"
-        self.t_head: Optional[float] = None
-
-
-class Watchdog(threading.Thread):
-    """Releases A's stream waits when F does not answer within ``timeout_s``.
-
-    Phases of one stream finish in order, so only the oldest unfinished phase is timed, from
-    when it became the oldest (an O(1) scan every ``SCAN_S``). On timeout every pending
-    phase's awaited values are stored into the pinned flag pages, which releases all parked
-    waits, and ``on_timeout`` is called."""
-
-    SCAN_S = 0.02
-
-    def __init__(self, timeout_s: float, on_timeout: Callable[[_Phase], None]):
-        super().__init__(name="asap-watchdog", daemon=True)
-        self.timeout_s, self.on_timeout = timeout_s, on_timeout
-        self._queue: collections.deque = collections.deque()
+    def __init__(self, page, timeout_s: float, on_stall: Callable[[str], None], period_s: float = 0.02):
+        self.page, self.timeout_s, self.on_stall, self.period_s = page, timeout_s, on_stall, period_s
+        self._want: Dict[int, Tuple[int, str]] = {}  # offset -> (largest awaited value, its wait)
+        self._quiet: Dict[int, Tuple[int, float]] = {}  # offset -> (value seen, since when)
         self._lock = threading.Lock()
-        self._stop_evt = threading.Event()
+        self._halt = threading.Event()
+        self._thread: Optional[threading.Thread] = None
 
-    def watch(self, stream, release: List[Tuple[hip.HostPage, int, int]], what: str) -> _Phase:
-        import torch
-
-        event = torch.cuda.Event()
-        event.record(stream)
-        phase = _Phase(event, release, what)
+    def expect(self, offset: int, value: int, what: str) -> None:
         with self._lock:
-            self._queue.append(phase)
-        return phase
+            if value > self._want.get(offset, (-1, ""))[0]:
+                self._want[offset] = (value, what)
 
-    def scan(self, now: Optional[float] = None) -> Optional[_Phase]:
-        """One scan; returns the phase that timed out, if any."""
+    def outstanding(self) -> Dict[int, int]:
+        with self._lock:
+            return {off: v for off, (v, _) in self._want.items()}
+
+    def scan(self, now: Optional[float] = None) -> Optional[str]:
         now = time.monotonic() if now is None else now
         with self._lock:
-            while self._queue and self._queue[0].event.query():
-                done = self._queue.popleft()
-                if done.state == "pending":
-                    done.state = "done"
-            head = self._queue[0] if self._queue else None
-            if head is None or head.state != "pending":
+            stalled = None
+            for off in list(self._want):
+                value, what = self._want[off]
+                seen = self.page.load(off)
+                if seen >= value:
+                    del self._want[off]
+                    self._quiet.pop(off, None)
+                    continue
+                last = self._quiet.get(off)
+                if last is None or last[0] != seen:
+                    self._quiet[off] = (seen, now)
+                elif now - last[1] > self.timeout_s and stalled is None:
+                    stalled = what
+            if stalled is None:
                 return None
-            if head.t_head is None:
-                head.t_head = now
-                return None
-            if now - head.t_head <= self.timeout_s:
-                return None
-            for p in self._queue:
-                if p.state == "pending":
-                    p.state = "failed"
-                    for page, off, value in p.release:
-                        page.store(off, value)
-        return head
+            for off, (value, _) in self._want.items():
+                self.page.store(off, value)
+            self._want.clear()
+            self._quiet.clear()
+            return stalled
 
-    def run(self) -> None:
-        while not self._stop_evt.wait(self.SCAN_S):
-            late = self.scan()
-            if late is not None:
-                self.on_timeout(late)
+    def _loop(self) -> None:
+        while not self._halt.wait(self.period_s):
+            what = self.scan()
+            if what is not None:
+                self.on_stall(what)
+
+    def start(self) -> "StallWatch":
+        self._thread = threading.Thread(target=self._loop, name="afd-stall-watch", daemon=True)
+        self._thread.start()
+        return self
 
     def stop(self) -> None:
-        self._stop_evt.set()
-        if self.is_alive():
-            self.join(timeout=5.0)
-        with self._lock:
-            self._queue.clear()
+        self._halt.set()
+        if self._thread is not None and self._thread.is_alive():
+            self._thread.join(timeout=5.0)
+        self._thread = None
 
 
-@dataclass
+@dataclass(frozen=True)
 class Ticket:
-    """One message in flight; ``send`` / ``reply`` are the watched phases of its waits."""
+    """A sent message: its slot, its 64-bit count on that slot, and what it carried."""
 
     slot: int
     seq: int
     layer_id: int
     n_tokens: int
-    send: Optional[_Phase] = None
-    reply: Optional[_Phase] = None
-    result_ptrs: List[int] = field(default_factory=list)
 
 
 class AttnChannel:
@@ -133,75 +126,93 @@ class AttnChannel:
             raise ValueError(f"need one server per F rank ({geometry.num_f}), got {len(servers)}")
         if not 0 <= a < geometry.num_a:
             raise ValueError(f"A rank {a} is outside [0, {geometry.num_a})")
+        if geometry.num_f > _lib.AFD_MAX_F:
+            raise ValueError(f"at most {_lib.AFD_MAX_F} F ranks, got {geometry.num_f}")
+        if not 0 <= seq_base < COUNT_LIMIT:
+            raise ValueError(f"seq_base must be in [0, 2^63), got {seq_base}")
         self.a, self.g, self.servers = a, geometry, list(servers)
-        self.device, self.seq_base, self.timeout_s = device, seq_base & SEQ_MASK, timeout_s
+        self.device, self.seq_base, self.timeout_s = device, seq_base, timeout_s
         self._backpressure, self._epoch_override = _backpressure, _epoch_override
-        self._poison: Optional[ChannelPoisoned] = None
-        self._watchdog: Optional[Watchdog] = None
         self.flags: Optional[hip.HostPage] = None
-        self.segments = None  # device tensor of num_f * slots result segments
-        self._recv: List[int] = []
-        self._bells: List[hip.HostPage] = []
-        self._epoch: List[int] = []
-        self._seq: List[int] = []
+        self.segments = None  # device uint8 tensor: num_f * slots result segments
+        self.watch: Optional[StallWatch] = None
+        self._poison: Optional[ChannelPoisoned] = None
+        self._count: List[int] = []
+        self._epochs: List[int] = []
+        self._desc: List[_lib.AfdSendDesc] = []
+        self._done_addrs: List[List[int]] = []
 
+    # ---- lifetime ----
     def connect(self) -> "AttnChannel":
-        """Allocate the result flags and segments, hand them to every F rank, map their
-        RecvArenas and doorbell pages."""
+        """Fresh done counters (all at seq_base) and result segments; one handshake per F
+        rank; the per-slot send descriptors."""
         import torch
 
         g = self.g
         self.flags = hip.HostPage(g.flags_bytes)
-        for f in range(g.num_f):
-            for s in range(g.slots):
-                self.flags.store(g.done_off(f, s), self.seq_base)
-        self.segments = torch.empty(g.num_f * g.slots * g.seg_bytes, dtype=torch.uint8, device=f"cuda:{self.device}")
+        self.segments = torch.empty(g.num_f * g.slots * g.seg_bytes, dtype=torch.uint8,
+                                    device=f"cuda:{self.device}")
+        arenas, bells = [], []
         try:
+            for f in range(g.num_f):
+                for s in range(g.slots):
+                    self.flags.store(g.done_off(f, s), self.seq_base)
+            self._epochs = []
             for server in self.servers:
-                reply = server.hello(self.a, self.flags, self.segments, g)
-                if reply["seq_base"] != self.seq_base:
-                    raise HandshakeError(f"seq_base A={self.seq_base} F={reply['seq_base']}")
-                self._recv.append(reply["recv"])
-                self._bells.append(reply["doorbells"])
-                self._epoch.append(reply["epoch"])
+                answer = server.hello(self.a, self.flags, self.segments, g)
+                if answer["seq_base"] != self.seq_base:
+                    raise HandshakeError(f"seq_base A={self.seq_base} F={answer['seq_base']}")
+                arenas.append(answer["recv"])
+                bells.append(answer["doorbells"])
+                self._epochs.append(answer["epoch"])
         except BaseException:
             self.close()
             raise
-        self._seq = [self.seq_base] * g.slots
+        self._desc, self._done_addrs = [], []
+        for s in range(g.slots):
+            d = _lib.AfdSendDesc()
+            d.num_f = g.num_f
+            d.xs_off, d.ids_off, d.w_off = g.xs_off, g.ids_off, g.w_off
+            done = [self.flags.addr(g.done_off(f, s)) for f in range(g.num_f)]
+            for f in range(g.num_f):
+                d.region[f] = arenas[f] + g.region_off(self.a, s)
+                d.bell[f] = bells[f].addr(g.bell_off(self.a, s))
+                d.done[f] = done[f] if self._backpressure else None
+            self._desc.append(d)
+            self._done_addrs.append(done)
+        self._count = [self.seq_base] * g.slots
         self._poison = None
-        self._watchdog = Watchdog(self.timeout_s, self._on_timeout)
-        self._watchdog.start()
+        self.watch = StallWatch(self.flags, self.timeout_s, self._stalled).start()
         return self
 
     def reconnect(self) -> "AttnChannel":
-        """The only way out of a poisoned channel: fresh flags and segments, a new epoch."""
+        """The only way out of a poisoned channel: new counters, segments and epochs."""
         self.close()
         return self.connect()
 
     def close(self) -> None:
         """Release everything (synchronize the streams that used the channel first)."""
-        if self._watchdog is not None:
-            self._watchdog.stop()
-            self._watchdog = None
+        if self.watch is not None:
+            self.watch.stop()
+            self.watch = None
         if self.flags is not None:
             self.flags.release()
             self.flags = None
         self.segments = None
-        self._recv, self._bells, self._epoch = [], [], []
+        self._desc, self._done_addrs = [], []
 
-    def _on_timeout(self, phase: _Phase) -> None:
+    def _stalled(self, what: str) -> None:
         self._poison = ChannelPoisoned(
-            f"A rank {self.a}: {phase.what} did not complete within {self.timeout_s}s, F is dead or stuck; "
-            "the results of every pending message are garbage until reconnect()"
+            f"A rank {self.a}: {what} saw no answer for {self.timeout_s}s; the F side is dead or "
+            "stuck, its pending waits were released and their results are invalid until reconnect()"
         )
 
     def check(self) -> None:
+        """Raise ``ChannelPoisoned`` if a wait had to be released."""
         if self._poison is not None:
             raise self._poison
 
-    def done_offset(self, f: int, slot: int) -> int:
-        return self.g.done_off(f, slot)
-
+    # ---- addresses ----
     def seg_ptr(self, f: int, slot: int) -> int:
         return self.segments.data_ptr() + self.g.seg_off(f, slot) - self.g.flags_bytes
 
@@ -214,56 +225,48 @@ class AttnChannel:
         seg = self.segments[off : off + n_tokens * self.g.hidden * 2]
         return seg.view(torch.bfloat16).view(n_tokens, self.g.hidden)
 
+    def done_count(self, f: int, slot: int) -> int:
+        """The done counter of (F rank f, slot) as the host sees it now."""
+        return self.flags.load(self.g.done_off(f, slot))
+
+    # ---- messages ----
     def send(self, layer_id: int, slot: int, x_ptr: int, ids_ptr: int, w_ptr: int, n_tokens: int, stream,
              xs_ptr: int = 0) -> Ticket:
         """Enqueue one message on ``stream`` (a torch stream): ``n_tokens`` rows of x (bf16
-        [n, hidden]), top-k ids (int32 [n, topk]) and weights (fp32 [n, topk]) to every F rank.
-        With fp8 activations on the wire (``g.act`` != "bf16") x_ptr holds the e4m3 codes
-        [n, hidden] and xs_ptr their scales [n, g.xs_bytes_per_token bytes]."""
+        [n, hidden], or with fp8 activations on the wire the e4m3 codes [n, hidden] at x_ptr
+        and their scales at xs_ptr), top-k ids (int32 [n, topk]) and weights (fp32 [n, topk])
+        to every F rank."""
         self.check()
         g = self.g
         if not (0 <= slot < g.slots and 1 <= n_tokens <= g.n_max):
             raise ValueError(f"slot {slot} / n_tokens {n_tokens} outside the geometry {g}")
         if (g.act != "bf16") != bool(xs_ptr):
-            raise ValueError(f"activation format {g.act} {'needs' if xs_ptr == 0 else 'takes no'} scales")
-        seq = self._seq[slot] = (self._seq[slot] + 1) & SEQ_MASK
-        sh = stream.cuda_stream
-        x_n, k_n = n_tokens * g.x_bytes_per_token, n_tokens * g.topk * ID_BYTES
-        xs_n = n_tokens * g.xs_bytes_per_token
-        if self._backpressure:  # the previous message of this slot must be answered first
-            for f in range(g.num_f):
-                hip.wait64(sh, self.flags.addr(g.done_off(f, slot)), (seq - 1) & SEQ_MASK)
+            raise ValueError(f"activation format {g.act} {'needs' if not xs_ptr else 'takes no'} scales")
+        seq = self._count[slot] + 1
+        d = self._desc[slot]
+        d.x, d.x_bytes = x_ptr, n_tokens * g.x_bytes_per_token
+        d.xs, d.xs_bytes = (xs_ptr or None), n_tokens * g.xs_bytes_per_token
+        d.ids, d.w, d.ids_bytes = ids_ptr, w_ptr, n_tokens * g.topk * ID_BYTES
+        d.done_min = seq - 1
+        for f in range(g.num_f):
+            epoch = self._epochs[f] if self._epoch_override is None else self._epoch_override
+            d.word[f] = pack_doorbell(seq, n_tokens, layer_id, epoch)
+        hip.send(d, stream.cuda_stream)
+        self._count[slot] = seq
         for f, server in enumerate(self.servers):
-            epoch = self._epoch[f] if self._epoch_override is None else self._epoch_override
-            dst = self._recv[f] + g.region_off(self.a, slot)
-            hip.copy_async(dst, x_ptr, x_n, sh)
-            if xs_n:
-                hip.copy_async(dst + g.xs_off, xs_ptr, xs_n, sh)
-            hip.copy_async(dst + g.ids_off, ids_ptr, k_n, sh)
-            hip.copy_async(dst + g.w_off, w_ptr, k_n, sh)  # fp32 weights: the size of the int32 ids
-            word = pack_doorbell(seq, n_tokens, layer_id, epoch)
-            # the doorbell goes last in the same stream: F's wait on it implies the payload landed
-            hip.write64(sh, self._bells[f].addr(g.bell_off(self.a, slot)), word)
-            server.announce(self.a, slot, word)
-        ticket = Ticket(slot, seq, layer_id, n_tokens)
-        ticket.send = self._watchdog.watch(
-            stream,
-            [(self.flags, g.done_off(f, slot), (seq - 1) & SEQ_MASK) for f in range(g.num_f)],
-            f"send of layer {layer_id} slot {slot} seq {seq}",
-        )
-        return ticket
+            server.announce(self.a, slot, d.word[f])
+        if self._backpressure and seq - 1 > self.seq_base:
+            for f in range(g.num_f):
+                self.watch.expect(g.done_off(f, slot), seq - 1, f"send of layer {layer_id} slot {slot} #{seq}")
+        return Ticket(slot, seq, layer_id, n_tokens)
 
     def wait(self, ticket: Ticket, stream) -> List[int]:
         """Enqueue on ``stream`` the waits for every F rank's answer to ``ticket``; returns the
-        device addresses of the E partial sums (bf16 [n_tokens, hidden] each)."""
+        device addresses of the partial sums (bf16 [n_tokens, hidden] each, F-rank order)."""
         self.check()
-        g, slot, seq = self.g, ticket.slot, ticket.seq
+        g, slot = self.g, ticket.slot
+        hip.wait_replies(self._done_addrs[slot], ticket.seq, stream.cuda_stream)
         for f in range(g.num_f):
-            hip.wait64(stream.cuda_stream, self.flags.addr(g.done_off(f, slot)), seq)
-        ticket.reply = self._watchdog.watch(
-            stream,
-            [(self.flags, g.done_off(f, slot), seq) for f in range(g.num_f)],
-            f"reply to layer {ticket.layer_id} slot {slot} seq {seq}",
-        )
-        ticket.result_ptrs = [self.seg_ptr(f, slot) for f in range(g.num_f)]
-        return ticket.result_ptrs
+            self.watch.expect(g.done_off(f, slot), ticket.seq,
+                              f"reply to layer {ticket.layer_id} slot {slot} #{ticket.seq}")
+        return [self.seg_ptr(f, slot) for f in range(g.num_f)]

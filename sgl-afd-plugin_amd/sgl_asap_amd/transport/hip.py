@@ -1,14 +1,17 @@
-"""Transport primitives over libafd: pinned flag pages, device copies, 64-bit stream memops.
+"""Transport calls into libafd: pinned flag pages, the fused send / reply, stream memops.
 
 Replaces the libcuda ctypes bindings the reference transport uses
 (``python/sgl_asap_plugin/transport/cuda_wrapper.py``: ``memcpy_async``, ``write32/64``,
-``wait32`` at :258-270). All calls only enqueue on the given stream; failures raise the
-exception classes of ``_lib.check`` (``HIPError`` for a HIP runtime error).
+``wait32`` at :258-270) with the calls of ``include/afd.h``: ``afd_send`` (backpressure waits,
+payload copies and doorbells of one message in one call), ``afd_reply`` (partial-sum copies
+and done counters of one job) and ``afd_wait_replies``. All of them only enqueue on the given
+stream; failures raise the exception classes of ``_lib.check``.
 
-Sequence numbers are compared with the EQ condition on their low 32 bits. With the
-protocol's backpressure (a slot's next message is sent only after the previous reply
-landed) a flag can only hold seq - 1 or seq when a wait for seq runs, so equality is the
-wrap-safe form of the reference's cyclic GEQ wait (HIP's GEQ is a plain unsigned compare).
+Done flags are 64-bit message counters that only grow and are waited on with ``>=``, so a
+store of any later count releases every earlier wait. The F side gates its stream on a
+doorbell word with an equality test on the word's 32-bit sequence field: the producer rings
+the next doorbell of a slot only after the F side answered the current one, so the field holds
+the awaited value or an older one while the gate waits.
 """
 
 from __future__ import annotations
@@ -20,13 +23,13 @@ import numpy as np
 from .. import _lib
 from .layout import SEQ_MASK
 
-WAIT_GEQ, WAIT_EQ, WAIT_AND, WAIT_NOR = _lib.AFD_WAIT_GEQ, _lib.AFD_WAIT_EQ, _lib.AFD_WAIT_AND, _lib.AFD_WAIT_NOR
+WAIT_GEQ, WAIT_EQ = _lib.AFD_WAIT_GEQ, _lib.AFD_WAIT_EQ
 
 
 class HostPage:
-    """Pinned, coherent, zero-filled host memory the GPU can read and write with memops
-    (the doorbell page and the done-flag page). ``words`` is a uint64 numpy view the host
-    reads and writes with plain loads and stores."""
+    """Pinned, coherent, zero-filled host memory the GPU reads and writes with memops (the
+    doorbell page, the done-counter page). ``words`` is a uint64 numpy view the host reads
+    and writes with plain loads and stores."""
 
     def __init__(self, nbytes: int):
         ptr = ctypes.c_void_p()
@@ -52,6 +55,28 @@ class HostPage:
             self.ptr = 0
 
 
+def send(desc: _lib.AfdSendDesc, stream: int) -> None:
+    """Enqueue one message (``afd_send``): backpressure waits, payload copies, doorbells."""
+    _lib.check(_lib.lib().afd_send(ctypes.byref(desc), stream), "afd_send")
+
+
+def reply(rows: "ctypes.Array", count: int, stream: int) -> None:
+    """Enqueue the answers of ``count`` rows (``afd_reply``): copies, then done counters."""
+    _lib.check(_lib.lib().afd_reply(rows, count, stream), "afd_reply")
+
+
+def wait_replies(addrs, seq: int, stream: int) -> None:
+    """Park ``stream`` until every done counter at ``addrs`` holds at least ``seq``."""
+    arr = (ctypes.c_void_p * len(addrs))(*addrs)
+    _lib.check(_lib.lib().afd_wait_replies(arr, len(addrs), seq, stream), "afd_wait_replies")
+
+
+def gate_on_doorbell(stream: int, addr: int, seq: int) -> None:
+    """Park ``stream`` until the sequence field of the doorbell word at ``addr`` equals the
+    low 32 bits of ``seq``."""
+    _lib.call("afd_stream_wait64", stream, addr, seq & SEQ_MASK, SEQ_MASK, WAIT_EQ)
+
+
 def copy_async(dst: int, src: int, nbytes: int, stream: int) -> None:
     _lib.call("afd_copy_async", dst, src, nbytes, stream)
 
@@ -61,7 +86,7 @@ def write64(stream: int, addr: int, value: int) -> None:
     _lib.call("afd_stream_write64", stream, addr, value)
 
 
-def wait64(stream: int, addr: int, value: int, mask: int = SEQ_MASK, cond: int = WAIT_EQ) -> None:
-    """Park ``stream`` until the 64-bit word at ``addr`` satisfies ``cond`` against
-    ``value`` under ``mask`` (default: low 32 bits equal ``value``)."""
+def wait64(stream: int, addr: int, value: int, mask: int = 0xFFFFFFFFFFFFFFFF, cond: int = WAIT_GEQ) -> None:
+    """Park ``stream`` until the 64-bit word at ``addr`` satisfies ``cond`` against ``value``
+    under ``mask`` (default: the whole word >= ``value``)."""
     _lib.call("afd_stream_wait64", stream, addr, value & 0xFFFFFFFFFFFFFFFF, mask, cond)

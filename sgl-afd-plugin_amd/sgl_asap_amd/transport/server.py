@@ -1,48 +1,59 @@
-"""F side of the transport on one MI355X: the RecvArena, the doorbell page, job discovery
-and replies.
+"""F side of the transport on one MI355X: the RecvArena, the doorbell page, job discovery,
+the doorbell gate and the replies.
 
-Follows ``python/sgl_asap_plugin/transport/server.py``: the ``Peer`` / ``Row`` / ``Job``
-records (:47-81), the handshake's epoch rule (:237, ``(old % 31) + 1``), ``poll`` with the
-cyclic int32 sequence compare, lost-message count and round-robin start (:262-294), ``_row``
-validation (unknown peer, stale epoch, bad n; :296-320), ``_job`` grouping of T rows
-(:322-338), ``reply`` (:340-350) and the observable ``stats`` / ``trace``.
+The F rank's end of the connection (the role of ``python/sgl_asap_plugin/transport/server.py``):
+``hello`` admits an A rank and hands out its epoch (``(old % 31) + 1``, :237), discovery turns
+doorbell words into ``Row`` / ``Job`` records (:47-81) under the reference's rules, and
+``reply_job`` answers a job (:340-350) with one ``afd_reply`` call.
 
-What differs on one GPU, and why:
-* The reference's F host polls the doorbell page and only then launches the experts. Here
-  the producer stream rings the doorbell in pinned host memory with a 64-bit stream memop,
-  and the same word is posted to ``announce`` (an in-process mirror of the page), so F's host
-  learns of the message without waiting for the GPU. ``run_job`` then parks F's stream on the
-  real doorbell (``hip.wait64``), so the experts start when the payload has landed and no
-  host thread ever waits for the GPU.
-* Handshakes are calls (``hello``) instead of a TCP JSON line: A and F share a process.
+Discovery, on one GPU: A's producer stream rings the doorbell in pinned host memory with a
+64-bit stream store, and ``AttnChannel.send`` also posts the same word to ``announce``. The
+server keeps the posted words in one arrival-ordered inbox, so its host learns of a message
+the moment it is enqueued, without waiting for the GPU, and ``gate`` then parks the F stream
+on the real doorbell so the experts start once the payload has landed. Because every posted
+word stays in the inbox until a poll consumes it, a message is never overwritten unread (two
+sends on one slot before a poll are served in order), and jobs are handed out first come,
+first served across A ranks.
+
+Rules a word is checked against, in this order (the reference's, with its stats keys):
+* sequence: the word's 32-bit sequence field against the last one seen on its (a, slot),
+  as a cyclic int32 difference; 0 or negative -> an old word, ignored; d > 1 -> d - 1
+  messages were never posted (``lost_messages``); the 64-bit count of the message is the
+  last count + d;
+* the A rank must have said hello (``unknown_peer``), the word must carry its current epoch
+  (``stale_epoch``), and 1 <= n_tokens <= n_max (``bad_doorbell``);
+* the rows of one replica's group of A ranks (``Geometry.group``) for one slot form a job once
+  all have arrived; they must name the same layer (``group_mismatch``).
+Handshakes are calls (``hello``) instead of a TCP JSON line: A and F share a process.
 """
 
 from __future__ import annotations
 
 import collections
+import ctypes
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 from typing import Callable, Dict, List, Optional
 
-import numpy as np
-
+from .. import _lib
 from . import hip
-from .layout import MAX_EPOCH, SEQ_MASK, Geometry, HandshakeError, unpack_doorbell
+from .layout import MAX_EPOCH, SEQ_MASK, Geometry, HandshakeError, seq_ahead, unpack_doorbell
 
 
 @dataclass
 class Peer:
-    """A connected A rank: its done-flag page, its result segments and its epoch."""
+    """A connected A rank: its done-counter page, its result segments and its epoch."""
 
     a: int
-    flags: Optional[hip.HostPage]  # A's done flags (pinned host page, FLAG_STRIDE apart)
-    segments: object  # A's result segments: a device uint8 tensor at seg_off - flags_bytes
+    flags: Optional[hip.HostPage]
+    segments: object  # device uint8 tensor: the rank's result segments (at seg_off - flags_bytes)
     epoch: int
 
 
 @dataclass
 class Row:
-    """One A rank's part of a job; the pointers address this F rank's RecvArena."""
+    """One A rank's part of a job. ``seq`` is the message's 64-bit count on its slot; the
+    pointers address this F rank's RecvArena."""
 
     a: int
     slot: int
@@ -57,7 +68,7 @@ class Row:
 
 @dataclass
 class Job:
-    """One micro-batch of one layer of one replica, ready to compute."""
+    """One micro-batch of one layer of one replica, ready to compute (rows in group order)."""
 
     replica: int
     slot: int
@@ -66,51 +77,47 @@ class Job:
     t_detect_ns: int
 
 
-@dataclass
-class _Mirror:
-    words: np.ndarray = field(default_factory=lambda: np.zeros(0, dtype=np.uint64))
-
-
 class FfnServer:
-    """One F rank's end of the transport: ``start`` -> (``hello`` per A rank) -> ``poll`` /
-    ``serve_pending`` -> ``reply`` -> ``close``.
+    """One F rank's end of the transport: ``start`` -> ``hello`` per A rank -> ``poll`` /
+    ``serve_pending`` -> ``gate`` + ``reply_job`` -> ``close``.
 
     ``memory="none"`` skips the device and pinned allocations (host-logic tests)."""
+
+    STATS = ("lost_messages", "unknown_peer", "stale_epoch", "bad_doorbell", "group_mismatch", "jobs",
+             "replica_switches", "reconnects", "dropped_replies")
 
     def __init__(self, f_rank: int, geometry: Geometry, *, device: int = 0, seq_base: int = 0,
                  memory: str = "device", trace_len: int = 4096):
         if memory not in ("device", "none"):
             raise ValueError(f"memory must be 'device' or 'none', got {memory!r}")
-        self.f, self.g, self.seq_base = f_rank, geometry, seq_base & SEQ_MASK
+        self.f, self.g, self.seq_base = f_rank, geometry, seq_base
         self.device, self.memory = device, memory
-        self.stats: collections.Counter = collections.Counter()
+        self.stats: collections.Counter = collections.Counter({k: 0 for k in self.STATS})
         self.trace: collections.deque = collections.deque(maxlen=trace_len)
         self.peers: Dict[int, Peer] = {}
-        self._pending: Dict[tuple, Dict[int, Row]] = {}
-        self._rr = 0
-        self._prev_replica = None
         self.recv = None
         self.recv_base = 0
         self.bells: Optional[hip.HostPage] = None
-        self._mirror = _Mirror()
-        self._last = np.zeros(0, dtype=np.uint32)
+        self._inbox: collections.deque = collections.deque()  # (a, slot, word) in arrival order
+        self._count: List[int] = []  # per (a, slot): 64-bit count of the last word taken
+        self._forming: Dict[tuple, Dict[int, Row]] = {}  # (replica, slot) -> rows so far
+        self._last_replica: Optional[int] = None
 
     # ---- lifetime ----
     def start(self) -> "FfnServer":
-        """Allocate the RecvArena (device) and the doorbell page (pinned host); every
-        doorbell starts at seq_base."""
+        """Allocate the RecvArena (device) and the doorbell page (pinned host); every doorbell
+        holds seq_base."""
         g = self.g
-        cells = g.num_a * g.slots
         if self.memory == "device":
             import torch
 
             self.recv = torch.zeros(g.recv_bytes, dtype=torch.uint8, device=f"cuda:{self.device}")
             self.recv_base = self.recv.data_ptr()
             self.bells = hip.HostPage(g.host_bytes)
-            for i in range(cells):
-                self.bells.store(g.bell_off(i // g.slots, i % g.slots), self.seq_base)
-        self._mirror.words = np.full(cells, self.seq_base, dtype=np.uint64)
-        self._last = np.full(cells, self.seq_base, dtype=np.uint32)
+            for a in range(g.num_a):
+                for s in range(g.slots):
+                    self.bells.store(g.bell_off(a, s), self.seq_base & SEQ_MASK)
+        self._count = [self.seq_base] * (g.num_a * g.slots)
         return self
 
     def close(self) -> None:
@@ -119,11 +126,13 @@ class FfnServer:
             self.bells = None
         self.recv = None
         self.peers.clear()
+        self._inbox.clear()
 
-    # ---- handshake (server.py:181-259, as a call) ----
+    # ---- handshake (the reference's server.py:181-259, as a call) ----
     def hello(self, a: int, flags: Optional[hip.HostPage], segments, geometry: Geometry) -> dict:
-        """Admit A rank ``a``: check the geometry field by field, hand out a new epoch, reset
-        its doorbells' last-seen sequence. Returns what A maps: recv base, doorbell page."""
+        """Admit A rank ``a``: the geometry must match field by field; a new epoch; the rank's
+        sequence state, doorbells, unread words and half-formed jobs are reset. Returns what
+        A maps: the RecvArena base, the doorbell page, the epoch and the sequence base."""
         if geometry.proto_version != self.g.proto_version:
             raise HandshakeError(f"protocol version A={geometry.proto_version} F={self.g.proto_version}")
         if geometry != self.g:
@@ -131,90 +140,89 @@ class FfnServer:
             raise HandshakeError(f"geometry mismatch (A, F): {diff}")
         if not 0 <= a < self.g.num_a:
             raise HandshakeError(f"A rank {a} outside [0, {self.g.num_a})")
-        old = self.peers.get(a)
-        if old is not None:  # a restarted or reconnecting A rank
+        before = self.peers.get(a)
+        if before is not None:
             self.stats["reconnects"] += 1
-        epoch = (old.epoch % MAX_EPOCH) + 1 if old is not None else 1
+        epoch = 1 if before is None else before.epoch % MAX_EPOCH + 1
         self.peers[a] = Peer(a, flags, segments, epoch)
-        for s in range(self.g.slots):
-            idx = a * self.g.slots + s
-            self._mirror.words[idx] = np.uint64(self.seq_base)
-            self._last[idx] = np.uint32(self.seq_base)
+        slots = self.g.slots
+        self._count[a * slots:(a + 1) * slots] = [self.seq_base] * slots
+        self._inbox = collections.deque(m for m in self._inbox if m[0] != a)
+        for s in range(slots):
             if self.bells is not None:
-                self.bells.store(self.g.bell_off(a, s), self.seq_base)
-            self._pending.pop((a // self.g.group, s), None)  # half-assembled jobs of the old incarnation
+                self.bells.store(self.g.bell_off(a, s), self.seq_base & SEQ_MASK)
+            self._forming.pop((a // self.g.group, s), None)
         return {"recv": self.recv_base, "doorbells": self.bells, "epoch": epoch, "seq_base": self.seq_base}
 
     # ---- discovery ----
-    def announce(self, a: int, s: int, word: int) -> None:
-        """The doorbell word A's producer stream writes to bell(a, s); F's host reads it from
-        this mirror instead of waiting for the GPU to land it."""
-        self._mirror.words[a * self.g.slots + s] = np.uint64(word)
+    def announce(self, a: int, slot: int, word: int) -> None:
+        """Post the doorbell word A's producer stream will write to bell(a, slot)."""
+        self._inbox.append((a, slot, int(word)))
 
     def poll(self) -> List[Job]:
-        """Jobs whose rows all arrived since the last call; never blocks (server.py:262-294)."""
-        g, jobs = self.g, []
-        words = self._mirror.words.copy()
-        seq = (words & np.uint64(SEQ_MASK)).astype(np.uint32)
-        ahead = (seq - self._last).view(np.int32)
-        ready = np.flatnonzero(ahead > 0)
-        if ready.size > 1:
-            ready = np.concatenate([ready[ready >= self._rr], ready[ready < self._rr]])
-        for idx in ready.tolist():
-            a, s = divmod(idx, g.slots)
-            self.stats["lost_messages"] += int(ahead[idx]) - 1
-            self._last[idx] = seq[idx]
-            self._rr = idx + 1
-            row = self._row(a, s, int(words[idx]))
-            if row is None:
-                continue
-            rows = self._pending.setdefault((a // g.group, s), {})
-            rows[a % g.group] = row
-            if len(rows) == g.group:
-                job = self._job(a // g.group, s, self._pending.pop((a // g.group, s)))
-                if job is not None:
-                    jobs.append(job)
+        """Every job completed by the words posted since the last call; never blocks."""
+        jobs = []
+        while self._inbox:
+            row = self._take(*self._inbox.popleft())
+            job = self._add_row(row) if row is not None else None
+            if job is not None:
+                jobs.append(job)
         return jobs
 
-    def _row(self, a: int, s: int, word: int) -> Optional[Row]:
-        seq, n_tokens, layer_id, epoch = unpack_doorbell(word)
+    def _take(self, a: int, slot: int, word: int) -> Optional[Row]:
+        """Check one posted word against the rules; a Row if it starts a message to serve."""
+        seq32, n_tokens, layer_id, epoch = unpack_doorbell(word)
+        cell = a * self.g.slots + slot
+        step = seq_ahead(seq32, self._count[cell] & SEQ_MASK)
+        if step <= 0:
+            return None
+        self.stats["lost_messages"] += step - 1
+        count = self._count[cell] = self._count[cell] + step
         peer = self.peers.get(a)
-        if peer is None:
-            self.stats["unknown_peer"] += 1
+        reason = ("unknown_peer" if peer is None else
+                  "stale_epoch" if epoch != peer.epoch else
+                  "bad_doorbell" if not 1 <= n_tokens <= self.g.n_max else None)
+        if reason is not None:
+            self.stats[reason] += 1
             return None
-        if epoch != peer.epoch:
-            self.stats["stale_epoch"] += 1
-            return None
-        if not 1 <= n_tokens <= self.g.n_max:
-            self.stats["bad_doorbell"] += 1
-            return None
-        base = self.recv_base + self.g.region_off(a, s)
-        return Row(a, s, seq, epoch, layer_id, n_tokens, base, base + self.g.ids_off, base + self.g.w_off)
+        x_ptr = self.recv_base + self.g.region_off(a, slot)
+        return Row(a=a, slot=slot, seq=count, epoch=epoch, layer_id=layer_id, n_tokens=n_tokens,
+                   x_ptr=x_ptr, ids_ptr=x_ptr + self.g.ids_off, w_ptr=x_ptr + self.g.w_off)
 
-    def _job(self, replica: int, slot: int, rows: Dict[int, Row]) -> Optional[Job]:
-        ordered = [rows[j] for j in range(self.g.group)]
-        if len({r.layer_id for r in ordered}) > 1:
+    def _add_row(self, row: Row) -> Optional[Job]:
+        group = self.g.group
+        key = (row.a // group, row.slot)
+        forming = self._forming.setdefault(key, {})
+        forming[row.a % group] = row
+        if len(forming) < group:
+            return None
+        del self._forming[key]
+        rows = [forming[i] for i in range(group)]
+        if any(r.layer_id != rows[0].layer_id for r in rows):
             self.stats["group_mismatch"] += 1
             return None
+        replica = key[0]
         self.stats["jobs"] += 1
-        if self._prev_replica is not None and replica != self._prev_replica:
+        if self._last_replica not in (None, replica):
             self.stats["replica_switches"] += 1
-        self._prev_replica = replica
-        self.trace.append((replica, slot, ordered[0].layer_id))
-        return Job(replica, slot, ordered[0].layer_id, ordered, time.monotonic_ns())
+        self._last_replica = replica
+        self.trace.append((replica, row.slot, rows[0].layer_id))
+        return Job(replica=replica, slot=row.slot, layer_id=rows[0].layer_id, rows=rows,
+                   t_detect_ns=time.monotonic_ns())
 
-    # ---- GPU-side gate and answer ----
-    def bell_addr(self, a: int, s: int) -> int:
-        return self.bells.addr(self.g.bell_off(a, s))
+    # ---- the F stream: gate, answer ----
+    def bell_addr(self, a: int, slot: int) -> int:
+        return self.bells.addr(self.g.bell_off(a, slot))
 
-    def wait_rows(self, job: Job, stream: int) -> None:
-        """Park ``stream`` until every row's doorbell has landed (its payload copies are then
-        complete: the producer rings after them, in stream order)."""
+    def gate(self, job: Job, stream: int) -> None:
+        """Park ``stream`` until every row's doorbell has landed; the producer rings after its
+        payload copies on the same stream, so the payload is then in the RecvArena."""
         for row in job.rows:
-            hip.wait64(stream, self.bell_addr(row.a, row.slot), row.seq)
+            hip.gate_on_doorbell(stream, self.bell_addr(row.a, row.slot), row.seq)
 
     def seg_view(self, row: Row):
-        """A rank row.a's result segment for this F rank and slot, as bf16 [n_tokens, hidden]."""
+        """A rank row.a's result segment for this F rank and the row's slot, as bf16
+        [n_tokens, hidden]."""
         import torch
 
         g = self.g
@@ -222,20 +230,32 @@ class FfnServer:
         seg = self.peers[row.a].segments[off : off + row.n_tokens * g.hidden * 2]
         return seg.view(torch.bfloat16).view(row.n_tokens, g.hidden)
 
-    def reply(self, row: Row, src_ptr: int, nbytes: int, stream: int) -> None:
-        """Enqueue: copy the partial sum into A's segment (skipped when the experts wrote it
-        there), then ring A's done flag with the row's seq. Dropped if A reconnected."""
-        peer, g = self.peers.get(row.a), self.g
-        if peer is None or peer.epoch != row.epoch:
-            self.stats["dropped_replies"] += 1
-            return
-        dst = self.seg_view(row).data_ptr()
-        if src_ptr != dst:
-            hip.copy_async(dst, src_ptr, nbytes, stream)
-        hip.write64(stream, peer.flags.addr(g.done_off(self.f, row.slot)), row.seq)
+    def reply_job(self, job: Job, output_ptr: int, stream: int) -> None:
+        """Answer every row of ``job`` in one ``afd_reply``: the row's slice of the job output
+        (bf16 [sum n_tokens, hidden] at ``output_ptr``, rows in order) goes to the A rank's
+        segment unless it is already there, then the A rank's done counter := the row's
+        count. Rows of A ranks that reconnected since are dropped (``dropped_replies``)."""
+        g = self.g
+        descs = (_lib.AfdReplyDesc * len(job.rows))()
+        used, offset = 0, 0
+        for row in job.rows:
+            nbytes = row.n_tokens * g.hidden * 2
+            peer = self.peers.get(row.a)
+            if peer is None or peer.epoch != row.epoch:
+                self.stats["dropped_replies"] += 1
+            else:
+                d = descs[used]
+                d.src, d.dst = output_ptr + offset, self.seg_view(row).data_ptr()
+                d.bytes = nbytes
+                d.done = peer.flags.addr(g.done_off(self.f, row.slot))
+                d.value = row.seq
+                used += 1
+            offset += nbytes
+        if used:
+            hip.reply(descs, used, stream)
 
     def serve_pending(self, handler: Callable[[Job], None]) -> int:
-        """Hand every job found by one poll to ``handler``; returns how many."""
+        """Hand every job of one poll to ``handler`` (which only enqueues); returns how many."""
         jobs = self.poll()
         for job in jobs:
             handler(job)

@@ -99,8 +99,9 @@ def test_sequence_wrap():
             out = layer(x, topk)
             torch.cuda.synchronize()
             assert np.array_equal(bits16(out), direct(experts, 0, x, topk))
-        assert afd.channel._seq[0] == 5  # 2^32 - 3 + 8 wrapped
-        assert afd.server.stats["jobs"] == 8
+        # the doorbells' 32-bit sequence field wrapped after 2 messages; the done counter did not
+        assert afd.channel.done_count(0, 0) == (1 << 32) - 3 + 8
+        assert afd.server.stats["jobs"] == 8 and afd.server.stats["lost_messages"] == 0
 
 
 def test_exchange_above_n_max():
@@ -216,3 +217,111 @@ def test_group_of_two_a_ranks(graphs):
                 torch.cuda.synchronize()
                 assert np.array_equal(bits16(got), direct(experts, 0, x, topk)), (rnd, r)
         assert afd.server.stats["jobs"] == 2
+
+
+def _send(afd, r, slot, x, topk, stream):
+    ids = topk.topk_ids.to(torch.int32).contiguous()
+    w = topk.topk_weights.to(torch.float32).contiguous()
+    stream.wait_stream(torch.cuda.current_stream())
+    t = afd.channels[r].send(0, slot, x.data_ptr(), ids.data_ptr(), w.data_ptr(), x.shape[0], stream)
+    return t, (x, ids, w)
+
+
+def test_group_jobs_served_back_to_back():
+    """A group of 2 A ranks, eager: two jobs served one after the other with no host
+    synchronization between them; each job's output buffer is only reused after its reply
+    copies ran, so both answers are right."""
+    say("loop: group of 2, two eager jobs back to back")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, slots=2, group=2) as afd:
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        main = torch.cuda.current_stream()
+        keep, tickets = [], []
+        for slot in range(2):
+            for r in range(2):
+                x, topk = job(9 + 11 * r + 5 * slot, 800 + 2 * slot + r)
+                t, held = _send(afd, r, slot, x, topk, sends[r])
+                tickets.append((r, t))
+                keep.append((x, topk, held))
+        assert afd.scheduler.serve_pending() == 2
+        got = []
+        for r, t in tickets:
+            afd.channels[r].wait(t, main)
+            got.append(afd.channels[r].result_view(0, t.slot, t.n_tokens).clone())
+        torch.cuda.synchronize()
+        for (x, topk, _), g in zip(keep, got):
+            assert np.array_equal(bits16(g), direct(experts, 0, x, topk))
+
+
+def test_two_sends_on_one_slot_before_serving():
+    """The producer posts message 2 of a slot before the F host polled message 1 (its stream
+    then waits for the answer to 1 before overwriting the region): F serves 1, then 2, and the
+    answer to 2 is right."""
+    say("loop: two sends on one slot before a poll")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, slots=1) as afd:
+        send = torch.cuda.Stream()
+        main = torch.cuda.current_stream()
+        (x1, k1), (x2, k2) = job(21, 901), job(30, 902)
+        t1, h1 = _send(afd, 0, 0, x1, k1, send)
+        t2, h2 = _send(afd, 0, 0, x2, k2, send)
+        assert (t1.seq, t2.seq) == (1, 2)
+        assert afd.scheduler.serve_pending() == 2
+        afd.channel.wait(t2, main)
+        got = afd.channel.result_view(0, 0, t2.n_tokens).clone()
+        torch.cuda.synchronize()
+        assert np.array_equal(bits16(got), direct(experts, 0, x2, k2))
+        assert afd.server.stats["lost_messages"] == 0 and afd.channel.done_count(0, 0) == 2
+
+
+def test_stall_releases_the_parked_wait_and_poisons():
+    """A message whose doorbell carries a wrong epoch is dropped by the F server, so its reply
+    never comes: the compute stream parked on the done counter is released by the stall watch
+    (a host store of the awaited count into the pinned page) after timeout_s, the channel is
+    poisoned, and after reconnect() messages flow again. The stream is polled, never
+    synchronized, until released."""
+    import time
+
+    from sgl_asap_amd.transport.layout import ChannelPoisoned
+
+    say("loop: dropped message -> stall watch releases the wait, channel poisoned, reconnect")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, slots=1, timeout_s=0.3, _epoch_override=7) as afd:
+        ch, main = afd.channel, torch.cuda.current_stream()
+        send = torch.cuda.Stream()
+        x, topk = job(12, 950)
+        t, held = _send(afd, 0, 0, x, topk, send)
+        assert afd.scheduler.serve_pending() == 0 and afd.server.stats["stale_epoch"] == 1
+        ch.wait(t, main)
+        done = torch.cuda.Event()
+        done.record(main)
+        deadline = time.monotonic() + 10.0
+        while not done.query() and time.monotonic() < deadline:
+            time.sleep(0.01)
+        if not done.query():  # keep the process able to exit, then fail
+            ch.flags.store(ch.g.done_off(0, 0), t.seq)
+            pytest.fail("the stall watch did not release the parked wait")
+        with pytest.raises(ChannelPoisoned):
+            ch.check()
+        with pytest.raises(ChannelPoisoned):
+            AsapMoE(E, H, I, 0, top_k=K)(x, topk)
+        ch._epoch_override = None
+        ch.reconnect()
+        layer = AsapMoE(E, H, I, 0, top_k=K)
+        out = layer(x, topk)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits16(out), direct(experts, 0, x, topk))
+
+
+def test_warmup_then_serve():
+    """The F scheduler's warm-up runs every bucket size on two layers, then jobs are served
+    as before."""
+    say("loop: scheduler warm-up up to 64 tokens, two layers")
+    experts = make_experts(64, layers=(0, 1))
+    with OneGpuAfd(experts, n_max=64, graph_max_tokens=64) as afd:
+        assert afd.scheduler.warmup(64) == [1, 2, 4, 8, 16, 32, 64]
+        for lid in (0, 1):
+            x, topk = job(40, 990 + lid)
+            out = AsapMoE(E, H, I, lid, top_k=K)(x, topk)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits16(out), direct(experts, lid, x, topk))

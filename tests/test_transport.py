@@ -1,11 +1,16 @@
-"""Transport host logic on the CPU: doorbell and geometry known answers, the F poller's
+"""Transport host logic on the CPU: doorbell and geometry known answers, the F server's
 rules (cyclic sequence compare, lost messages, stale epochs, unknown peers, bad sizes,
-round-robin order, T-row jobs) and the watchdog's timing, without a GPU."""
+arrival order, every posted word served, T-row jobs) against the oracle's restatement of the
+reference's poller, and the stall watch (timing, release stores, poisoning), without a GPU."""
 
+import random
+
+import numpy as np
 import pytest
 
 from oracle import transport as OT
 from sgl_asap_amd.transport import layout as L
+from sgl_asap_amd.transport.channel import AttnChannel, StallWatch
 from sgl_asap_amd.transport.server import FfnServer
 
 
@@ -132,7 +137,7 @@ def test_seq_ahead_cyclic():
     assert L.seq_ahead(3, 3) == 0
 
 
-# ---- F poller (server.py:262-338)
+# ---- F server: discovery rules (the reference's server.py:262-338)
 def server(num_a=2, group=1, slots=2, seq_base=0):
     g = L.Geometry(num_a=num_a, group=group, slots=slots, n_max=64, hidden=256, topk=2, num_f=1)
     s = FfnServer(0, g, memory="none", seq_base=seq_base).start()
@@ -143,6 +148,10 @@ def connect(s, g, a):
     return s.hello(a, None, None, g)["epoch"]
 
 
+def served(jobs):
+    return [(j.replica, j.slot, j.layer_id, [r.seq for r in j.rows]) for j in jobs]
+
+
 def test_poll_basic_and_empty():
     s, g = server()
     e = connect(s, g, 0)
@@ -151,25 +160,41 @@ def test_poll_basic_and_empty():
     jobs = s.poll()
     assert len(jobs) == 1 and jobs[0].layer_id == 3 and jobs[0].slot == 1
     assert jobs[0].rows[0].n_tokens == 10 and jobs[0].rows[0].ids_ptr == g.region_off(0, 1) + g.ids_off
-    assert s.poll() == []  # already seen
+    assert jobs[0].rows[0].w_ptr == g.region_off(0, 1) + g.w_off
+    assert s.poll() == []  # nothing new
     assert s.stats["jobs"] == 1 and s.trace[-1] == (0, 1, 3)
 
 
-def test_poll_counts_lost_messages():
+def test_two_sends_on_one_slot_before_a_poll_are_both_served_in_order():
+    """The producer may post message s + 1 of a slot before the F host polled s (its stream
+    then waits for the answer to s before it overwrites the region): both are served, s
+    first, and nothing counts as lost."""
     s, g = server()
     e = connect(s, g, 0)
     s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
-    s.announce(0, 0, L.pack_doorbell(3, 5, 0, e))  # 2 overwritten before the poll saw 1
+    s.announce(0, 0, L.pack_doorbell(2, 7, 1, e))
     jobs = s.poll()
-    assert len(jobs) == 1 and jobs[0].rows[0].seq == 3
+    assert served(jobs) == [(0, 0, 0, [1]), (0, 0, 1, [2])]
+    assert s.stats["lost_messages"] == 0
+
+
+def test_gaps_count_as_lost_and_old_words_are_ignored():
+    s, g = server()
+    e = connect(s, g, 0)
+    s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
+    s.announce(0, 0, L.pack_doorbell(4, 5, 0, e))  # 2 and 3 were never posted
+    assert served(s.poll()) == [(0, 0, 0, [1]), (0, 0, 0, [4])]
     assert s.stats["lost_messages"] == 2
+    s.announce(0, 0, L.pack_doorbell(4, 5, 0, e))  # the same word again
+    s.announce(0, 0, L.pack_doorbell(2, 5, 0, e))  # an older one
+    assert s.poll() == [] and s.stats["lost_messages"] == 2
 
 
 def test_poll_drops_stale_epoch_unknown_peer_bad_size():
     s, g = server()
     e = connect(s, g, 0)
     s.announce(0, 0, L.pack_doorbell(1, 5, 0, (e % 31) + 1))
-    s.announce(1, 0, L.pack_doorbell(1, 5, 0, 1))  # rank 1 never connected
+    s.announce(1, 0, L.pack_doorbell(1, 5, 0, 1))  # rank 1 never said hello
     s.announce(0, 1, L.pack_doorbell(1, 64, 0, e))  # n == n_max is fine
     assert len(s.poll()) == 1
     assert s.stats["stale_epoch"] == 1 and s.stats["unknown_peer"] == 1
@@ -179,37 +204,28 @@ def test_poll_drops_stale_epoch_unknown_peer_bad_size():
     assert s2.poll() == [] and s2.stats["bad_doorbell"] == 1
 
 
-def test_poll_round_robin_order():
+def test_jobs_come_out_in_arrival_order():
     s, g = server(num_a=2, slots=2)
-    e0, e1 = connect(s, g, 0), connect(s, g, 1)
-    for seq in (1, 2):
-        for a, e in ((0, e0), (1, e1)):
-            for slot in (0, 1):
-                s.announce(a, slot, L.pack_doorbell(seq, 4, seq, e))
-        jobs = s.poll()
-        order = [(j.replica, j.slot) for j in jobs]
-        if seq == 1:
-            assert order == [(0, 0), (0, 1), (1, 0), (1, 1)]
-        else:  # starts after the last served index, then wraps
-            assert order == [(0, 0), (0, 1), (1, 0), (1, 1)]
-    # one doorbell ahead of the round-robin pointer is served before the ones behind it
-    s.announce(0, 1, L.pack_doorbell(3, 4, 0, e0))
-    s.announce(1, 0, L.pack_doorbell(3, 4, 0, e1))
-    s._rr = 2
-    assert [(j.replica, j.slot) for j in s.poll()] == [(1, 0), (0, 1)]
+    e = [connect(s, g, 0), connect(s, g, 1)]
+    order = [(1, 1), (0, 0), (1, 0), (0, 1)]
+    for a, slot in order:
+        s.announce(a, slot, L.pack_doorbell(1, 4, 0, e[a]))
+    assert [(j.replica, j.slot) for j in s.poll()] == order
+    assert s.stats["replica_switches"] == 3
 
 
-def test_poll_sequence_wrap():
-    s, g = server(seq_base=(1 << 32) - 2)
+def test_sequence_field_wraps_while_counts_grow():
+    base = (1 << 32) - 2
+    s, g = server(seq_base=base)
     e = connect(s, g, 0)
-    for seq in ((1 << 32) - 1, 0, 1, 2):
-        s.announce(0, 0, L.pack_doorbell(seq, 4, 0, e))
+    for m in range(1, 5):  # sequence fields 0xFFFFFFFF, 0, 1, 2
+        s.announce(0, 0, L.pack_doorbell(base + m, 4, 0, e))
         jobs = s.poll()
-        assert len(jobs) == 1 and jobs[0].rows[0].seq == seq & L.SEQ_MASK
+        assert len(jobs) == 1 and jobs[0].rows[0].seq == base + m
     assert s.stats["lost_messages"] == 0
 
 
-def test_poll_groups_tp_rows_into_one_job():
+def test_group_rows_form_one_job():
     s, g = server(num_a=4, group=2, slots=1)
     eps = [connect(s, g, a) for a in range(4)]
     s.announce(1, 0, L.pack_doorbell(1, 4, 7, eps[1]))
@@ -218,7 +234,7 @@ def test_poll_groups_tp_rows_into_one_job():
     jobs = s.poll()
     assert len(jobs) == 1 and [r.a for r in jobs[0].rows] == [0, 1] and jobs[0].replica == 0
     s.announce(2, 0, L.pack_doorbell(1, 4, 7, eps[2]))
-    s.announce(3, 0, L.pack_doorbell(1, 4, 8, eps[3]))  # TP ranks disagree on the layer
+    s.announce(3, 0, L.pack_doorbell(1, 4, 8, eps[3]))  # the ranks of a group disagree on the layer
     assert s.poll() == [] and s.stats["group_mismatch"] == 1
 
 
@@ -230,7 +246,9 @@ def test_hello_epochs_cycle_and_reconnect_resets():
     e = epochs[-1]
     s.announce(0, 0, L.pack_doorbell(9, 4, 0, e))
     assert len(s.poll()) == 1
-    e2 = connect(s, g, 0)  # reconnect: last-seen back to seq_base
+    s.announce(0, 1, L.pack_doorbell(1, 4, 0, e))  # posted, then the rank reconnects unread
+    e2 = connect(s, g, 0)  # sequence state back to seq_base, unread words dropped
+    assert s.poll() == []
     s.announce(0, 0, L.pack_doorbell(1, 4, 0, e2))
     assert len(s.poll()) == 1
 
@@ -248,31 +266,128 @@ def test_hello_rejects_geometry_mismatch():
         s.hello(0, None, None, fp8)
 
 
-def test_server_matches_oracle_poll_on_random_streams():
-    """The poller against the oracle's restatement on random doorbell streams."""
-    import random
+def random_stream(rnd, s, g, oracle=None):
+    """Random doorbell words of 3 A ranks (some never connect, some words carry a wrong
+    epoch or size, some skip a sequence number)."""
+    eps = {}
+    for a in range(3):
+        if rnd.random() < 0.8:
+            eps[a] = connect(s, g, a)
+            if oracle is not None:
+                oracle.hello(a)
+    seqs = {(a, sl): s.seq_base for a in range(3) for sl in range(2)}
+    words = []
+    for _ in range(40):
+        a, sl = rnd.randrange(3), rnd.randrange(2)
+        seqs[(a, sl)] += rnd.choice([1, 1, 1, 2])
+        epoch = eps.get(a, 1) if rnd.random() < 0.9 else 17
+        words.append((a, sl, L.pack_doorbell(seqs[(a, sl)], rnd.choice([1, 5, 64, 65]), rnd.randrange(4), epoch)))
+    return words
 
+
+def test_server_matches_oracle_poller_on_random_streams():
+    """Polled after every posted word (the only order the reference's page can show, since a
+    slot's doorbell cannot advance before its previous message was answered), the server
+    hands out the jobs of the oracle's restatement of the reference's poller, with the same
+    counts (sequence fields compared modulo 2^32)."""
     rnd = random.Random(0)
     for trial in range(20):
         s, g = server(num_a=3, slots=2, seq_base=rnd.choice([0, (1 << 32) - 5]))
         o = OT.Poller(num_a=3, group=1, slots=2, n_max=64, seq_base=s.seq_base)
-        eps = {}
-        for a in range(3):
-            if rnd.random() < 0.8:
-                eps[a] = connect(s, g, a)
-                o.hello(a)
-        seqs = {(a, sl): s.seq_base for a in range(3) for sl in range(2)}
-        for step in range(40):
-            a, sl = rnd.randrange(3), rnd.randrange(2)
-            seqs[(a, sl)] = (seqs[(a, sl)] + rnd.choice([1, 1, 1, 2])) & L.SEQ_MASK
-            epoch = eps.get(a, 1) if rnd.random() < 0.9 else 17
-            n = rnd.choice([1, 5, 64, 65])
-            word = L.pack_doorbell(seqs[(a, sl)], n, rnd.randrange(4), epoch)
+        for a, sl, word in random_stream(rnd, s, g, o):
             s.announce(a, sl, word)
             o.announce(a, sl, word)
-            if rnd.random() < 0.5:
-                got = [(j.replica, j.slot, j.layer_id, [r.seq for r in j.rows]) for j in s.poll()]
-                want = o.poll()
-                assert got == want
+            got = [(r, sl_, lay, [q & L.SEQ_MASK for q in seqs]) for r, sl_, lay, seqs in served(s.poll())]
+            assert got == o.poll(), trial
         for k, v in o.stats.items():
             assert s.stats[k] == v, (trial, k)
+
+
+def test_polling_rarely_serves_the_same_jobs():
+    """Every posted word stays in the inbox until a poll takes it: polling at random moments
+    yields exactly the jobs (and counts) of polling after every word."""
+    rnd = random.Random(1)
+    for trial in range(20):
+        base = rnd.choice([0, (1 << 32) - 5])
+        s1, g = server(num_a=3, slots=2, seq_base=base)
+        s2, _ = server(num_a=3, slots=2, seq_base=base)
+        words = random_stream(random.Random(trial), s1, g)
+        random_stream(random.Random(trial), s2, g)
+        every, rare = [], []
+        for a, sl, word in words:
+            s1.announce(a, sl, word)
+            every += served(s1.poll())
+            s2.announce(a, sl, word)
+            if rnd.random() < 0.2:
+                rare += served(s2.poll())
+        rare += served(s2.poll())
+        assert rare == every, trial
+        assert s1.stats == s2.stats
+
+
+# ---- stall watch (liveness of the F side, seen from the attention rank)
+class FakePage:
+    """The done-counter page as the host sees it: 64-bit words at byte offsets."""
+
+    def __init__(self, nbytes=256):
+        self.words = np.zeros(nbytes // 8, dtype=np.uint64)
+
+    def load(self, off):
+        return int(self.words[off // 8])
+
+    def store(self, off, value):
+        self.words[off // 8] = np.uint64(value)
+
+
+def test_stall_watch_times_unmoving_counters_and_releases_every_wait():
+    page = FakePage()
+    stalls = []
+    w = StallWatch(page, timeout_s=1.0, on_stall=stalls.append)
+    page.store(0, 3)
+    page.store(64, 6)
+    w.expect(0, 5, "reply #5")
+    w.expect(0, 4, "send #5")  # a smaller value on the same counter adds nothing
+    w.expect(64, 7, "reply on slot 1")
+    assert w.scan(now=0.0) is None  # clocks start
+    page.store(0, 4)  # progress on counter 0 restarts its clock
+    assert w.scan(now=0.8) is None
+    assert w.scan(now=1.5) == "reply on slot 1"  # counter 64 quiet since 0.0
+    assert (page.load(0), page.load(64)) == (5, 7)  # every awaited value stored: waits are >=
+    assert w.outstanding() == {} and w.scan(now=10.0) is None
+
+
+def test_stall_watch_forgets_answered_waits():
+    page = FakePage()
+    w = StallWatch(page, timeout_s=0.5, on_stall=lambda what: None)
+    w.expect(8, 2, "reply #2")
+    assert w.scan(now=0.0) is None
+    page.store(8, 9)  # answered (and later messages too)
+    assert w.scan(now=5.0) is None and w.outstanding() == {}
+    assert page.load(8) == 9  # nothing stored over a satisfied counter
+
+
+def test_stall_poisons_the_channel():
+    g = L.Geometry(num_a=1, group=1, slots=2, n_max=64, hidden=256, topk=2, num_f=1)
+    ch = AttnChannel(0, g, [None], timeout_s=0.5)
+    page = FakePage()
+    ch.watch = StallWatch(page, 0.5, ch._stalled)
+    ch.watch.expect(g.done_off(0, 1), 1, "reply to layer 3 slot 1 #1")
+    ch.check()  # healthy
+    assert ch.watch.scan(now=0.0) is None
+    what = ch.watch.scan(now=1.0)
+    ch._stalled(what)
+    with pytest.raises(L.ChannelPoisoned, match="layer 3 slot 1"):
+        ch.check()
+    with pytest.raises(L.ChannelPoisoned):
+        ch.send(3, 1, 0, 0, 0, 1, None)
+    assert page.load(g.done_off(0, 1)) == 1
+
+
+def test_channel_argument_checks():
+    g = L.Geometry(num_a=1, group=1, slots=2, n_max=64, hidden=256, topk=2, num_f=1)
+    with pytest.raises(ValueError):
+        AttnChannel(1, g, [None])  # rank outside the geometry
+    with pytest.raises(ValueError):
+        AttnChannel(0, g, [None, None])  # one server per F rank
+    with pytest.raises(ValueError):
+        AttnChannel(0, g, [None], seq_base=1 << 63)
