@@ -209,6 +209,20 @@ int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights, con
                   const void* xs, const int32_t* ids, const float* w, int32_t n, void* ws,
                   uint64_t ws_bytes, uint16_t* out, afd_stream_t stream);
 
+/* The expert call without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments and results as afd_moe_ffn,
+ * bit for bit; the workspace is the library's own file-scope device array of
+ * AFD_NOALLOC_SCRATCH_BYTES (128 MiB), one per GPU, held from the library's load until the
+ * process ends. Jobs whose afd_workspace_layout(cfg, n).total exceeds it are rejected with
+ * AFD_ERR_WORKSPACE (DeepSeek-V4 F-rank shape, hidden 4096 / inter 2048 / 64 local experts /
+ * top-8: up to 568 tokens). Allocates nothing. Every call on a GPU uses that GPU's one array:
+ * calls that overlap on one GPU (different streams, or host threads) race. */
+#define AFD_NOALLOC_SCRATCH_BYTES (128ull << 20)
+int afd_moe_ffn_noalloc(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                        const uint16_t* x, const int32_t* ids, const float* w, int32_t n,
+                        uint16_t* out, afd_stream_t stream);
+
 /* A job described in device memory, for callers that replay captured HIP graphs: the
  * launches of afd_moe_ffn_job read the descriptor when they run, so one capture serves every
  * job written into the descriptor afterwards (no copies into static buffers, no padding of

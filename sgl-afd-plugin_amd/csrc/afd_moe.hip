@@ -306,6 +306,45 @@ extern "C" int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* wei
   return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream, nullptr);
 }
 
+// ---------------------------------------------------------------- allocation-free call
+// The workspace of afd_moe_ffn_noalloc: file-scope device memory, one copy per GPU. In host
+// code the name `scratch` stands for a host-side shadow, not a device address, so host code
+// never passes it to a kernel or a copy: it uses the address hipGetSymbolAddress returns,
+// taken once per device with that device current and kept per device.
+static __device__ __align__(256) uint8_t scratch[AFD_NOALLOC_SCRATCH_BYTES];
+
+static int scratch_address(void** out) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* address[kMaxDevices] = {};
+  int dev = 0;
+  AFD_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return AFD_ERR_ARG;
+  std::lock_guard<std::mutex> lock(mu);
+  if (address[dev] == nullptr) {
+    void* p = nullptr;
+    AFD_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr) return AFD_ERR_ARG;
+    address[dev] = p;
+  }
+  *out = address[dev];
+  return AFD_OK;
+}
+
+extern "C" int afd_moe_ffn_noalloc(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                                   const uint16_t* x, const int32_t* ids, const float* w,
+                                   int32_t n, uint16_t* out, afd_stream_t stream) {
+  afd_ws_layout L;
+  int st = afd_workspace_layout(cfg, n, &L);
+  if (st != AFD_OK) return st;
+  if (L.total > AFD_NOALLOC_SCRATCH_BYTES) return AFD_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if ((st = scratch_address(&ws)) != AFD_OK) return st;
+  const JobIn job{nullptr, x, ids, w, out, n};
+  return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, AFD_NOALLOC_SCRATCH_BYTES,
+                      stream, nullptr);
+}
+
 extern "C" int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                              const uint8_t* xq, const void* xs, const int32_t* ids,
                              const float* w, int32_t n, void* ws, uint64_t ws_bytes,

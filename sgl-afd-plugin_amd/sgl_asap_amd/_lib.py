@@ -47,6 +47,7 @@ EXPORTED = (
     "afd_route",
     "afd_moe_ffn",
     "afd_moe_ffn_q",
+    "afd_moe_ffn_noalloc",
     "afd_moe_ffn_job",
     "afd_job_set",
     "afd_moe_ffn_profiled",
@@ -63,6 +64,7 @@ EXPORTED = (
 )
 
 AFD_MAX_F = 16
+AFD_NOALLOC_SCRATCH_BYTES = 128 << 20
 
 
 class HIPError(RuntimeError):
@@ -184,6 +186,10 @@ _SIGS = {
     "afd_route": ([_P, _I32, ctypes.POINTER(AfdMoeCfg), _P, _U64, _P], _I32),
     "afd_moe_ffn": (
         [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _I32, _P, _U64, _P, _P],
+        _I32,
+    ),
+    "afd_moe_ffn_noalloc": (
+        [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _I32, _P, _P],
         _I32,
     ),
     "afd_quant_act": ([ctypes.POINTER(AfdMoeCfg), _P, _I32, _P, _P, _P], _I32),
