@@ -78,8 +78,12 @@ struct MxTile {
   static constexpr int kQP = 16 / kWaves;
   static constexpr int kPieces = kImgs * kQP + 1;
   static_assert(kWaves >= 2 * kImgs, "a scale piece per image, two for a gathered A");
-  static constexpr int kYStride = kBN + 8;  // bf16 stride of the down epilogue tile
-  static_assert(kBM * kYStride * 2 <= kLds, "down epilogue tile must fit the stages");
+  // the down epilogue's bf16 tile: kBM rows of kBN / 8 16-byte chunks, chunk c of row r at
+  // physical chunk c ^ (r % 16), so the 16 rows a 16-lane pass of a write covers (one logical
+  // chunk each) and the 16 consecutive chunks a pass of a read covers (one row) fall on 16
+  // distinct 16-byte bank groups
+  static constexpr int kYChunks = kBN / 8;
+  static_assert(kBM * kBN * 2 <= kLds, "down epilogue tile must fit the stages");
   static_assert(kImgB == 17 * 1024, "B images are 17 pieces of 1 KiB");
   static_assert(kLds <= 160 * 1024, "LDS of one CU");
   static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
@@ -425,35 +429,46 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     } else {
       // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
       // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
-      // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile: one 8-byte LDS write per
-      // group of four. Rows [0, nvalid) of this tile are real. The stores are non-temporal:
-      // y (np x H bf16) is read once, by the finalize, and does not fit in L2 anyway.
+      // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile; one exchange with the other
+      // lane half per pair of chunks gives lane half lk whole 16-byte chunks q4 = lk and
+      // 2 + lk, written with one 16-byte LDS write each. Rows [0, nvalid) of this tile are
+      // real. The stores are non-temporal: y (np x H bf16) is read once, by the finalize, and
+      // does not fit in L2 anyway.
       const int nvalid = min(kBM, row_end - m0);
-      uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
+      auto y_chunk = [](int r, int c) { return (r * T::kYChunks + (c ^ (r & 15))) * 16; };
       static_for<2>([&](auto ic) {
         constexpr int i = decltype(ic)::value;
         const int row = wm * 64 + i * 32 + lr;
         static_for<4>([&](auto jc) {
           constexpr int j = decltype(jc)::value;
+          uint32_t h[4][2];  // the lane's 4 columns of chunk q4, as two bf16 pairs
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const uint2 two = {pk_bf16(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1]),
-                               pk_bf16(acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3])};
-            *reinterpret_cast<uint2*>(yl + row * T::kYStride + wn * 128 + j * 32 + q4 * 8 +
-                                      lk * 4) = two;
+            h[q4][0] = pk_bf16(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1]);
+            h[q4][1] = pk_bf16(acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
+          }
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) {  // chunks 2 pr (lane half 0) and 2 pr + 1 (half 1)
+            // v_permlane32_swap trades the first operand of lanes 32-63 for the second operand
+            // of lanes 0-31: afterwards lane half 0 holds its own columns of chunk 2 pr and its
+            // partner's, lane half 1 its partner's columns of chunk 2 pr + 1 and its own, both
+            // in column order, with no select
+            const auto d0 = __builtin_amdgcn_permlane32_swap(h[2 * pr][0], h[2 * pr + 1][0], false, false);
+            const auto d1 = __builtin_amdgcn_permlane32_swap(h[2 * pr][1], h[2 * pr + 1][1], false, false);
+            const v4i chunk = {static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
+                               static_cast<int>(d1[1])};
+            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 128 + j * 32) / 8 + 2 * pr + lk)) = chunk;
           }
         });
       });
       __syncthreads();
-      constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
 #pragma unroll 4
-      for (int q = 0; q < 16; ++q) {
+      for (int q = 0; q < kBM * T::kYChunks / T::kThreads; ++q) {
         const int idx = q * T::kThreads + t;
-        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        const int row = idx / T::kYChunks, c = idx % T::kYChunks;
         if (row < nvalid)
-          __builtin_nontemporal_store(
-              *reinterpret_cast<const v4i*>(yl + row * T::kYStride + c * 8),
-              reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
+          __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
+                                      reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
       }
       __syncthreads();
     }
