@@ -68,9 +68,13 @@ constexpr int kLds = kAmax + kBM * 4 * 4;
 constexpr int kQX = kBM / 8 / kWaves;  // 2
 constexpr int kQW = kBN / 8 / kWaves;  // 4
 constexpr int kPieces = kQX + kQW + 1;
-constexpr int kYStride = kBN + 8;      // bf16 stride of the down epilogue tile
+// the down epilogue's bf16 tile: kBM rows of kBN / 8 16-byte chunks, chunk c of row r at
+// physical chunk c ^ (r % 16), so the 16 rows a 16-lane pass of a write covers (one logical
+// chunk each) and the 16 consecutive chunks a pass of a read covers (one row) fall on 16
+// distinct 16-byte bank groups
+constexpr int kYChunks = kBN / 8;
 static_assert(kQX * kWaves * 8 == kBM && kQW * kWaves * 8 == kBN, "pieces cover the tile");
-static_assert(kBM * kYStride * 2 <= kStages * kStage, "down epilogue tile must fit the stages");
+static_assert(kBM * kBN * 2 <= kStages * kStage, "down epilogue tile must fit the stages");
 static_assert(kLds <= 160 * 1024, "LDS of one CU");
 static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
 
@@ -445,30 +449,41 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
         quant_store([](float g, float u) { return act_swiglu(g, u); });
       }
     } else {
+      // Lane half lk holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile; trading halves
+      // with v_permlane32_swap (first operand of lanes 32-63 for the second of lanes 0-31)
+      // leaves lane half lk with whole 16-byte chunks 2 pr + lk, in column order, written to
+      // LDS with one 16-byte write each.
       const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
-      uint16_t* yl = reinterpret_cast<uint16_t*>(lds);
+      auto y_chunk = [](int r, int c) { return (r * kYChunks + (c ^ (r & 15))) * 16; };
 #pragma unroll
       for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 2; ++j) {
+          const int row = wm * 64 + i2 * 32 + lr;
+          const v16f& a = acc[i2][j];
+          uint32_t h[4][2];
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            const int row = wm * 64 + i2 * 32 + lr;
-            const int col = wn * 64 + j * 32 + q4 * 8 + lk * 4;
-            const v16f& a = acc[i2][j];
-            uint2 two = {pk_bf16(a[q4 * 4], a[q4 * 4 + 1]), pk_bf16(a[q4 * 4 + 2], a[q4 * 4 + 3])};
-            *reinterpret_cast<uint2*>(yl + row * kYStride + col) = two;
+            h[q4][0] = pk_bf16(a[q4 * 4], a[q4 * 4 + 1]);
+            h[q4][1] = pk_bf16(a[q4 * 4 + 2], a[q4 * 4 + 3]);
           }
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr) {
+            const auto d0 = __builtin_amdgcn_permlane32_swap(h[2 * pr][0], h[2 * pr + 1][0], false, false);
+            const auto d1 = __builtin_amdgcn_permlane32_swap(h[2 * pr][1], h[2 * pr + 1][1], false, false);
+            const v4i chunk = {static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
+                               static_cast<int>(d1[1])};
+            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 64 + j * 32) / 8 + 2 * pr + lk)) = chunk;
+          }
+        }
       __syncthreads();
-      constexpr int kChunksPerRow = kBN / 8;  // 16-byte chunks of a bf16 output row
 #pragma unroll 4
-      for (int q = 0; q < kBM * kChunksPerRow / kThreads; ++q) {
+      for (int q = 0; q < kBM * kYChunks / kThreads; ++q) {
         const int idx = q * kThreads + t;
-        const int row = idx / kChunksPerRow, c = idx % kChunksPerRow;
+        const int row = idx / kYChunks, c = idx % kYChunks;
         if (row < nvalid)
-          __builtin_nontemporal_store(
-              *reinterpret_cast<const v4i*>(yl + row * kYStride + c * 8),
-              reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
+          __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
+                                      reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
       }
       __syncthreads();
     }
