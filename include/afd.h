@@ -292,8 +292,9 @@ int afd_combine(const uint16_t* const* parts, int32_t num_parts, const uint16_t*
 /* One message of an attention rank to every F rank (replaces AttnChannel.send,
  * P/transport/channel.py:317-362). On `stream`, in this order:
  *   1. for every F rank f with done[f] != NULL: wait until *done[f] >= done_min;
- *   2. one copy launch: x (x_bytes), xs (xs_bytes, fp8 activations on the wire; NULL / 0 for
- *      bf16), ids and w (ids_bytes each) to region[f] + 0 / xs_off / ids_off / w_off for every f;
+ *   2. the device-to-device copies of x (x_bytes), xs (xs_bytes, fp8 activations on the wire;
+ *      NULL / 0 for bf16), ids and w (ids_bytes each) to region[f] + 0 / xs_off / ids_off / w_off
+ *      for every f;
  *   3. for every f: the 64-bit store word[f] -> *bell[f].
  * Fields must not overlap inside a region; bell and done addresses 8-byte aligned. */
 typedef struct afd_send_desc {
@@ -316,8 +317,8 @@ typedef struct afd_send_desc {
 int afd_send(const afd_send_desc* msg, afd_stream_t stream);
 
 /* One F-rank answer per row of a job (replaces FfnServer.reply, P/transport/server.py
- * :340-350): one copy launch of every row's partial sum (src -> dst, bytes; none when
- * src == dst or bytes == 0), then the 64-bit store value -> *done per row. 1..64 rows. */
+ * :340-350): the copy of every row's partial sum (src -> dst, bytes; none when src == dst or
+ * bytes == 0), then the 64-bit store value -> *done per row. 1..64 rows. */
 typedef struct afd_reply_desc {
   const void* src;
   void* dst;
