@@ -34,8 +34,10 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # the first ~25 layer calls after start-up run ~7% slower while the GPU's clocks settle
     ap.add_argument("--warmup", type=int, default=60)
+    # the first ~25 layer calls after start-up run up to 45% slower while the GPU's clocks
+    # settle: untimed calls before the warm-up steps, reported as settle_calls
+    ap.add_argument("--settle-calls", type=int, default=40)
     ap.add_argument("--workload", default="layer", choices=["layer", "stream", "loop"],
                     help="layer: one expert call per step (default); stream: the skewed job stream "
                     "from 2 replicas x 2 micro-batches through the F scheduler; loop: the one-GPU "
@@ -499,7 +501,7 @@ def main():
             w32.data_ptr(), n, ws.data_ptr(), ws.numel(), out.data_ptr(), stream.cuda_stream, arr,
         )
 
-    for _ in range(args.warmup):
+    for _ in range(args.settle_calls + args.warmup):
         step()
     torch.cuda.synchronize()
 
@@ -568,6 +570,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_calls": args.settle_calls,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -98,6 +98,7 @@ class AsapBuffer:
         self.n_max = channel.g.n_max
         self.hidden = channel.g.hidden
         self.send_stream = torch.cuda.Stream(device)
+        self._inputs_ready = torch.cuda.Event()  # recorded on the compute stream per send
         self.pump = pump
         self.act = channel.g.act
         self.stage = []
@@ -132,12 +133,14 @@ class AsapBuffer:
         for the work that produced the inputs; the caller keeps them until the answer."""
         if x.dtype != torch.bfloat16:
             raise TypeError(f"ASAP carries bf16 activations, got {x.dtype}")
+        given = (x, ids, weights)
         x = x.contiguous()
         ids = ids.to(torch.int32).contiguous()
         weights = weights.to(torch.float32).contiguous()
         slot = SLOT if micro_batch is None else micro_batch
         n = x.shape[0]
-        self.send_stream.wait_stream(torch.cuda.current_stream())
+        self._inputs_ready.record()
+        self.send_stream.wait_event(self._inputs_ready)
         x_ptr, xs_ptr = x.data_ptr(), 0
         if self.stage:
             if not (0 <= slot < len(self.stage) and 1 <= n <= self.n_max):
@@ -147,8 +150,12 @@ class AsapBuffer:
             x_ptr, xs_ptr = q.data_ptr(), s.data_ptr()
         ticket = self.channel.send(layer_id, slot, x_ptr, ids.data_ptr(), weights.data_ptr(), n, self.send_stream,
                                    xs_ptr=xs_ptr)
-        for t in (x, ids, weights):  # the caching allocator must not hand them out before the copies ran
-            t.record_stream(self.send_stream)
+        # The caller keeps its own tensors alive until the answer (keepalive); tensors made
+        # here by a conversion are registered with the send stream, so the caching allocator
+        # does not hand their memory out before the copies ran.
+        for t, g in zip((x, ids, weights), given):
+            if t is not g:
+                t.record_stream(self.send_stream)
         return ticket, (x, ids, weights)
 
     def recv(self, ticket, shared: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -401,6 +401,26 @@ class AfdExperts(torch.nn.Module):
         )
         return out
 
+    def call_ptrs(self, n: int, x_ptr: int, xs_ptr: int, ids_ptr: int, w_ptr: int, out_ptr: int,
+                  stream: int) -> None:
+        """The expert call on raw device pointers, enqueued on ``stream`` (a hipStream_t): bf16
+        rows at x_ptr (xs_ptr = 0), or the e4m3 rows and their scales of quant_act; int32 ids and
+        fp32 weights [n, k]; bf16 output [n, H]. For the serving loop, whose rows are arena
+        records: no tensor is made. The caller guarantees the sizes (``n`` <= n_max) and the
+        lifetimes; the C entry points check the configuration and the pointers."""
+        if not 0 < n <= self.n_max:
+            raise ValueError(f"{n} tokens outside [1, n_max={self.n_max}]")
+        ws = self._ws.get(stream)
+        if ws is None:
+            ws = torch.empty(self.layout["total"], dtype=torch.uint8, device=self.weights.w13.device)
+            self._ws[stream] = ws
+        if xs_ptr:
+            _lib.call("afd_moe_ffn_q", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), x_ptr, xs_ptr, ids_ptr,
+                      w_ptr, n, ws.data_ptr(), ws.numel(), out_ptr, stream)
+        else:
+            _lib.call("afd_moe_ffn", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), x_ptr, ids_ptr, w_ptr, n,
+                      ws.data_ptr(), ws.numel(), out_ptr, stream)
+
     # ---- graph replay: the job is read from a device descriptor when the calls run ----
     def call_job(self, desc: torch.Tensor, n_cap: int, quantized: bool = False) -> None:
         """Enqueue the expert call on whatever job ``desc`` (from ``new_job_desc``) holds when

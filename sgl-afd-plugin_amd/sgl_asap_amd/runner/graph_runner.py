@@ -24,11 +24,13 @@ capture time.
 from __future__ import annotations
 
 import bisect
+import ctypes
 import time
 from typing import Dict, Optional
 
 import torch
 
+from .. import _lib
 from ..moe.experts import new_job_desc, set_job
 
 
@@ -63,6 +65,28 @@ class FfnGraphRunner:
                 self.graphs[(layer_id, b)] = graph
         torch.cuda.synchronize()
         self.capture_s = time.perf_counter() - tic
+        self._job = _lib.AfdJob()  # host staging of run_ptrs' descriptor writes
+
+    def run_ptrs(self, layer_id: int, n: int, x_ptr: int, xs_ptr: int, ids_ptr: int, w_ptr: int,
+                 out_ptr: int) -> bool:
+        """``run`` on raw device pointers (the serving loop's arena records): writes the job into
+        the descriptor and replays the bucket's graph on the current stream; False, doing
+        nothing, if n is above the largest bucket. bf16 rows at x_ptr (xs_ptr = 0), or, for a
+        runner of quantized rows, the e4m3 codes at x_ptr and their scales at xs_ptr."""
+        i = bisect.bisect_left(self.buckets, n)
+        if i == len(self.buckets) or n < 1:
+            return False
+        if bool(xs_ptr) != self.quantized:
+            raise ValueError(f"the graphs take {'quantized' if self.quantized else 'bf16'} rows")
+        j = self._job
+        if self.quantized:
+            j.x, j.xq, j.xs = None, x_ptr, xs_ptr
+        else:
+            j.x, j.xq, j.xs = x_ptr, None, None
+        j.ids, j.w, j.out, j.n = ids_ptr, w_ptr, out_ptr, n
+        _lib.call("afd_job_set", self.desc.data_ptr(), ctypes.byref(j), torch.cuda.current_stream().cuda_stream)
+        self.graphs[(layer_id, self.buckets[i])].replay()
+        return True
 
     def run(self, layer_id: int, x, topk_ids, topk_weights, buffer: int = 0,
             out: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:

@@ -173,6 +173,30 @@ class FfnScheduler:
         topk = StandardTopKOutput(w, ids)
         return layer(x[0], topk, out=out) if len(x) == 1 else layer.forward_q(*x, topk, out=out)
 
+    def _run_row(self, job, stream) -> int:
+        """A job of one row (one A rank per replica): the expert call reads the arena record
+        and writes A's result segment through raw pointers (a graph replay, or the eager call
+        above the largest bucket), so no tensor is made on the way. Returns n."""
+        row, g = job.rows[0], self.g
+        n = row.n_tokens
+        xs_ptr = row.x_ptr + g.xs_off if g.act != "bf16" else 0
+        out_ptr = self.server.seg_ptr(row)
+        if self.graph_runner is None or not self.graph_runner.run_ptrs(
+                job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr):
+            self.experts[job.layer_id].call_ptrs(n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr,
+                                                 stream.cuda_stream)
+        self.server.reply_job(job, out_ptr, stream.cuda_stream)
+        return n
+
+    def _run_rows(self, job, stream) -> int:
+        """A job of several rows: their records concatenated, the output in a buffer that the
+        reply copies into each A rank's segment (same stream, so the buffer is free again
+        before the next job writes it). Returns n."""
+        x, ids, w = self._inputs(job)
+        output = self._experts(job.layer_id, x, ids, w, None)
+        self.server.reply_job(job, output.data_ptr(), stream.cuda_stream)
+        return ids.shape[0]
+
     @torch.no_grad()
     def run_job(self, job) -> None:
         """Gate, expert call and reply of one job, all enqueued on the F stream."""
@@ -180,13 +204,10 @@ class FfnScheduler:
         self.server.gate(job, stream.cuda_stream)
         token = self.clock.start(stream) if self.clock is not None else None
         with torch.cuda.stream(stream):
-            x, ids, w = self._inputs(job)
-            out = self.server.seg_view(job.rows[0]) if len(job.rows) == 1 else None
-            output = self._experts(job.layer_id, x, ids, w, out)
-            self.server.reply_job(job, output.data_ptr(), stream.cuda_stream)
+            n = self._run_row(job, stream) if len(job.rows) == 1 else self._run_rows(job, stream)
         self.layer_calls[job.layer_id] += 1
         if token is not None:
-            self.clock.stop(token, ids.shape[0], stream)
+            self.clock.stop(token, n, stream)
 
     def serve_pending(self) -> int:
         """Poll once and run every complete job (the one-GPU form of serve_forever)."""

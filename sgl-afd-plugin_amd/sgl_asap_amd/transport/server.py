@@ -230,6 +230,10 @@ class FfnServer:
         seg = self.peers[row.a].segments[off : off + row.n_tokens * g.hidden * 2]
         return seg.view(torch.bfloat16).view(row.n_tokens, g.hidden)
 
+    def seg_ptr(self, row: Row) -> int:
+        """Device address of A rank row.a's result segment for this F rank and the row's slot."""
+        return self.peers[row.a].segments.data_ptr() + self.g.seg_off(self.f, row.slot) - self.g.flags_bytes
+
     def reply_job(self, job: Job, output_ptr: int, stream: int) -> None:
         """Answer every row of ``job`` in one ``afd_reply``: the row's slice of the job output
         (bf16 [sum n_tokens, hidden] at ``output_ptr``, rows in order) goes to the A rank's
@@ -245,7 +249,7 @@ class FfnServer:
                 self.stats["dropped_replies"] += 1
             else:
                 d = descs[used]
-                d.src, d.dst = output_ptr + offset, self.seg_view(row).data_ptr()
+                d.src, d.dst = output_ptr + offset, self.seg_ptr(row)
                 d.bytes = nbytes
                 d.done = peer.flags.addr(g.done_off(self.f, row.slot))
                 d.value = row.seq
