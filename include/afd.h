@@ -19,6 +19,9 @@
  *   afd_moe_ffn_job / .......... the graph runner's replay (P/srt/model_executor/runner/
  *   afd_job_set                  ffn_cuda_graph_runner.py:75-92) with the job read from a
  *                                device descriptor instead of copied into static inputs
+ *   afd_moe_ffn_answer ......... the expert call followed by FfnServer.reply's done flag
+ *                                (P/srt/managers/scheduler.py:410-412, P/transport/server.py
+ *                                :340-350), the flag stored by the call's last workgroup
  *   afd_moe_ffn_q .............. the expert call on activations quantized before the arena
  *                                copy (the reference's TODO, scripts/run_asap.sh:110-111)
  *   afd_finalize ............... the finalize (top-k weighted sum, do_finalize=True,
@@ -208,6 +211,20 @@ int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const
 int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint8_t* xq,
                   const void* xs, const int32_t* ids, const float* w, int32_t n, void* ws,
                   uint64_t ws_bytes, uint16_t* out, afd_stream_t stream);
+
+/* The expert call of a served job with its reply folded in: afd_moe_ffn (x != NULL, xq = xs =
+ * NULL) or afd_moe_ffn_q (x = NULL, xq / xs), writing out (normally the asking rank's result
+ * segment), then *done := value, stored by the last workgroup of the call's final launch once
+ * every output row is visible device-wide, with system-scope release (so a stream or a host
+ * waiting on a host-memory *done sees the output). Replaces, for a job whose output lands in
+ * place, the expert call at P/srt/managers/scheduler.py:410-412 followed by the done flag of
+ * FfnServer.reply (P/transport/server.py:340-350), without the separate stream store. done:
+ * 8-byte aligned, pinned host or device memory; with n = 0 it is a stream store. The call's
+ * workspace must not be shared with a call on another stream that overlaps it. */
+int afd_moe_ffn_answer(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                       const uint16_t* x, const uint8_t* xq, const void* xs, const int32_t* ids,
+                       const float* w, int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
+                       uint64_t* done, uint64_t value, afd_stream_t stream);
 
 /* The expert call without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid

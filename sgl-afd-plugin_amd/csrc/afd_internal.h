@@ -37,6 +37,19 @@ __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   return j;
 }
 
+// The reply an expert call can carry (afd_moe_ffn_answer): once every output row of the call
+// is visible device-wide, *done := value, stored by the last workgroup of the finalize launch
+// to finish. arrive counts the finished workgroups; the routing launch of the same call zeroes
+// it. done == nullptr: no reply.
+struct Reply {
+  uint64_t* done;
+  uint64_t value;
+  uint32_t* arrive;
+};
+// Where a call's arrive counter lives: the word 128 bytes into the workspace's num_tiles slot
+// (the slot is padded to 256 bytes and num_tiles uses the first 4).
+constexpr uint64_t kArriveOffset = 128;
+
 // Activation quantization as the expert call applies it (MXFP8 with stage-order scales, or
 // FP8 1x128, by cfg.weight_fmt) into q / s.
 int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
@@ -46,8 +59,10 @@ int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8
 // of job.x into ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs
 // beside the expert histogram (without, the rows are quantized already). `mid` (optional)
 // is recorded between the two launches.
+// `arrive` (optional): a reply's arrive counter, zeroed by the first launch.
 int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
-                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid);
+                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid,
+                       uint32_t* arrive = nullptr);
 
 // Grouped MXFP4 GEMMs (afd_gemm_mx.hip).
 // xq / xs: the quantized activation rows [n][H] and their scales (the workspace's, or the

@@ -45,18 +45,17 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 constexpr int kFinThreads = 256;
 constexpr int kFinElems = 8;  // bf16 per lane = one 16-byte vector
 
-__global__ __launch_bounds__(kFinThreads) void finalize_kernel(
-    const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos, JobIn jin, int k,
-    int hidden, int col_blocks) {
+// One (token, column block) item: out[tok, col .. col + 7]. kWriteThrough: the 16 bytes go out
+// with the system-scope cache bits, which write them through the L2 to memory, so they are
+// visible device-wide once acknowledged.
+template <bool kWriteThrough>
+__device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
+                                              const int32_t* __restrict__ pair_pos,
+                                              const float* __restrict__ w,
+                                              uint16_t* __restrict__ out, int64_t tok, int col,
+                                              int k, int hidden) {
   // products and sums round separately: no contraction of w * y + acc into an fma
 #pragma clang fp contract(off)
-  const JobIn job = resolve_job(jin);
-  if (int64_t(blockIdx.x) >= job.n * col_blocks) return;  // past a descriptor's job
-  const float* __restrict__ w = job.w;
-  uint16_t* __restrict__ out = job.out;
-  const int64_t tok = blockIdx.x / col_blocks;
-  const int col = ((blockIdx.x % col_blocks) * kFinThreads + threadIdx.x) * kFinElems;
-  if (col >= hidden) return;
   float acc[kFinElems];
 #pragma unroll
   for (int i = 0; i < kFinElems; ++i) acc[i] = 0.0f;
@@ -94,17 +93,63 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     o[i] = static_cast<int>(pk_bf16(acc[2 * i], acc[2 * i + 1]));
-  *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
+  if constexpr (kWriteThrough) {
+    // one 16-byte vector store per lane (a wavefront writes 1 KiB of whole lines), with the
+    // system-scope cache bits; the caller waits for its acknowledgement
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(out + tok * hidden + col), "v"(o)
+                 : "memory");
+  } else {
+    *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
+  }
+}
+
+// Workgroups stride over the job's (token, column block) items (one item each when the grid
+// covers them; with a descriptor, items past the job's tokens are skipped). With a reply, the
+// grid is a few workgroups per CU; their output stores write through to memory, and each
+// workgroup, once all its stores are acknowledged, counts itself in reply.arrive (one atomic
+// per workgroup, no cache write-back); the last to arrive stores the reply value (system
+// scope), so a stream waiting on *reply.done (host memory) runs after every output row is in
+// memory.
+template <bool kReply>
+__global__ __launch_bounds__(kFinThreads) void finalize_kernel(
+    const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos, JobIn jin, int k,
+    int hidden, int col_blocks, Reply reply) {
+  const JobIn job = resolve_job(jin);
+  const uint32_t items = static_cast<uint32_t>(job.n) * static_cast<uint32_t>(col_blocks);
+  for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const uint32_t tok = item / static_cast<uint32_t>(col_blocks);
+    const int col = static_cast<int>((item - tok * col_blocks) * kFinThreads + threadIdx.x) * kFinElems;
+    if (col < hidden) finalize_item<kReply>(y, pair_pos, job.w, job.out, tok, col, k, hidden);
+  }
+  if constexpr (kReply) {
+    wait_vmcnt<0>();  // this lane's output stores are acknowledged (written through)
+    __syncthreads();  // and every lane's of the workgroup
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(reply.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            gridDim.x - 1)
+      __hip_atomic_store(reply.done, reply.value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
 }
 
 // one workgroup per (token, column block) of job.n tokens (with a descriptor: of n_cap, the
-// ones past the job's tokens return at once)
+// ones past the job's tokens do nothing); with a reply, at most kReplyGroupsPerCu workgroups
+// per CU
+constexpr int kReplyGroupsPerCu = 4;
 static int launch_finalize(const uint16_t* y, const int32_t* pair_pos, const JobIn& job,
-                           int32_t k, int32_t hidden, hipStream_t stream) {
+                           int32_t k, int32_t hidden, const Reply& reply, hipStream_t stream) {
   if (job.n == 0) return AFD_OK;
   const int col_blocks = (hidden / kFinElems + kFinThreads - 1) / kFinThreads;
-  hipLaunchKernelGGL(finalize_kernel, dim3(static_cast<unsigned>(col_blocks * job.n)),
-                     dim3(kFinThreads), 0, stream, y, pair_pos, job, k, hidden, col_blocks);
+  const int64_t items = col_blocks * job.n;
+  if (reply.done != nullptr) {
+    const int64_t cap = int64_t(kReplyGroupsPerCu) * device_cu_count();
+    hipLaunchKernelGGL(finalize_kernel<true>, dim3(static_cast<unsigned>(items < cap ? items : cap)),
+                       dim3(kFinThreads), 0, stream, y, pair_pos, job, k, hidden, col_blocks,
+                       reply);
+  } else {
+    hipLaunchKernelGGL(finalize_kernel<false>, dim3(static_cast<unsigned>(items)),
+                       dim3(kFinThreads), 0, stream, y, pair_pos, job, k, hidden, col_blocks,
+                       reply);
+  }
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }
@@ -250,7 +295,8 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
 // x, which is quantized here.
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                         const JobIn& job, bool quantized, const uint8_t* xq, const void* xs,
-                        void* ws, uint64_t ws_bytes, afd_stream_t stream, void* const* ev) {
+                        void* ws, uint64_t ws_bytes, afd_stream_t stream, void* const* ev,
+                        uint64_t* done = nullptr, uint64_t done_value = 0) {
   if (job.n < 0 || job.n > 0x1ffff) return AFD_ERR_ARG;
   const int32_t n = static_cast<int32_t>(job.n);
   afd_ws_layout L;
@@ -275,8 +321,10 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
     // routing and the activation quantization (one launch beside the expert histogram), then
     // the pair scatter; stage mark 1 falls between the two launches
+    const Reply reply{done, done_value,
+                      done ? reinterpret_cast<uint32_t*>(wsb + L.num_tiles + kArriveOffset) : nullptr};
     st = launch_route_quant(job, !quantized, *cfg, wsb, L, s,
-                            ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
+                            ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr, reply.arrive);
     if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
     const uint8_t* aq = quantized ? xq : wsb + L.xq;
@@ -290,11 +338,12 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     if (st != AFD_OK || (st = mark(4)) != AFD_OK) return st;
     st = launch_finalize(reinterpret_cast<const uint16_t*>(wsb + L.y),
                          reinterpret_cast<const int32_t*>(wsb + L.pair_pos), job, cfg->topk,
-                         cfg->hidden, s);
+                         cfg->hidden, reply, s);
     if (st != AFD_OK) return st;
   } else {
     for (int i = 1; i < 5; ++i)
       if ((st = mark(i)) != AFD_OK) return st;
+    if (done) AFD_CHECK_HIP(hipStreamWriteValue64(s, done, done_value, 0));
   }
   return mark(5);
 }
@@ -353,6 +402,18 @@ extern "C" int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* w
   return moe_ffn_impl(cfg, weights, job, true, xq, xs, ws, ws_bytes, stream, nullptr);
 }
 
+extern "C" int afd_moe_ffn_answer(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                                  const uint16_t* x, const uint8_t* xq, const void* xs,
+                                  const int32_t* ids, const float* w, int32_t n, void* ws,
+                                  uint64_t ws_bytes, uint16_t* out, uint64_t* done,
+                                  uint64_t value, afd_stream_t stream) {
+  if (!done || (reinterpret_cast<uintptr_t>(done) & 7) != 0) return AFD_ERR_ARG;
+  if ((x == nullptr) == (xq == nullptr)) return AFD_ERR_ARG;  // exactly one activation form
+  const JobIn job{nullptr, x, ids, w, out, n};
+  return moe_ffn_impl(cfg, weights, job, x == nullptr, xq, xs, ws, ws_bytes, stream, nullptr,
+                      done, value);
+}
+
 extern "C" int afd_moe_ffn_job(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                                const afd_job* job, int32_t n_cap, int32_t quantized, void* ws,
                                uint64_t ws_bytes, afd_stream_t stream) {
@@ -400,7 +461,8 @@ extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const fl
   if (n > 0 && (!y || !pair_pos || !w || !out)) return AFD_ERR_ARG;
   if (hidden <= 0 || hidden % kFinElems) return AFD_ERR_SHAPE;
   const JobIn job{nullptr, nullptr, nullptr, w, out, n};
-  return launch_finalize(y, pair_pos, job, k, hidden, static_cast<hipStream_t>(stream));
+  return launch_finalize(y, pair_pos, job, k, hidden, Reply{nullptr, 0, nullptr},
+                         static_cast<hipStream_t>(stream));
 }
 
 extern "C" int afd_combine(const uint16_t* const* parts, int32_t num_parts,

@@ -47,6 +47,7 @@ EXPORTED = (
     "afd_route",
     "afd_moe_ffn",
     "afd_moe_ffn_q",
+    "afd_moe_ffn_answer",
     "afd_moe_ffn_noalloc",
     "afd_moe_ffn_job",
     "afd_job_set",
@@ -197,6 +198,11 @@ _SIGS = {
     "afd_job_set": ([_P, ctypes.POINTER(AfdJob), _P], _I32),
     "afd_moe_ffn_q": (
         [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _P, _I32, _P, _U64, _P, _P],
+        _I32,
+    ),
+    "afd_moe_ffn_answer": (
+        [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _P, _P, _I32, _P, _U64, _P, _P,
+         _U64, _P],
         _I32,
     ),
     "afd_moe_ffn_profiled": (

@@ -6,11 +6,12 @@ Wires the pieces the reference runs in separate processes (``AsapBuffer.connect`
 
     AsapMoE.forward -> AsapDispatcher.dispatch -> AttnChannel.send   (A send stream)
         copies x / ids / w into the RecvArena, rings the doorbell
-    [shared experts on the compute stream]
-    AsapDispatcher.combine -> AsapBuffer.recv
         pump: FfnServer.poll -> FfnScheduler.run_job                (F stream)
             gates on the doorbell, runs the experts into A's result segment, stores the
-            message's count into A's done counter (afd_reply)
+            message's count into A's done counter
+    [shared experts on the compute stream]
+    AsapDispatcher.combine -> AsapBuffer.recv
+        pump again (serves whatever is still pending)
         AttnChannel.wait (compute stream: done counter >= count) -> afd_combine (+ shared)
 
 Every wait is enqueued after the work that satisfies it (host order equals causal order),

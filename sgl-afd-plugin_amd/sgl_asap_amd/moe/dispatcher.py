@@ -18,9 +18,11 @@ With fp8 activations on the wire (the channel geometry's ``act``) ``send`` quant
 rows on the send stream first (``quant_act``, the expert call's own quantizer) and copies the
 e4m3 codes and their scales: half the bytes of bf16, and the F rank skips its quantizer.
 
-On one GPU the F rank is in-process: ``AsapBuffer.pump`` (if set) is called before a wait
-is enqueued so the F side has enqueued its job first, which keeps host order equal to causal
-order on the device (no stream can ever wait on work that is enqueued after it).
+On one GPU the F rank is in-process: ``AsapBuffer.pump`` (if set) stands in for the F rank's
+poll loop. It runs right after every send, so the F side enqueues a job as soon as its message
+is enqueued (as a separate F process polling its doorbells would pick it up), and again before
+a wait is enqueued, which keeps host order equal to causal order on the device (no stream can
+ever wait on work that is enqueued after it).
 """
 
 from __future__ import annotations
@@ -150,6 +152,8 @@ class AsapBuffer:
             x_ptr, xs_ptr = q.data_ptr(), s.data_ptr()
         ticket = self.channel.send(layer_id, slot, x_ptr, ids.data_ptr(), weights.data_ptr(), n, self.send_stream,
                                    xs_ptr=xs_ptr)
+        if self.pump is not None:
+            self.pump()
         # The caller keeps its own tensors alive until the answer (keepalive); tensors made
         # here by a conversion are registered with the send stream, so the caching allocator
         # does not hand their memory out before the copies ran.

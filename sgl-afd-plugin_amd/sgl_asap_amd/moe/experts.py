@@ -402,19 +402,26 @@ class AfdExperts(torch.nn.Module):
         return out
 
     def call_ptrs(self, n: int, x_ptr: int, xs_ptr: int, ids_ptr: int, w_ptr: int, out_ptr: int,
-                  stream: int) -> None:
+                  stream: int, done_ptr: int = 0, done_value: int = 0) -> None:
         """The expert call on raw device pointers, enqueued on ``stream`` (a hipStream_t): bf16
         rows at x_ptr (xs_ptr = 0), or the e4m3 rows and their scales of quant_act; int32 ids and
         fp32 weights [n, k]; bf16 output [n, H]. For the serving loop, whose rows are arena
-        records: no tensor is made. The caller guarantees the sizes (``n`` <= n_max) and the
-        lifetimes; the C entry points check the configuration and the pointers."""
+        records: no tensor is made. With ``done_ptr`` the call also answers the job
+        (afd_moe_ffn_answer): the 64-bit word there becomes ``done_value`` once the output is
+        visible, stored by the call's last workgroup. The caller guarantees the sizes
+        (``n`` <= n_max) and the lifetimes; the C entry points check the configuration and the
+        pointers."""
         if not 0 < n <= self.n_max:
             raise ValueError(f"{n} tokens outside [1, n_max={self.n_max}]")
         ws = self._ws.get(stream)
         if ws is None:
             ws = torch.empty(self.layout["total"], dtype=torch.uint8, device=self.weights.w13.device)
             self._ws[stream] = ws
-        if xs_ptr:
+        if done_ptr:
+            _lib.call("afd_moe_ffn_answer", ctypes.byref(self.cfg), ctypes.byref(self._wstruct),
+                      None if xs_ptr else x_ptr, x_ptr if xs_ptr else None, xs_ptr or None, ids_ptr, w_ptr,
+                      n, ws.data_ptr(), ws.numel(), out_ptr, done_ptr, done_value, stream)
+        elif xs_ptr:
             _lib.call("afd_moe_ffn_q", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), x_ptr, xs_ptr, ids_ptr,
                       w_ptr, n, ws.data_ptr(), ws.numel(), out_ptr, stream)
         else:

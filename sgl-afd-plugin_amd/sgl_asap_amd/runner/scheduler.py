@@ -7,11 +7,15 @@ Plays the part of ``FfnScheduler`` in ``python/sgl_asap_plugin/srt/managers/sche
 Design on one GPU: everything a job does is stream-ordered on one F stream, enqueued by
 ``run_job`` without any host wait:
 
-    gate on the rows' doorbells -> expert call (a HIP-graph replay, or eager above the largest
-    bucket) -> afd_reply (copies if any, then the done counters)
+    gate on the rows' doorbells -> expert call -> reply (copies if any, then the done counters)
 
 A job of one row (the normal case, one attention rank per replica) writes its output straight
-into that rank's result segment, so its reply is only the done counter. A job of several rows
+into that rank's result segment, so its reply is only the done counter, which the eager expert
+call stores itself (afd_moe_ffn_answer). The expert call is one C call that enqueues the whole
+job (five launches); HIP graphs of it (``graph_max_tokens``, the reference runner's buckets)
+are available, but on this stack a replay costs more host time (~60 vs ~35 µs per job) and
+~14 µs more GPU time (a gap after each graph launch plus the descriptor write) than the eager
+call, so the default is eager. A job of several rows
 (a group of A ranks per replica) computes into a buffer that the reply copies from on the
 same stream, so one output buffer is enough and its memory is never handed out while a copy
 still reads it. With fp8 activations on the wire (``Geometry.act``) the rows arrive as e4m3
@@ -175,17 +179,21 @@ class FfnScheduler:
 
     def _run_row(self, job, stream) -> int:
         """A job of one row (one A rank per replica): the expert call reads the arena record
-        and writes A's result segment through raw pointers (a graph replay, or the eager call
-        above the largest bucket), so no tensor is made on the way. Returns n."""
+        and writes A's result segment through raw pointers, so no tensor is made on the way.
+        The eager call also stores the reply (its last workgroup writes A's done counter once
+        the output is visible), so the F stream needs no separate reply launch, which would
+        queue behind whatever occupies the CUs; a graph replay is answered by ``reply_job``.
+        Returns n."""
         row, g = job.rows[0], self.g
         n = row.n_tokens
         xs_ptr = row.x_ptr + g.xs_off if g.act != "bf16" else 0
         out_ptr = self.server.seg_ptr(row)
-        if self.graph_runner is None or not self.graph_runner.run_ptrs(
+        if self.graph_runner is not None and self.graph_runner.run_ptrs(
                 job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr):
+            self.server.reply_job(job, out_ptr, stream.cuda_stream)
+        else:
             self.experts[job.layer_id].call_ptrs(n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr,
-                                                 stream.cuda_stream)
-        self.server.reply_job(job, out_ptr, stream.cuda_stream)
+                                                 stream.cuda_stream, self.server.done_addr(row), row.seq)
         return n
 
     def _run_rows(self, job, stream) -> int:

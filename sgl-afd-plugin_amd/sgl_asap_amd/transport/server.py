@@ -4,7 +4,9 @@ the doorbell gate and the replies.
 The F rank's end of the connection (the role of ``python/sgl_asap_plugin/transport/server.py``):
 ``hello`` admits an A rank and hands out its epoch (``(old % 31) + 1``, :237), discovery turns
 doorbell words into ``Row`` / ``Job`` records (:47-81) under the reference's rules, and
-``reply_job`` answers a job (:340-350) with one ``afd_reply`` call.
+``reply_job`` answers a job (:340-350) with one ``afd_reply`` call (or, for a job whose output
+the expert call writes in place, ``done_addr`` hands the counter to that call, which stores it
+itself).
 
 Discovery, on one GPU: A's producer stream rings the doorbell in pinned host memory with a
 64-bit stream store, and ``AttnChannel.send`` also posts the same word to ``announce``. The
@@ -234,6 +236,15 @@ class FfnServer:
         """Device address of A rank row.a's result segment for this F rank and the row's slot."""
         return self.peers[row.a].segments.data_ptr() + self.g.seg_off(self.f, row.slot) - self.g.flags_bytes
 
+    def done_addr(self, row: Row) -> int:
+        """Address of the done counter whose store answers ``row``; 0 if the row's A rank
+        reconnected since the row was sent (the answer is dropped: ``dropped_replies``)."""
+        peer = self.peers.get(row.a)
+        if peer is None or peer.epoch != row.epoch:
+            self.stats["dropped_replies"] += 1
+            return 0
+        return peer.flags.addr(self.g.done_off(self.f, row.slot))
+
     def reply_job(self, job: Job, output_ptr: int, stream: int) -> None:
         """Answer every row of ``job`` in one ``afd_reply``: the row's slice of the job output
         (bf16 [sum n_tokens, hidden] at ``output_ptr``, rows in order) goes to the A rank's
@@ -244,14 +255,12 @@ class FfnServer:
         used, offset = 0, 0
         for row in job.rows:
             nbytes = row.n_tokens * g.hidden * 2
-            peer = self.peers.get(row.a)
-            if peer is None or peer.epoch != row.epoch:
-                self.stats["dropped_replies"] += 1
-            else:
+            done = self.done_addr(row)
+            if done:
                 d = descs[used]
                 d.src, d.dst = output_ptr + offset, self.seg_ptr(row)
                 d.bytes = nbytes
-                d.done = peer.flags.addr(g.done_off(self.f, row.slot))
+                d.done = done
                 d.value = row.seq
                 used += 1
             offset += nbytes
