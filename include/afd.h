@@ -60,7 +60,7 @@
 extern "C" {
 #endif
 
-#define AFD_ABI_VERSION 1
+#define AFD_ABI_VERSION 2
 
 typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
 
@@ -96,6 +96,18 @@ enum afd_activation {
                               FusedMoE (python/sgl_asap_plugin/srt/models/deepseek_v4.py:63) */
 };
 
+/* How the persistent GEMMs of the expert call hand out their output tiles. */
+enum afd_tile_walk {
+  AFD_WALK_STATIC = 0, /* a fixed share per workgroup: best when the call has the GPU's CUs to
+                          itself */
+  AFD_WALK_DYNAMIC = 1 /* taken in order from a per-XCD counter: when kernels of other
+                          streams or parked stream waits (HIP runs hipStreamWaitValue as a
+                          kernel) may hold CUs, a workgroup that starts late takes fewer tiles
+                          instead of adding a whole round (one parked wait slowed a static
+                          16384-token call by 38%, a dynamic one by <2%; on an idle GPU the
+                          counter costs 1-4%) */
+};
+
 /* Shape of one MoE layer on one F rank. Experts [expert_lo, expert_lo + num_local) are
  * local; top-k ids are global expert ids; pairs with other ids are skipped.
  * Limits: hidden a multiple of 256, inter a multiple of 128, num_local <= 256,
@@ -110,6 +122,7 @@ typedef struct afd_moe_cfg {
   int32_t activation; /* enum afd_activation (0: SwiGLU) */
   float act_alpha;    /* SiTU: A > 0 (unused otherwise) */
   float act_limit;    /* SiTU, SwiGLU with limit: L > 0 and finite (unused for SwiGLU) */
+  int32_t tile_walk;  /* enum afd_tile_walk (0: static) */
 } afd_moe_cfg;
 
 /* Packed expert weights of one layer (device pointers), as afd_pack_* writes them.

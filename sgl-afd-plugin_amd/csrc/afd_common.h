@@ -196,14 +196,23 @@ inline int walk_col_blocks(int ntn) {
   return (ntn + 32 / BR - 1) / (32 / BR);
 }
 
+// Tiles can also be handed out dynamically: one counter per XCD (one in all if the rows are
+// not split) counts the XCD's tiles in walk order with the holes left out (`at_dense`), and
+// one lane of a workgroup takes the next with an atomic increment (`claim_ticket`). The
+// tiles then stay on the XCD whose L2 shares their operands, while a workgroup that starts
+// late (its CU held by another kernel, e.g. a parked stream wait) takes fewer tiles instead
+// of adding a whole round at the end.
 template <int BR>
 struct TileWalk {
   static_assert(BR == 1 || BR == 2 || BR == 4 || BR == 8 || BR == 16 || BR == 32, "BR divides 32");
   static constexpr int kBC = 32 / BR;
   int mt0, rows_here, ntn, ncb, first, stride, count;
+  int tiles;  // rows_here * ntn: the dense positions of at_dense
   uint32_t ncb_magic;
-  // ncb_magic_ = div_magic(walk_col_blocks<BR>(ntn_))
-  __device__ __forceinline__ TileWalk(int rows, int ntn_, uint32_t ncb_magic_) {
+  uint32_t* ctr;
+  // ncb_magic_ = div_magic(walk_col_blocks<BR>(ntn_)); counters: 8 zeroed words for claim()
+  __device__ __forceinline__ TileWalk(int rows, int ntn_, uint32_t ncb_magic_,
+                                      uint32_t* counters = nullptr) {
     ntn = ntn_;
     ncb = (ntn_ + kBC - 1) / kBC;
     ncb_magic = ncb_magic_;
@@ -211,14 +220,44 @@ struct TileWalk {
     rows_here = rows;
     first = blockIdx.x;
     stride = gridDim.x;
+    ctr = counters;
     if ((gridDim.x & 7) == 0 && rows >= kWalkSplitRows) {
       const int xcd = blockIdx.x & 7;
       mt0 = (rows * xcd) >> 3;
       rows_here = ((rows * (xcd + 1)) >> 3) - mt0;
       first = blockIdx.x >> 3;
       stride = gridDim.x >> 3;
+      if (counters != nullptr) ctr = counters + xcd;
     }
     count = (rows_here + BR - 1) / BR * ncb * 32;
+    tiles = rows_here * ntn;
+  }
+  // the next dense position of this walk's counter, possibly past the last tile
+  // (global_atomic_inc with the largest limit is a plain increment); one lane calls it
+  __device__ __forceinline__ uint32_t claim_ticket() const {
+    return __builtin_amdgcn_atomic_inc32(ctr, 0xffffffffu, __ATOMIC_RELAXED, "agent");
+  }
+  // a claimed dense position, or `tiles` if it is past the last tile
+  __device__ __forceinline__ int resolve(uint32_t i) const {
+    return i < static_cast<uint32_t>(tiles) ? static_cast<int>(i) : tiles;
+  }
+  // The tile at dense position i < tiles: the i-th tile of at()'s order without its holes.
+  // Row blocks of BR row tiles (the last may have fewer, vr), in each, column blocks of kBC
+  // column tiles (the last may have fewer); inside a block, row tiles fastest.
+  __device__ __forceinline__ void at_dense(int i, int& mt, int& nt) const {
+    const int full = rows_here / BR;  // full row blocks
+    int rb, vr = BR, j = i;
+    if (i < full * BR * ntn) {
+      rb = i / (BR * ntn);
+      j = i - rb * BR * ntn;
+    } else {
+      rb = full;
+      vr = rows_here - full * BR;
+      j = i - full * BR * ntn;
+    }
+    const int cb = j / (vr * kBC), jj = j - cb * vr * kBC;
+    mt = mt0 + rb * BR + jj % vr;
+    nt = cb * kBC + jj / vr;
   }
   // the tile at walk position i; false for a hole
   __device__ __forceinline__ bool at(int i, int& mt, int& nt) const {

@@ -92,6 +92,7 @@ struct Fp8GemmArgs {
   const int32_t* num_tiles;       // [1]
   const int32_t* padded_offsets;  // [E + 1]
   const int32_t* counts;          // [E]
+  uint32_t* walk_ctr;             // [8] zeroed tile counters (one per XCD); nullptr: static walk
   int K, N;
   ActParams act;  // gate_up: the activation
   uint8_t* hq;  // gate_up out: e4m3 [np][N/2]
@@ -105,7 +106,8 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / 4, wn = w_u % 4, lr = lane & 31, lk = lane >> 5;
-  const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic);
+  const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  __shared__ int claimed[2];  // the claimed walk positions lane 0 publishes (as in the MX kernel)
   const int KT = p.K / kBK;
   const int nblk = p.N / kBK;  // weight scale blocks along N
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   int sp_next[kQX + 1], e_next = 0;
   auto load_next = [&](int ii) {
     int m, nn;
-    walk.at(ii, m, nn);
+    walk.at_dense(ii, m, nn);
     e_next = p.tile_expert[m];
     if constexpr (MODE != kDown) {
 #pragma unroll
@@ -222,28 +224,45 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     issue(min(1, last));
   };
 
-  int i = walk.begin();
-  if (i < walk.count) {
+  // The walk's dense positions: static, or with p.walk_ctr claimed one tile ahead by lane 0
+  // (the first two here, each later one during the last K stage of the tile before the one
+  // that needs it); see the MX kernel.
+  const bool dynamic = p.walk_ctr != nullptr;
+  int i = walk.first, i_next = walk.first + walk.stride;
+  if (dynamic) {
+    if (t == 0) {
+      const uint32_t a = walk.claim_ticket(), b = walk.claim_ticket();
+      claimed[0] = walk.resolve(a);
+      claimed[1] = walk.resolve(b);
+    }
+    __syncthreads();
+    i = __builtin_amdgcn_readfirstlane(claimed[0]);
+    i_next = __builtin_amdgcn_readfirstlane(claimed[1]);
+  }
+  i = min(i, walk.tiles);
+  i_next = min(i_next, walk.tiles);
+  uint32_t ticket = 0;  // lives across the tile loop (no write to its register waits for it)
+  if (i < walk.tiles) {
     load_next(i);
     decode_next();
     if constexpr (kEarlyStart) {
       int mt, nt;
-      walk.at(i, mt, nt);
+      walk.at_dense(i, mt, nt);
       copy_tile(mt, nt, e_cur);
       start_copies();
     }
   }
 
-  for (int i_next; i < walk.count; i = i_next) {
+  for (int i_after = walk.tiles; i < walk.tiles; i = i_next, i_next = i_after) {
     int mt, nt;
-    walk.at(i, mt, nt);
-    i_next = walk.next(i);
+    walk.at_dense(i, mt, nt);
+    const bool has_next = i_next < walk.tiles;
+    const bool claims = dynamic && t == 0 && has_next;  // publishes the tile after next
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = e_cur;
     // down: the expert's pairs fill its first rows; rows below row_end are real
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    const bool has_next = i_next < walk.count;
     if (has_next) load_next(i_next);
     if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
@@ -339,6 +358,8 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     __syncthreads();
     if (wm == 0) {
       for (int kt = 0; kt < KT; ++kt) {
+        // the claim rides on the last stage, whose end waits for every copy anyway
+        if (claims && kt == last) ticket = walk.claim_ticket();
         issue(min(kt + 2, last));
         read_stage(kt);
         wait_vmcnt_lds<2 * kPieces>();  // own reads done (copies may be in flight)
@@ -377,12 +398,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
         for (int q = 0; q < 16; ++q) acc[i2][j][q] *= sl;
       }
     wait_vmcnt<0>();  // every copy of this tile landed
+    if (claims) claimed[0] = walk.resolve(ticket);
     __syncthreads();  // and every wavefront is done reading the stages
     if (has_next) {
+      i_after = dynamic ? __builtin_amdgcn_readfirstlane(claimed[0])
+                        : min(i_next + walk.stride, walk.tiles);
       decode_next();
       if constexpr (kEarlyStart) {
         int mt2, nt2;
-        walk.at(i_next, mt2, nt2);
+        walk.at_dense(i_next, mt2, nt2);
         copy_tile(mt2, nt2, e_cur);
         start_copies();
       }
@@ -539,6 +563,7 @@ int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uin
   p.rows_desc = rows_desc;
   p.b = static_cast<const uint8_t*>(wt.w13);
   p.bs = static_cast<const float*>(wt.s13);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kGateUpWalkWord : nullptr;
   p.K = cfg.hidden;
   p.N = 2 * cfg.inter;
   p.hq = ws + L.hq;
@@ -556,6 +581,7 @@ int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_
   p.rows_desc = nullptr;
   p.b = static_cast<const uint8_t*>(wt.w2);
   p.bs = static_cast<const float*>(wt.s2);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kDownWalkWord : nullptr;
   p.K = cfg.inter;
   p.N = cfg.hidden;
   p.y = reinterpret_cast<uint16_t*>(ws + L.y);

@@ -50,6 +50,7 @@ struct MxGemmArgs {
   const int32_t* num_tiles;     // [1]
   const int32_t* padded_offsets;  // [E + 1] first padded row of each expert
   const int32_t* counts;          // [E] pairs of each expert (its first rows)
+  uint32_t* walk_ctr;             // [8] zeroed tile counters (one per XCD); nullptr: static walk
   int K, N;
   uint8_t* h_img;  // gate_up out: the down GEMM's A images [row tiles][N/256]
   ActParams act;   // gate_up: the activation
@@ -106,7 +107,10 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
   const int nt256 = p.N / kImgBRows;
-  const TileWalk<kMxWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic);
+  const TileWalk<kMxWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  // lane 0 claims the walk's dense positions (the tile after next, one tile ahead) and
+  // publishes them here; every wavefront reads them after a barrier
+  __shared__ int claimed[2];
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   const uint32_t voff = static_cast<uint32_t>(lane) * 16;
@@ -133,7 +137,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   int sp_next[T::kQP + 1], e_next = 0, own_next = -1;
   auto load_next = [&](int ii) {
     int m, nn;
-    walk.at(ii, m, nn);
+    walk.at_dense(ii, m, nn);
     e_next = p.tile_expert[m];
     own_next = p.sorted_pairs[m * kBM + 64 * wm + lane];
     if constexpr (MODE != kDown) {
@@ -212,29 +216,50 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   };
   const int last = KT - 1;
 
-  int i = walk.begin();
-  if (i < walk.count) {
+  // The walk's dense positions: static (this workgroup's first, first + stride, ...) or,
+  // with p.walk_ctr, claimed one tile ahead by lane 0 from its XCD's counter (the first two
+  // here, each later one during the last K stage of the tile before the one that needs it).
+  const bool dynamic = p.walk_ctr != nullptr;
+  int i = walk.first, i_next = walk.first + walk.stride;
+  if (dynamic) {
+    if (t == 0) {
+      // two increments in flight together (b > a, so b is past the last tile if a is)
+      const uint32_t a = walk.claim_ticket(), b = walk.claim_ticket();
+      claimed[0] = walk.resolve(a);
+      claimed[1] = walk.resolve(b);
+    }
+    __syncthreads();
+    i = __builtin_amdgcn_readfirstlane(claimed[0]);
+    i_next = __builtin_amdgcn_readfirstlane(claimed[1]);
+  }
+  i = min(i, walk.tiles);
+  i_next = min(i_next, walk.tiles);
+  // (`ticket` lives across the tile loop, so no write to its register waits for the
+  // increment; an increment, which the compiler's atomic combining leaves alone, so nothing
+  // waits for its result before the use)
+  uint32_t ticket = 0;
+  if (i < walk.tiles) {
     load_next(i);
     decode_next();
     if constexpr (kEarlyStart) {
       int mt, nt;
-      walk.at(i, mt, nt);
+      walk.at_dense(i, mt, nt);
       copy_tile(mt, nt, e_cur);
       issue(0);
       issue(min(1, last));
     }
   }
-  for (int i_next; i < walk.count; i = i_next) {
+  for (int i_after = walk.tiles; i < walk.tiles; i = i_next, i_next = i_after) {
     int mt, nt;
-    walk.at(i, mt, nt);
-    i_next = walk.next(i);
+    walk.at_dense(i, mt, nt);
+    const bool has_next = i_next < walk.tiles;
+    const bool claims = dynamic && t == 0 && has_next;  // publishes the tile after next
     const int m0 = mt * kBM, n0 = nt * kBN;
     const int64_t e = e_cur;
     // down: the expert's pairs fill its first rows, padding the rest; rows below row_end are
     // real (loaded now, used by the epilogue)
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    const bool has_next = i_next < walk.count;
     // 32-row blocks i of this group with a real row
     const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
     if (has_next) load_next(i_next);
@@ -326,6 +351,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     __syncthreads();
     if (wm == 0) {
       for (int kt = 0; kt < KT; ++kt) {
+        // the claim rides on the last stage, whose end waits for every copy anyway
+        if (claims && kt == last) ticket = walk.claim_ticket();
         issue(min(kt + 2, last));
         read_stage(kt % kStages);
         wait_vmcnt_lds<2 * T::kPieces>();  // own reads done (copies may be in flight)
@@ -355,12 +382,15 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       }
     }
     wait_vmcnt<0>();  // every copy of this tile landed
+    if (claims) claimed[0] = walk.resolve(ticket);
     __syncthreads();  // and every wavefront is done reading the stages
     if (has_next) {
+      i_after = dynamic ? __builtin_amdgcn_readfirstlane(claimed[0])
+                        : min(i_next + walk.stride, walk.tiles);
       decode_next();
       if constexpr (kEarlyStart) {
         int mt2, nt2;
-        walk.at(i_next, mt2, nt2);
+        walk.at_dense(i_next, mt2, nt2);
         copy_tile(mt2, nt2, e_cur);
         issue(0);
         issue(min(1, last));
@@ -520,6 +550,7 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
   p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
   p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kGateUpWalkWord : nullptr;
   p.K = cfg.hidden;
   p.N = 2 * cfg.inter;
   p.h_img = ws + L.hq;
@@ -545,6 +576,7 @@ int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
   p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
   p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kDownWalkWord : nullptr;
   p.K = cfg.inter;
   p.N = cfg.hidden;
   p.h_img = nullptr;

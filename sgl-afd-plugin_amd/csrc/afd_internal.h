@@ -37,18 +37,25 @@ __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   return j;
 }
 
+// Counter words of one call, in the workspace's num_tiles slot (padded to 256 bytes; num_tiles
+// is word 0): the routing launch zeroes words [kCounterWord0, kCounterWord0 + kCounterWords)
+// before any later launch of the call uses them.
+constexpr int kCounterWord0 = 8, kCounterWords = 32;
+constexpr int kGateUpWalkWord = 8;  // the gate_up GEMM's tile counters, one per XCD
+constexpr int kDownWalkWord = 16;   // the down GEMM's
+constexpr int kArriveWord = 32;     // the reply's arrive counter
+inline uint32_t* call_counters(uint8_t* ws, const afd_ws_layout& L) {
+  return reinterpret_cast<uint32_t*>(ws + L.num_tiles);
+}
+
 // The reply an expert call can carry (afd_moe_ffn_answer): once every output row of the call
 // is visible device-wide, *done := value, stored by the last workgroup of the finalize launch
-// to finish. arrive counts the finished workgroups; the routing launch of the same call zeroes
-// it. done == nullptr: no reply.
+// to finish. arrive counts the finished workgroups. done == nullptr: no reply.
 struct Reply {
   uint64_t* done;
   uint64_t value;
   uint32_t* arrive;
 };
-// Where a call's arrive counter lives: the word 128 bytes into the workspace's num_tiles slot
-// (the slot is padded to 256 bytes and num_tiles uses the first 4).
-constexpr uint64_t kArriveOffset = 128;
 
 // Activation quantization as the expert call applies it (MXFP8 with stage-order scales, or
 // FP8 1x128, by cfg.weight_fmt) into q / s.
@@ -59,10 +66,9 @@ int launch_quant_act(const afd_moe_cfg& cfg, const uint16_t* x, int32_t n, uint8
 // of job.x into ws.xq / ws.xs (MXFP8 in stage order, or FP8 1x128, by cfg.weight_fmt) runs
 // beside the expert histogram (without, the rows are quantized already). `mid` (optional)
 // is recorded between the two launches.
-// `arrive` (optional): a reply's arrive counter, zeroed by the first launch.
+// The first launch also zeroes the call's counter words.
 int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
-                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid,
-                       uint32_t* arrive = nullptr);
+                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid);
 
 // Grouped MXFP4 GEMMs (afd_gemm_mx.hip).
 // xq / xs: the quantized activation rows [n][H] and their scales (the workspace's, or the

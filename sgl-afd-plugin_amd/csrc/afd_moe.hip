@@ -226,6 +226,7 @@ static int check_cfg(const afd_moe_cfg* cfg) {
     return AFD_ERR_ARG;
   if (cfg->activation == AFD_ACT_SWIGLU_LIMIT && !(cfg->act_limit > 0.0f && cfg->act_limit < INFINITY))
     return AFD_ERR_ARG;
+  if (cfg->tile_walk != AFD_WALK_STATIC && cfg->tile_walk != AFD_WALK_DYNAMIC) return AFD_ERR_ARG;
   return AFD_OK;
 }
 
@@ -321,10 +322,9 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
     // routing and the activation quantization (one launch beside the expert histogram), then
     // the pair scatter; stage mark 1 falls between the two launches
-    const Reply reply{done, done_value,
-                      done ? reinterpret_cast<uint32_t*>(wsb + L.num_tiles + kArriveOffset) : nullptr};
+    const Reply reply{done, done_value, done ? call_counters(wsb, L) + kArriveWord : nullptr};
     st = launch_route_quant(job, !quantized, *cfg, wsb, L, s,
-                            ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr, reply.arrive);
+                            ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
     if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
     const uint8_t* aq = quantized ? xq : wsb + L.xq;

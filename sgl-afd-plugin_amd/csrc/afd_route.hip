@@ -40,9 +40,9 @@ struct PrepQuant {
 template <int QUANT>
 __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
     JobIn jin, int topk, int chunk, int chunks, int e_lo, int num_local,
-    int32_t* __restrict__ hist, PrepQuant pq, uint32_t* __restrict__ arrive) {
+    int32_t* __restrict__ hist, PrepQuant pq, uint32_t* __restrict__ counters) {
   const JobIn job = resolve_job(jin);
-  if (arrive != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *arrive = 0u;
+  if (blockIdx.x == 0 && threadIdx.x < kCounterWords) counters[kCounterWord0 + threadIdx.x] = 0u;
   if (static_cast<int>(blockIdx.x) >= chunks) {
     const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
     const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;
@@ -224,8 +224,8 @@ void route_chunking(int64_t pairs, int* chunks, int* chunk) {
 }
 
 int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, uint8_t* ws,
-                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid,
-                       uint32_t* arrive) {
+                       const afd_ws_layout& L, hipStream_t stream, hipEvent_t mid) {
+  uint32_t* counters = call_counters(ws, L);
   // grids for job.n tokens (with a descriptor: n_cap; chunks past the job's pairs are empty)
   const int64_t pairs = job.n * cfg.topk;
   int chunks, chunk;
@@ -239,13 +239,13 @@ int launch_route_quant(const JobIn& job, bool quantize, const afd_moe_cfg& cfg, 
     const dim3 grid(chunks + quant_grid);
     if (fmt == kPrepMxfp8)
       hipLaunchKernelGGL(route_prep_kernel<kPrepMxfp8>, grid, dim3(kRouteThreads), 0, stream, job,
-                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, arrive);
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, counters);
     else if (fmt == kPrepFp8)
       hipLaunchKernelGGL(route_prep_kernel<kPrepFp8>, grid, dim3(kRouteThreads), 0, stream, job,
-                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, arrive);
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, counters);
     else
       hipLaunchKernelGGL(route_prep_kernel<kPrepNone>, grid, dim3(kRouteThreads), 0, stream, job,
-                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, arrive);
+                         cfg.topk, chunk, chunks, cfg.expert_lo, cfg.num_local, hist, pq, counters);
     AFD_CHECK_LAUNCH();
   }
   if (mid) AFD_CHECK_HIP(hipEventRecord(mid, stream));

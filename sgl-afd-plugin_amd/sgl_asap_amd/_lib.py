@@ -31,6 +31,11 @@ AFD_ACT_SWIGLU_LIMIT = 2
 
 AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 
+AFD_WALK_STATIC, AFD_WALK_DYNAMIC = 0, 1
+
+# afd_abi_version() of the library these structures match
+ABI_VERSION = 2
+
 # Every entry point include/afd.h declares; tests check the library exports all of them.
 EXPORTED = (
     "afd_abi_version",
@@ -87,6 +92,7 @@ class AfdMoeCfg(ctypes.Structure):
         ("activation", ctypes.c_int32),
         ("act_alpha", ctypes.c_float),
         ("act_limit", ctypes.c_float),
+        ("tile_walk", ctypes.c_int32),
     ]
 
 
@@ -241,6 +247,11 @@ def lib() -> ctypes.CDLL:
                 for name, (args, res) in _SIGS.items():
                     fn = getattr(handle, name)
                     fn.argtypes, fn.restype = args, res
+                if handle.afd_abi_version() != ABI_VERSION:
+                    raise ImportError(
+                        f"{LIB_PATH} has ABI version {handle.afd_abi_version()}, this binding "
+                        f"expects {ABI_VERSION}: rebuild it"
+                    )
                 _lib = handle
     return _lib
 

@@ -208,6 +208,8 @@ def moe_cfg(
     )
 
 
+TILE_WALKS = {"static": _lib.AFD_WALK_STATIC, "dynamic": _lib.AFD_WALK_DYNAMIC}
+
 # activation formats of the expert call's input -> the weight format whose GEMMs read them
 ACT_FORMATS = {"mxfp8": "mxfp4", "fp8_1x128": "fp8_block"}
 
@@ -303,6 +305,11 @@ class AfdExperts(torch.nn.Module):
     ``activation``, ``gemm1_alpha`` and ``gemm1_clamp_limit`` are FusedMoE's (see
     ``moe_cfg``); ``swiglu_limit`` is DeepSeek-V4's FusedMoE argument, the clamp limit of
     its SwiGLU (P/srt/models/deepseek_v4.py:63).
+
+    ``tile_walk`` (no counterpart in the reference): "static" gives each GEMM workgroup a
+    fixed share of the tiles, best when the call has the GPU to itself; "dynamic" hands them
+    out from per-XCD counters, for a GPU shared with other streams' kernels or parked stream
+    waits (the FFN scheduler's setting). Results are identical bit for bit.
     """
 
     def __init__(
@@ -317,6 +324,7 @@ class AfdExperts(torch.nn.Module):
         gemm1_alpha: Optional[float] = None,
         gemm1_clamp_limit: Optional[float] = None,
         swiglu_limit: Optional[float] = None,
+        tile_walk: str = "static",
     ):
         super().__init__()
         if swiglu_limit is not None:  # DeepSeek-V4's FusedMoE argument: the SwiGLU clamp limit
@@ -334,9 +342,20 @@ class AfdExperts(torch.nn.Module):
         self.n_max = n_max
         self.activation = activation
         self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit)
+        self.tile_walk = tile_walk
         self.layout = workspace_layout(self.cfg, n_max)
         self._ws: Dict[int, torch.Tensor] = {}
         self._wstruct = weights.as_struct()
+
+    @property
+    def tile_walk(self) -> str:
+        return "dynamic" if self.cfg.tile_walk == _lib.AFD_WALK_DYNAMIC else "static"
+
+    @tile_walk.setter
+    def tile_walk(self, walk: str) -> None:
+        if walk not in TILE_WALKS:
+            raise ValueError(f"tile_walk must be one of {sorted(TILE_WALKS)}, got {walk!r}")
+        self.cfg.tile_walk = TILE_WALKS[walk]
 
     def workspace(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         """The workspace of ``stream`` (one per stream, so jobs on different streams can

@@ -109,6 +109,12 @@ class FfnScheduler:
         self.server, self.g = server, server.g
         self.experts = experts
         self.local = next(iter(experts.values())).local
+        # A serving GPU is shared: the attention side's kernels and its parked stream waits
+        # (a wait is a kernel on this stack) may hold CUs while a job runs, so the GEMMs take
+        # their tiles dynamically (identical results; a static share would leave a whole round
+        # to a workgroup that starts late).
+        for layer in experts.values():
+            layer.tile_walk = "dynamic"
         self.stream = torch.cuda.Stream()
         self.layer_calls: collections.Counter = collections.Counter()
         self.clock = JobClock() if timing else None

@@ -1,0 +1,88 @@
+"""GPU: the two tile walks of the persistent GEMMs give identical results. "dynamic" hands
+the tiles out from per-XCD counters, "static" gives each workgroup a fixed share; both run
+over the same dense tile order, so every output bit must agree, for both weight formats, for
+jobs from one token (8 row tiles, fewer than the 32 needed to split the rows over the XCDs)
+to thousands, for skewed routing, and while another stream holds a parked wait (a CU held by
+a wait kernel: the dynamic walk must still cover every tile)."""
+
+import time
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits16, dev, say
+from sgl_asap_amd import workloads as W
+from sgl_asap_amd.moe.experts import AfdExperts, pack_fp8_block_experts, pack_mxfp4_experts
+from sgl_asap_amd.moe.topk import StandardTopKOutput
+from sgl_asap_amd.transport import hip
+
+pytestmark = pytest.mark.gpu
+
+PACK = {"mxfp4": pack_mxfp4_experts, "fp8_block": pack_fp8_block_experts}
+
+
+def layer(fmt, hidden, inter, num_local, n_max, seed=0):
+    gen = W.generator("cpu", seed)
+    w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
+    return AfdExperts(num_local, 8, 0, range(0, num_local), PACK[fmt](w13, w2, device=dev()), n_max=n_max)
+
+
+def job(n, hidden, num_experts, seed, zipf=None):
+    gen = W.generator("cpu", seed)
+    x = W.tokens(n, hidden, gen, "cpu").to(dev())
+    if zipf:
+        ids, w = W.route_zipf(n, num_experts, 8, zipf, gen, "cpu")
+    else:
+        ids, w = W.route_uniform(n, num_experts, 8, gen, "cpu")
+    return x, StandardTopKOutput(w.to(torch.float32).to(dev()), ids.to(torch.int32).to(dev()))
+
+
+def both(experts, x, topk):
+    outs = []
+    for walk in ("static", "dynamic"):
+        experts.tile_walk = walk
+        outs.append(bits16(experts(x, topk)))
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_walks_agree(fmt):
+    experts = layer(fmt, 1024, 512, 32, 4096)
+    for n, seed, zipf in ((1, 1, None), (7, 2, None), (300, 3, None), (4096, 4, None), (3000, 5, 1.2)):
+        say(f"walks fmt={fmt} n={n} zipf={zipf}")
+        x, topk = job(n, 1024, 32, seed, zipf)
+        s, d = both(experts, x, topk)
+        assert np.array_equal(s, d), (fmt, n, seed)
+
+
+def test_dynamic_walk_with_a_parked_wait():
+    say("walks: a parked stream wait holds a CU during dynamic and static calls")
+    experts = layer("mxfp4", 1024, 512, 32, 4096)
+    x, topk = job(4096, 1024, 32, 9)
+    ref = both(experts, x, topk)[0]
+    page = hip.HostPage(4096)
+    other = torch.cuda.Stream()
+    try:
+        for walk in ("dynamic", "static"):
+            experts.tile_walk = walk
+            page.store(0, 0)
+            other.wait_stream(torch.cuda.current_stream())
+            hip.wait64(other.cuda_stream, page.addr(0), 1)  # parked until the host stores 1
+            out = experts(x, topk)
+            done = torch.cuda.Event()
+            done.record()
+            # the call normally finishes while the wait is parked; the host releases the wait
+            # after at most 10 s in any case (were the two streams on one hardware queue, the
+            # call would queue behind the wait), so nothing can hang
+            deadline = time.monotonic() + 10.0
+            while not done.query() and time.monotonic() < deadline:
+                time.sleep(0.001)
+            page.store(0, 1)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits16(out), ref), walk
+    finally:
+        page.store(0, 1)
+        torch.cuda.synchronize()
+        page.release()
