@@ -136,9 +136,13 @@ class AsapBuffer:
         if x.dtype != torch.bfloat16:
             raise TypeError(f"ASAP carries bf16 activations, got {x.dtype}")
         given = (x, ids, weights)
-        x = x.contiguous()
-        ids = ids.to(torch.int32).contiguous()
-        weights = weights.to(torch.float32).contiguous()
+        # conversions only where needed (each torch call costs host time even as a no-op)
+        if not x.is_contiguous():
+            x = x.contiguous()
+        if ids.dtype != torch.int32 or not ids.is_contiguous():
+            ids = ids.to(torch.int32).contiguous()
+        if weights.dtype != torch.float32 or not weights.is_contiguous():
+            weights = weights.to(torch.float32).contiguous()
         slot = SLOT if micro_batch is None else micro_batch
         n = x.shape[0]
         self._inputs_ready.record()

@@ -194,12 +194,15 @@ class FfnScheduler:
         n = row.n_tokens
         xs_ptr = row.x_ptr + g.xs_off if g.act != "bf16" else 0
         out_ptr = self.server.seg_ptr(row)
-        if self.graph_runner is not None and self.graph_runner.run_ptrs(
-                job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr):
-            self.server.reply_job(job, out_ptr, stream.cuda_stream)
-        else:
-            self.experts[job.layer_id].call_ptrs(n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr,
-                                                 stream.cuda_stream, self.server.done_addr(row), row.seq)
+        if self.graph_runner is not None:
+            with torch.cuda.stream(stream):  # a replay runs on the current stream
+                replayed = self.graph_runner.run_ptrs(job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr,
+                                                      row.w_ptr, out_ptr)
+            if replayed:
+                self.server.reply_job(job, out_ptr, stream.cuda_stream)
+                return n
+        self.experts[job.layer_id].call_ptrs(n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr,
+                                             stream.cuda_stream, self.server.done_addr(row), row.seq)
         return n
 
     def _run_rows(self, job, stream) -> int:
@@ -217,8 +220,11 @@ class FfnScheduler:
         stream = self.stream
         self.server.gate(job, stream.cuda_stream)
         token = self.clock.start(stream) if self.clock is not None else None
-        with torch.cuda.stream(stream):
-            n = self._run_row(job, stream) if len(job.rows) == 1 else self._run_rows(job, stream)
+        if len(job.rows) == 1:
+            n = self._run_row(job, stream)  # raw pointers on the F stream: no torch op
+        else:
+            with torch.cuda.stream(stream):
+                n = self._run_rows(job, stream)
         self.layer_calls[job.layer_id] += 1
         if token is not None:
             self.clock.stop(token, n, stream)

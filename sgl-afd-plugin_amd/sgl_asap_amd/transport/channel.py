@@ -248,14 +248,21 @@ class AttnChannel:
         d.xs, d.xs_bytes = (xs_ptr or None), n_tokens * g.xs_bytes_per_token
         d.ids, d.w, d.ids_bytes = ids_ptr, w_ptr, n_tokens * g.topk * ID_BYTES
         d.done_min = seq - 1
+        pending = False  # some F rank has not answered the slot's previous message yet
         for f in range(g.num_f):
             epoch = self._epochs[f] if self._epoch_override is None else self._epoch_override
             d.word[f] = pack_doorbell(seq, n_tokens, layer_id, epoch)
+            if self._backpressure:
+                # an answer the host already sees needs no wait on the GPU (the wait is a
+                # kernel there, which may have to queue for a free CU)
+                answered = self.flags.load(g.done_off(f, slot)) >= seq - 1
+                d.done[f] = None if answered else self._done_addrs[slot][f]
+                pending = pending or not answered
         hip.send(d, stream.cuda_stream)
         self._count[slot] = seq
         for f, server in enumerate(self.servers):
             server.announce(self.a, slot, d.word[f])
-        if self._backpressure and seq - 1 > self.seq_base:
+        if pending:
             for f in range(g.num_f):
                 self.watch.expect(g.done_off(f, slot), seq - 1, f"send of layer {layer_id} slot {slot} #{seq}")
         return Ticket(slot, seq, layer_id, n_tokens)
