@@ -66,6 +66,11 @@ CASES = [
     (777, 32, 256, 0, 256, 8),
     (131071, 8, 256, 0, 64, 9),  # the largest job a doorbell announces: 1M pairs, 128 chunks
     (131071, 1, 256, 0, 256, 10),
+    # more small-job shapes: 8192 pairs, one more, all 256 experts local, one local expert
+    (1024, 8, 256, 0, 64, 11),
+    (1025, 8, 256, 0, 64, 12),
+    (200, 32, 256, 0, 256, 13),
+    (500, 3, 16, 5, 1, 14),
 ]
 
 
