@@ -241,7 +241,8 @@ def bench_stream(args) -> dict:
     arriving from 2 A replicas x 2 micro-batches (round robin) through the one-GPU transport
     into the F scheduler, served with one eager expert call per job (the default) and, for
     comparison, with HIP graphs for every power-of-two bucket up to 16384 tokens. Timed: first
-    send to the last reply landing, after one untimed pass of the same stream."""
+    send to the last reply landing, after one untimed pass of the same stream, which also
+    collects the per-job GPU times (job_clock)."""
     import torch
 
     from sgl_asap_amd import workloads as W
@@ -296,9 +297,9 @@ def bench_stream(args) -> dict:
                 for r, t in tickets:
                     afd.channels[r].wait(t, main)
 
-        run()
+        run()  # untimed, with the per-job clock (two event records per job)
         torch.cuda.synchronize()
-        afd.scheduler.clock = type(afd.scheduler.clock)()  # time the measured pass only
+        clock, afd.scheduler.clock = afd.scheduler.clock, None  # the timed pass records nothing
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         h0 = time.perf_counter()
         e0.record(main)
@@ -307,6 +308,7 @@ def bench_stream(args) -> dict:
         host_ms = (time.perf_counter() - h0) * 1e3
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1)
+        afd.scheduler.clock = clock
         out[mode] = {
             "ms": round(ms, 3),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
