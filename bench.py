@@ -44,6 +44,8 @@ def parse():
                     "A<->F loop with a shared expert, 2 micro-batches per layer")
     ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
     ap.add_argument("--jobs", type=int, default=32, help="stream: jobs in the stream")
+    ap.add_argument("--f-streams", type=int, default=None,
+                    help="stream / loop: F streams the eager jobs alternate over (default: the loop's)")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
@@ -203,6 +205,10 @@ def _mxfp4_layer(W, shape, dev, n_max, seed=1):
     return AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n_max)
 
 
+def _f_streams(args) -> dict:
+    return {} if getattr(args, "f_streams", None) is None else {"f_streams": args.f_streams}
+
+
 def small_jobs(W, shape, dev, sizes=(256, 512, 1024, 2048)) -> list:
     """Single small jobs of the stream's shape through the eager expert call: at these sizes
     the layer is bound by streaming the touched experts' weights from HBM. Compulsory bytes =
@@ -278,7 +284,8 @@ def bench_stream(args) -> dict:
     for mode, graph_max in (("graphs", n_max), ("eager", 0)):
         experts = {0: _mxfp4_layer(W, shape, dev, n_max)}
         t0 = time.perf_counter()
-        afd = OneGpuAfd(experts, n_max=n_max, slots=2, replicas=2, graph_max_tokens=graph_max, timing=True)
+        afd = OneGpuAfd(experts, n_max=n_max, slots=2, replicas=2, graph_max_tokens=graph_max, timing=True,
+                        **_f_streams(args))
         setup_s = time.perf_counter() - t0
         sends = [torch.cuda.Stream() for _ in range(2)]
         main = torch.cuda.current_stream()
@@ -364,7 +371,8 @@ def bench_loop(args) -> dict:
     main = torch.cuda.current_stream()
 
     def measure(act, graphs=False):
-        afd = OneGpuAfd(experts, n_max=n, slots=2, graph_max_tokens=n if graphs else 0, act=act)
+        afd = OneGpuAfd(experts, n_max=n, slots=2, graph_max_tokens=n if graphs else 0, act=act,
+                        **_f_streams(args))
 
         def step():
             d = [layer.dispatcher.dispatch(x, t, micro_batch=m) for m, (x, t) in enumerate(mbs)]

@@ -4,8 +4,9 @@ Plays the part of ``FfnScheduler`` in ``python/sgl_asap_plugin/srt/managers/sche
 ``local_experts`` (:206-218), ``warmup`` (:329-351), ``run_job`` (:387-436), ``rows_of``
 (:438-450) and the per-job timing of its ``JobTimer`` (:109-159).
 
-Design on one GPU: everything a job does is stream-ordered on one F stream, enqueued by
-``run_job`` without any host wait:
+Design on one GPU: everything a job does is stream-ordered on one F stream (jobs in turn over
+one stream per job that can be in flight, so concurrent jobs overlap), enqueued by ``run_job``
+without any host wait:
 
     gate on the rows' doorbells -> expert call -> reply (copies if any, then the done counters)
 
@@ -105,7 +106,7 @@ class FfnScheduler:
     """Serves the jobs an ``FfnServer`` discovers with the routed experts of every layer."""
 
     def __init__(self, server, experts: Dict[int, torch.nn.Module], *, graph_max_tokens: int = 0,
-                 timing: bool = False):
+                 timing: bool = False, streams: Optional[int] = None):
         self.server, self.g = server, server.g
         self.experts = experts
         self.local = next(iter(experts.values())).local
@@ -115,7 +116,19 @@ class FfnScheduler:
         # to a workgroup that starts late).
         for layer in experts.values():
             layer.tile_walk = "dynamic"
-        self.stream = torch.cuda.Stream()
+        # Eager jobs alternate over ``streams`` F streams (each with its own workspace): jobs
+        # in flight together run concurrently, each one's GEMMs taking the CUs that the
+        # others' partial last rounds leave idle (results are the same; the dynamic tile walk
+        # lets a late workgroup take fewer tiles). Default: one stream per job that can be in
+        # flight at once, replicas x slots. Graph replays share their captured buffers and
+        # stay on one stream.
+        if streams is None:
+            streams = max(1, self.g.num_a // self.g.group) * self.g.slots
+        if streams < 1:
+            raise ValueError(f"streams must be >= 1, got {streams}")
+        self.streams = [torch.cuda.Stream() for _ in range(1 if graph_max_tokens else streams)]
+        self.stream = self.streams[0]
+        self._turn = 0
         self.layer_calls: collections.Counter = collections.Counter()
         self.clock = JobClock() if timing else None
         self.graph_runner: Optional[FfnGraphRunner] = None
@@ -216,8 +229,10 @@ class FfnScheduler:
 
     @torch.no_grad()
     def run_job(self, job) -> None:
-        """Gate, expert call and reply of one job, all enqueued on the F stream."""
-        stream = self.stream
+        """Gate, expert call and reply of one job, all enqueued on one F stream (the next in
+        turn)."""
+        stream = self.streams[self._turn]
+        self._turn = (self._turn + 1) % len(self.streams)
         self.server.gate(job, stream.cuda_stream)
         token = self.clock.start(stream) if self.clock is not None else None
         if len(job.rows) == 1:

@@ -151,3 +151,40 @@ def test_stream_through_the_transport(stream_layer):
         assert afd.server.stats["jobs"] == 4
     for g, e, n in zip(got, eager, SIZES):
         assert np.array_equal(g, e), n
+
+
+@pytest.mark.parametrize("f_streams", [None, 1, 3])
+def test_stream_through_the_transport_eager_on_concurrent_f_streams(stream_layer, f_streams):
+    """The same four jobs, eager, served over F streams in turn (default: one per job in
+    flight, 2 replicas x 2 slots = 4, so the four run concurrently; 1; and 3, so the streams
+    rotate across passes), two passes enqueued back to back before any synchronization: every
+    answer equals the plain call's bit for bit."""
+    experts, _, jobs = stream_layer
+    say(f"C3: the four jobs through the transport, eager, f_streams={f_streams}, two passes")
+    eager = []
+    for x, ids, w in jobs:
+        eager.append(bits16(experts[0](x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))))
+    torch.cuda.synchronize()
+    order = [(r, mb) for r in range(2) for mb in range(2)]
+    kw = {} if f_streams is None else {"f_streams": f_streams}
+    with OneGpuAfd(experts, n_max=N_MAX, slots=2, replicas=2, **kw) as afd:
+        assert len(afd.scheduler.streams) == (4 if f_streams is None else f_streams)
+        main = torch.cuda.current_stream()
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        dev_jobs = [(x.to(dev()), ids.to(dev()), w.to(dev())) for x, ids, w in jobs]
+        copies = []
+        for _ in range(2):
+            for s in sends:
+                s.wait_stream(main)
+            tickets = []
+            for (r, mb), (x, ids, w) in zip(order, dev_jobs):
+                tickets.append((r, afd.channels[r].send(0, mb, x.data_ptr(), ids.data_ptr(), w.data_ptr(),
+                                                        x.shape[0], sends[r])))
+            afd.scheduler.serve_pending()
+            for r, t in tickets:
+                afd.channels[r].wait(t, main)
+                copies.append(afd.channels[r].result_view(0, t.slot, t.n_tokens).clone())
+        torch.cuda.synchronize()
+        assert afd.server.stats["jobs"] == 8
+    for i, c in enumerate(copies):
+        assert np.array_equal(bits16(c), eager[i % 4]), (i, SIZES[i % 4])
