@@ -116,33 +116,37 @@ class FfnScheduler:
         # to a workgroup that starts late).
         for layer in experts.values():
             layer.tile_walk = "dynamic"
-        # Eager jobs alternate over ``streams`` F streams (each with its own workspace): jobs
-        # in flight together run concurrently, each one's GEMMs taking the CUs that the
-        # others' partial last rounds leave idle (results are the same; the dynamic tile walk
-        # lets a late workgroup take fewer tiles). Default: one stream per job that can be in
-        # flight at once, replicas x slots. Graph replays share their captured buffers and
-        # stay on one stream.
+        # Jobs go to ``streams`` F streams in turn (each with its own workspace, and with
+        # graphs its own graph runner: workspace, descriptor and output buffers): jobs in
+        # flight together run concurrently, each one's GEMMs taking the CUs that the others'
+        # partial last rounds leave idle (results are the same; the dynamic tile walk lets a
+        # late workgroup take fewer tiles). Default: one stream per job that can be in flight
+        # at once, replicas x slots.
         if streams is None:
             streams = max(1, self.g.num_a // self.g.group) * self.g.slots
         if streams < 1:
             raise ValueError(f"streams must be >= 1, got {streams}")
-        self.streams = [torch.cuda.Stream() for _ in range(1 if graph_max_tokens else streams)]
+        self.streams = [torch.cuda.Stream() for _ in range(streams)]
         self.stream = self.streams[0]
         self._turn = 0
         self.layer_calls: collections.Counter = collections.Counter()
         self.clock = JobClock() if timing else None
-        self.graph_runner: Optional[FfnGraphRunner] = None
+        self.graph_runners: List[FfnGraphRunner] = []
         if graph_max_tokens:
-            with torch.cuda.stream(self.stream):
-                self.graph_runner = FfnGraphRunner(experts, graph_max_tokens, self.local, act=self.g.act)
+            for s in self.streams:
+                with torch.cuda.stream(s):
+                    self.graph_runners.append(
+                        FfnGraphRunner(experts, graph_max_tokens, self.local, act=self.g.act))
+        self.graph_runner: Optional[FfnGraphRunner] = self.graph_runners[0] if self.graph_runners else None
 
     @torch.no_grad()
     def warmup(self, n_max: int) -> list:
         """Run the expert call once at every graph-bucket size up to ``n_max`` on seeded
         inputs (the prefixes of one batch: x ~ N(0,1) bf16, k distinct experts per token drawn
         uniformly over all experts, weights ~ U(0,1)), on the first layer at every size and on
-        every other layer at the smallest size, so every kernel and every workspace has been
-        used before serving. Synchronizes; returns the sizes run."""
+        every other layer at the smallest size, on the first F stream; on every other F stream
+        each layer at the smallest size. So every kernel and every workspace has been used
+        before serving. Synchronizes; returns the sizes run."""
         order = sorted(self.experts)
         first = self.experts[order[0]]
         sizes = graph_buckets(n_max)
@@ -158,6 +162,11 @@ class FfnScheduler:
                 topk = StandardTopKOutput(w[:size], ids[:size])
                 for layer_id in (order if i == 0 else order[:1]):
                     self.experts[layer_id](x[:size], topk)
+        topk = StandardTopKOutput(w[: sizes[0]], ids[: sizes[0]])
+        for stream in self.streams[1:]:
+            with torch.cuda.stream(stream):
+                for layer_id in order:
+                    self.experts[layer_id](x[: sizes[0]], topk)
         torch.cuda.synchronize()
         return sizes
 
@@ -187,16 +196,16 @@ class FfnScheduler:
         x = tuple(torch.cat([p[0][i] for p in parts]) for i in range(len(parts[0][0])))
         return x, torch.cat([p[1] for p in parts]), torch.cat([p[2] for p in parts])
 
-    def _experts(self, layer_id: int, x: tuple, ids, w, out):
-        if self.graph_runner is not None:
-            result = self.graph_runner.run(layer_id, x, ids, w, 0, out=out)
+    def _experts(self, layer_id: int, x: tuple, ids, w, out, runner=None):
+        if runner is not None:
+            result = runner.run(layer_id, x, ids, w, 0, out=out)
             if result is not None:
                 return result
         layer = self.experts[layer_id]
         topk = StandardTopKOutput(w, ids)
         return layer(x[0], topk, out=out) if len(x) == 1 else layer.forward_q(*x, topk, out=out)
 
-    def _run_row(self, job, stream) -> int:
+    def _run_row(self, job, stream, runner) -> int:
         """A job of one row (one A rank per replica): the expert call reads the arena record
         and writes A's result segment through raw pointers, so no tensor is made on the way.
         The eager call also stores the reply (its last workgroup writes A's done counter once
@@ -207,10 +216,9 @@ class FfnScheduler:
         n = row.n_tokens
         xs_ptr = row.x_ptr + g.xs_off if g.act != "bf16" else 0
         out_ptr = self.server.seg_ptr(row)
-        if self.graph_runner is not None:
+        if runner is not None:
             with torch.cuda.stream(stream):  # a replay runs on the current stream
-                replayed = self.graph_runner.run_ptrs(job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr,
-                                                      row.w_ptr, out_ptr)
+                replayed = runner.run_ptrs(job.layer_id, n, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, out_ptr)
             if replayed:
                 self.server.reply_job(job, out_ptr, stream.cuda_stream)
                 return n
@@ -218,12 +226,12 @@ class FfnScheduler:
                                              stream.cuda_stream, self.server.done_addr(row), row.seq)
         return n
 
-    def _run_rows(self, job, stream) -> int:
+    def _run_rows(self, job, stream, runner) -> int:
         """A job of several rows: their records concatenated, the output in a buffer that the
         reply copies into each A rank's segment (same stream, so the buffer is free again
         before the next job writes it). Returns n."""
         x, ids, w = self._inputs(job)
-        output = self._experts(job.layer_id, x, ids, w, None)
+        output = self._experts(job.layer_id, x, ids, w, None, runner)
         self.server.reply_job(job, output.data_ptr(), stream.cuda_stream)
         return ids.shape[0]
 
@@ -231,15 +239,17 @@ class FfnScheduler:
     def run_job(self, job) -> None:
         """Gate, expert call and reply of one job, all enqueued on one F stream (the next in
         turn)."""
-        stream = self.streams[self._turn]
-        self._turn = (self._turn + 1) % len(self.streams)
+        turn = self._turn
+        self._turn = (turn + 1) % len(self.streams)
+        stream = self.streams[turn]
+        runner = self.graph_runners[turn] if self.graph_runners else None
         self.server.gate(job, stream.cuda_stream)
         token = self.clock.start(stream) if self.clock is not None else None
         if len(job.rows) == 1:
-            n = self._run_row(job, stream)  # raw pointers on the F stream: no torch op
+            n = self._run_row(job, stream, runner)  # raw pointers on the F stream: no torch op
         else:
             with torch.cuda.stream(stream):
-                n = self._run_rows(job, stream)
+                n = self._run_rows(job, stream, runner)
         self.layer_calls[job.layer_id] += 1
         if token is not None:
             self.clock.stop(token, n, stream)
