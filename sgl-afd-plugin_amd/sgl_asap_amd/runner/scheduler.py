@@ -47,24 +47,25 @@ def local_experts(ep_rank: int, ep_size: int, num_experts: int) -> range:
 class JobClock:
     """GPU and host time of every served job, grouped by the job's power-of-two size class.
 
-    ``start`` / ``stop`` bracket a job's GPU work with two timing events on the F stream and
-    note the host time spent enqueueing it; whether the F stream was idle when the job was
-    enqueued is recorded too (the previous job's end event had completed), since a job queued
-    behind another starts late. Records are resolved lazily: ``collect`` reads only those
+    ``start`` / ``stop`` bracket a job's GPU work with two timing events on the job's F stream
+    and note the host time spent enqueueing it; whether that stream was idle when the job was
+    enqueued is recorded too (the end event of the stream's previous job had completed), since
+    a job queued behind another starts late. Records are resolved lazily: ``collect`` reads only those
     whose end event the GPU has passed, so timing never synchronizes the serving loop."""
 
     def __init__(self, keep: int = 4096):
         self.keep = keep
         self._open: collections.deque = collections.deque()
         self._rows: Dict[int, List[tuple]] = collections.defaultdict(list)
-        self._last_end: Optional[torch.cuda.Event] = None
+        self._last_end: Dict[int, torch.cuda.Event] = {}  # per F stream
 
     @staticmethod
     def size_class(n_tokens: int) -> int:
         return 1 << max(0, n_tokens - 1).bit_length()
 
     def start(self, stream) -> tuple:
-        idle = self._last_end is None or self._last_end.query()
+        last = self._last_end.get(stream.cuda_stream)
+        idle = last is None or last.query()
         begin = torch.cuda.Event(enable_timing=True)
         begin.record(stream)
         return time.perf_counter(), idle, begin
@@ -73,7 +74,7 @@ class JobClock:
         t0, idle, begin = token
         end = torch.cuda.Event(enable_timing=True)
         end.record(stream)
-        self._last_end = end
+        self._last_end[stream.cuda_stream] = end
         self._open.append((self.size_class(n_tokens), idle, begin, end, time.perf_counter() - t0))
         self.collect()
 
