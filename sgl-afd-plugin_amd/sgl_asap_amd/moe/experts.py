@@ -258,6 +258,30 @@ def _quant_act(cfg, act, x, q, s, stream):
 
 JOB_BYTES = ctypes.sizeof(_lib.AfdJob)
 
+# Workspaces of the expert calls: one per (device, stream, size), shared by every layer whose
+# calls need that size. Calls on one stream run in order, so a model's MoE layers (which
+# usually share one size) use one buffer per stream instead of one each; calls on different
+# streams get different buffers and may overlap. A buffer is never reallocated, and a graph
+# runner keeps a workspace of its own, so pointers captured in HIP graphs stay valid.
+_WORKSPACES: Dict[tuple, torch.Tensor] = {}
+
+
+def stream_workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
+    """The shared workspace of ``nbytes`` for calls on the stream ``stream_handle``."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, int(stream_handle), int(nbytes))
+    ws = _WORKSPACES.get(key)
+    if ws is None:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", index))
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def release_workspaces() -> None:
+    """Drop every shared workspace (after the device has finished the calls that used them)."""
+    torch.cuda.synchronize()
+    _WORKSPACES.clear()
+
 
 def new_job_desc(device=None) -> torch.Tensor:
     """A zeroed device job descriptor (afd_job) for ``AfdExperts.call_job`` / ``set_job``."""
@@ -344,7 +368,6 @@ class AfdExperts(torch.nn.Module):
         self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit)
         self.tile_walk = tile_walk
         self.layout = workspace_layout(self.cfg, n_max)
-        self._ws: Dict[int, torch.Tensor] = {}
         self._wstruct = weights.as_struct()
 
     @property
@@ -358,14 +381,12 @@ class AfdExperts(torch.nn.Module):
         self.cfg.tile_walk = TILE_WALKS[walk]
 
     def workspace(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
-        """The workspace of ``stream`` (one per stream, so jobs on different streams can
-        overlap; calls on one stream are ordered and share it)."""
+        """The workspace of this layer's calls on ``stream`` (default: current): one per stream
+        and size, shared with the other layers of that size (``stream_workspace``), so jobs
+        on different streams can overlap while calls on one stream, which are ordered, share
+        it."""
         s = stream if stream is not None else torch.cuda.current_stream()
-        ws = self._ws.get(s.cuda_stream)
-        if ws is None:
-            ws = torch.empty(self.layout["total"], dtype=torch.uint8, device=self.weights.w13.device)
-            self._ws[s.cuda_stream] = ws
-        return ws
+        return stream_workspace(self.weights.w13.device, s.cuda_stream, self.layout["total"])
 
     def _topk(self, n: int, topk_output, device):
         if not format_is_standard(topk_output):
@@ -432,10 +453,7 @@ class AfdExperts(torch.nn.Module):
         pointers."""
         if not 0 < n <= self.n_max:
             raise ValueError(f"{n} tokens outside [1, n_max={self.n_max}]")
-        ws = self._ws.get(stream)
-        if ws is None:
-            ws = torch.empty(self.layout["total"], dtype=torch.uint8, device=self.weights.w13.device)
-            self._ws[stream] = ws
+        ws = stream_workspace(self.weights.w13.device, stream, self.layout["total"])
         if done_ptr:
             _lib.call("afd_moe_ffn_answer", ctypes.byref(self.cfg), ctypes.byref(self._wstruct),
                       None if xs_ptr else x_ptr, x_ptr if xs_ptr else None, xs_ptr or None, ids_ptr, w_ptr,
@@ -448,16 +466,21 @@ class AfdExperts(torch.nn.Module):
                       ws.data_ptr(), ws.numel(), out_ptr, stream)
 
     # ---- graph replay: the job is read from a device descriptor when the calls run ----
-    def call_job(self, desc: torch.Tensor, n_cap: int, quantized: bool = False) -> None:
+    def call_job(self, desc: torch.Tensor, n_cap: int, quantized: bool = False,
+                 ws: Optional[torch.Tensor] = None) -> None:
         """Enqueue the expert call on whatever job ``desc`` (from ``new_job_desc``) holds when
         it runs, up to ``n_cap`` tokens (afd_moe_ffn_job): bf16 rows, or with ``quantized``
         the xq / xs of ``quant_act``. Capture it in a HIP graph once, then ``set_job`` +
-        replay per job: no copies into static buffers, no work for tokens the job lacks."""
+        replay per job: no copies into static buffers, no work for tokens the job lacks.
+        ``ws``: the workspace (a graph runner's own; default: the current stream's)."""
         if not 0 <= n_cap <= self.n_max:
             raise ValueError(f"n_cap {n_cap} outside [0, n_max={self.n_max}]")
         if desc.dtype != torch.uint8 or desc.numel() != JOB_BYTES or not desc.is_cuda:
             raise ValueError(f"desc must be a device uint8 tensor of {JOB_BYTES} bytes")
-        ws = self.workspace()
+        if ws is None:
+            ws = self.workspace()
+        elif ws.dtype != torch.uint8 or ws.numel() < self.layout["total"] or not ws.is_contiguous():
+            raise ValueError(f"ws must be a contiguous uint8 tensor of at least {self.layout['total']} bytes")
         _lib.call(
             "afd_moe_ffn_job",
             ctypes.byref(self.cfg),

@@ -48,6 +48,9 @@ class FfnGraphRunner:
         self.quantized = act != "bf16"
         device = torch.cuda.current_device()
         self.desc = new_job_desc(device)  # n = 0 until the first job: a replay then does nothing
+        # the runner's own workspace (its graphs capture its pointer), large enough for every layer
+        self.ws = torch.empty(max(layer.layout["total"] for layer in experts.values()), dtype=torch.uint8,
+                              device=device)
         self.outs = [torch.zeros(max_tokens, hidden, dtype=torch.bfloat16, device=device) for _ in range(2)]
         self.graphs: Dict[tuple, torch.cuda.CUDAGraph] = {}
         tic = time.perf_counter()
@@ -57,11 +60,11 @@ class FfnGraphRunner:
             for layer_id, layer in experts.items():
                 stream.wait_stream(torch.cuda.current_stream())
                 with torch.cuda.stream(stream):  # first call outside the capture
-                    layer.call_job(self.desc, b, self.quantized)
+                    layer.call_job(self.desc, b, self.quantized, ws=self.ws)
                 torch.cuda.current_stream().wait_stream(stream)
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, pool=pool, stream=stream):
-                    layer.call_job(self.desc, b, self.quantized)
+                    layer.call_job(self.desc, b, self.quantized, ws=self.ws)
                 self.graphs[(layer_id, b)] = graph
         torch.cuda.synchronize()
         self.capture_s = time.perf_counter() - tic

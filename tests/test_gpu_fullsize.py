@@ -22,7 +22,7 @@ from gpu_util import bits16, dev, rel_l2, say
 from oracle import experts as OX
 from oracle import formats as F
 from sgl_asap_amd import workloads as W
-from sgl_asap_amd.moe.experts import AfdExperts, new_job_desc, pack_fp8_block_experts, pack_mxfp4_experts, set_job
+from sgl_asap_amd.moe.experts import AfdExperts, new_job_desc, pack_fp8_block_experts, pack_mxfp4_experts, set_job, release_workspaces
 from sgl_asap_amd.moe.topk import StandardTopKOutput
 
 pytestmark = pytest.mark.gpu
@@ -43,6 +43,7 @@ def layer(request):
     torch.cuda.synchronize()
     yield shape, experts, (w13, w2), (x, ids, w), job, out
     del experts
+    release_workspaces()  # the shared per-stream workspaces of this size
     torch.cuda.empty_cache()
 
 
@@ -159,4 +160,5 @@ def test_largest_job_rows_match_a_subset():
     sub = torch.cat([torch.arange(0, 1000), torch.arange(n - 1000, n)]).to(dev())
     assert np.array_equal(bits16(call(experts, x[sub], ids[sub], w[sub])), full[sub.cpu().numpy()])
     del experts
+    release_workspaces()  # the shared per-stream workspaces of this size
     torch.cuda.empty_cache()

@@ -24,7 +24,7 @@ from oracle import experts as OX
 from oracle import formats as F
 from sgl_asap_amd import workloads as W
 from sgl_asap_amd.loop import OneGpuAfd
-from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts
+from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts, release_workspaces
 from sgl_asap_amd.moe.layer import AsapMoE
 from sgl_asap_amd.moe.shared import SharedExpertMLP
 from sgl_asap_amd.moe.topk import StandardTopKOutput
@@ -81,6 +81,7 @@ def workload():
     torch.cuda.synchronize()
     yield experts, (w13, w2), shared, mbs
     del experts
+    release_workspaces()  # the shared per-stream workspaces of this size
     torch.cuda.empty_cache()
 
 

@@ -25,7 +25,7 @@ from oracle import formats as F
 from oracle import routing as R
 from sgl_asap_amd import workloads as W
 from sgl_asap_amd.loop import OneGpuAfd
-from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts
+from sgl_asap_amd.moe.experts import AfdExperts, pack_mxfp4_experts, release_workspaces
 from sgl_asap_amd.moe.topk import StandardTopKOutput
 from sgl_asap_amd.runner.graph_runner import FfnGraphRunner
 
@@ -51,6 +51,7 @@ def stream_layer():
     torch.cuda.synchronize()
     yield experts, (w13, w2), jobs
     del experts
+    release_workspaces()  # the shared per-stream workspaces of this size
     torch.cuda.empty_cache()
 
 
