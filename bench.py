@@ -322,6 +322,7 @@ def bench_stream(args) -> dict:
             "tokens_per_s": round(tokens / (ms * 1e-3), 1),
             "host_enqueue_ms": round(host_ms, 3),
             "setup_s": round(setup_s, 2),
+            "f_streams": len(afd.scheduler.streams),
             "jobs_per_bucket": {str(b): v["jobs"] for b, v in afd.scheduler.clock.summary().items()},
             "job_clock": afd.scheduler.clock.summary(),
         }
@@ -391,9 +392,11 @@ def bench_loop(args) -> dict:
             e1.record(main)
             torch.cuda.synchronize()
             lat.append(e0.elapsed_time(e1))
+        streams_used.append(len(afd.scheduler.streams))
         afd.close()
         return lat
 
+    streams_used = []
     # activations on the wire: bf16 (the reference's layout), then MXFP8 (A quantizes before
     # the copy; bit-identical outputs, half the copy bytes, no quantizer on the F side)
     lat_fp8 = measure("mxfp8")
@@ -431,6 +434,7 @@ def bench_loop(args) -> dict:
             "workload": f"dsv4_zipf loop: 2 micro-batches x {n} tokens, H={shape.hidden} I={shape.inter}, "
             f"{shape.num_local} local of {shape.num_experts} experts, top-{shape.top_k}, shared expert I={shared_i} bf16",
             "local_pairs": pairs,
+            "f_streams": streams_used[0],
         },
         "layer_latency_ms": round(ms, 4),
         "layer_latency_ms_min": round(min(lat), 4),

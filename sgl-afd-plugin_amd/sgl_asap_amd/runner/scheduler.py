@@ -158,6 +158,8 @@ class FfnScheduler:
         ids = torch.multinomial(torch.ones(n, first.num_experts, device=device), first.top_k,
                                 replacement=False, generator=gen).to(torch.int32)
         w = torch.rand(n, first.top_k, generator=gen, device=device)
+        for stream in self.streams:  # the inputs come from the current stream
+            stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(self.stream):
             for i, size in enumerate(sizes):
                 topk = StandardTopKOutput(w[:size], ids[:size])
