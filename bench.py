@@ -38,10 +38,12 @@ def parse():
     # the first ~25 layer calls after start-up run up to 45% slower while the GPU's clocks
     # settle: untimed calls before the warm-up steps, reported as settle_calls
     ap.add_argument("--settle-calls", type=int, default=40)
-    ap.add_argument("--workload", default="layer", choices=["layer", "stream", "loop"],
+    ap.add_argument("--workload", default="layer", choices=["layer", "stream", "loop", "vendor"],
                     help="layer: one expert call per step (default); stream: the skewed job stream "
                     "from 2 replicas x 2 micro-batches through the F scheduler; loop: the one-GPU "
-                    "A<->F loop with a shared expert, 2 micro-batches per layer")
+                    "A<->F loop with a shared expert, 2 micro-batches per layer; vendor: the vendor "
+                    "library's dense fp8 GEMM (torch._scaled_mm, hipBLASLt) at the layer's padded "
+                    "GEMM shapes, a ceiling to compare the grouped GEMMs with")
     ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
     ap.add_argument("--jobs", type=int, default=32, help="stream: jobs in the stream")
     ap.add_argument("--f-streams", type=int, default=None,
@@ -451,6 +453,61 @@ def bench_loop(args) -> dict:
     }
 
 
+def bench_vendor(args) -> dict:
+    """The vendor library's dense e4m3 x e4m3 GEMM (torch._scaled_mm on hipBLASLt, bf16 out,
+    per-tensor scales) at the config's two GEMM shapes with the expert call's padded row count
+    (every local expert's rows rounded up to 128): the same MFMA rate as the grouped W4A8 and
+    FP8 GEMMs, without their gather, routing and epilogues."""
+    import torch
+
+    from sgl_asap_amd import workloads as W
+
+    shape = W.SHAPES[args.config]
+    n = args.tokens or shape.tokens
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _, ids, _ = W.job(shape, n=n, seed=0, device=dev)
+    lo, hi = shape.local.start, shape.local.stop
+    local = ids[(ids >= lo) & (ids < hi)] - lo
+    counts = torch.bincount(local.flatten().long(), minlength=hi - lo)
+    padded = int(((counts + 127) // 128 * 128).sum())
+    out = {}
+    for name, (m, nn, k) in (("gate_up", (padded, 2 * shape.inter, shape.hidden)),
+                             ("down", (padded, shape.hidden, shape.inter))):
+        a = torch.randn(m, k, device=dev).to(torch.float8_e4m3fn)
+        b = torch.randn(nn, k, device=dev).to(torch.float8_e4m3fn)
+        one = torch.ones((), device=dev)
+
+        def mm():
+            return torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+
+        for _ in range(args.warmup):
+            mm()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            mm()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / args.steps
+        out[name] = {"m": m, "n": nn, "k": k, "us": round(us, 1), "tflops": round(2 * m * nn * k / us / 1e6, 1)}
+        del a, b
+    return {
+        "metric": "dense fp8 GEMM throughput of the vendor library at the expert call's GEMM shapes",
+        "value": out["gate_up"]["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "higher_is_better": True,
+        "dtype": "e4m3 x e4m3 -> bf16",
+        "data": "synthetic (N(0,1) operands)",
+        "config": {"workload": f"{args.config}: {padded} padded rows (torch._scaled_mm, hipBLASLt)"},
+        "gemms": out,
+    }
+
+
 def main():
     args = parse()
     if args.stats_summary:
@@ -475,6 +532,9 @@ def main():
         return
     if args.workload == "loop":
         print(json.dumps(bench_loop(args)), flush=True)
+        return
+    if args.workload == "vendor":
+        print(json.dumps(bench_vendor(args)), flush=True)
         return
 
     from sgl_asap_amd import _lib
