@@ -60,7 +60,9 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
 #pragma unroll
   for (int i = 0; i < kFinElems; ++i) acc[i] = 0.0f;
   // up to 8 pairs at a time: their positions, then their rows, are loaded together; the sum
-  // still runs over kk in ascending order
+  // still runs over kk in ascending order. y is read once, so its rows are loaded
+  // non-temporally (measured 4% faster at 2 local pairs per token, 12% at 8; the same hint
+  // on the streaming reads of the quantizer and the combine made those slower).
   constexpr int kBatch = 8;
   for (int k0 = 0; k0 < k; k0 += kBatch) {
     int pos[kBatch];
@@ -74,7 +76,7 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
     v4i raw[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j)
-      raw[j] = pos[j] >= 0 ? *reinterpret_cast<const v4i*>(y + int64_t(pos[j]) * hidden + col)
+      raw[j] = pos[j] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(y + int64_t(pos[j]) * hidden + col))
                            : v4i{0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
