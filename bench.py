@@ -394,11 +394,27 @@ def bench_loop(args) -> dict:
             e1.record(main)
             torch.cuda.synchronize()
             lat.append(e0.elapsed_time(e1))
+        # Chained layers: each step's micro-batch m dispatches the previous step's combine
+        # output of m (the data dependency of consecutive MoE layers; attention left out), with
+        # no host synchronization between the steps, as a serving loop runs them. The host
+        # enqueues ahead, so its latency hides behind the GPU work of the earlier layers.
+        xs = [x for x, _ in mbs]
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(main)
+        for _ in range(args.steps):
+            d = [layer.dispatcher.dispatch(xs[m], mbs[m][1], micro_batch=m) for m in range(2)]
+            afd.scheduler.serve_pending()
+            s = [shared(x) for x in xs]
+            xs = [layer.dispatcher.combine(d[m], s[m]) for m in range(2)]
+        e1.record(main)
+        torch.cuda.synchronize()
+        chained.append(e0.elapsed_time(e1) / args.steps)
         streams_used.append(len(afd.scheduler.streams))
         afd.close()
         return lat
 
-    streams_used = []
+    streams_used, chained = [], []
     # activations on the wire: bf16 (the reference's layout), then MXFP8 (A quantizes before
     # the copy; bit-identical outputs, half the copy bytes, no quantizer on the F side)
     lat_fp8 = measure("mxfp8")
@@ -440,6 +456,11 @@ def bench_loop(args) -> dict:
         },
         "layer_latency_ms": round(ms, 4),
         "layer_latency_ms_min": round(min(lat), 4),
+        # chained: ms per layer over the timed steps run as consecutive layers (each one's
+        # inputs are the previous one's outputs, no synchronization between them); in the
+        # order of the measures below (fp8 wire, bf16 wire, bf16 with graph replays)
+        "chained_ms_per_layer": {"mxfp8": round(chained[0], 4), "bf16": round(chained[1], 4),
+                                 "bf16_graphs": round(chained[2], 4)},
         "tokens_per_s": round(2 * n / (ms * 1e-3), 1),
         "tflops_routed_plus_shared": round((routed_flops + shared_flops) / (ms * 1e-3) / 1e12, 2),
         "combine": {"ms": round(comb_ms, 4), "bytes": comb_bytes,
