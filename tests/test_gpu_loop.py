@@ -89,6 +89,33 @@ def test_two_micro_batches_in_flight():
             assert np.array_equal(bits16(ob), direct(experts, lid, xb, tb))
 
 
+def test_chained_layers_without_synchronization():
+    """Consecutive layers as a serving loop runs them: each micro-batch's next send reads the
+    combine output of its previous layer (made on the compute stream, still in flight), the
+    slots are reused every layer, and nothing synchronizes until the end. Every layer's output
+    equals the expert call on the previous output, bit for bit."""
+    say("loop: 4 chained layers x 2 micro-batches, no host synchronization")
+    experts = make_experts(64, layers=(0, 1))
+    with OneGpuAfd(experts, n_max=64, slots=2) as afd:
+        layers = [AsapMoE(E, H, I, lid, top_k=K) for lid in (0, 1)]
+        starts = [job(40, 500), job(29, 501)]
+        xs = [x for x, _ in starts]
+        outs = []
+        for step in range(4):
+            layer = layers[step % 2]
+            d = [layer.dispatcher.dispatch(xs[m], starts[m][1], micro_batch=m) for m in range(2)]
+            xs = [layer.dispatcher.combine(d[m]) for m in range(2)]
+            outs.append(list(xs))
+        torch.cuda.synchronize()
+        ref = [x for x, _ in starts]
+        for step in range(4):
+            ref = [experts[step % 2](ref[m], starts[m][1]) for m in range(2)]
+            torch.cuda.synchronize()
+            for m in range(2):
+                assert np.array_equal(bits16(outs[step][m]), bits16(ref[m])), (step, m)
+        assert afd.server.stats["jobs"] == 8 and afd.server.stats["lost_messages"] == 0
+
+
 def test_sequence_wrap():
     say("loop: seq_base 2^32 - 3, eight messages across the wrap")
     experts = make_experts(64)
