@@ -4,9 +4,11 @@
 //   1. route_prep:    workgroup c < chunks histograms chunk c of the flat pair array by local
 //                     expert (LDS atomics; counts are order-free); with the expert call, the
 //                     remaining workgroups quantize the activations meanwhile (afd_quant_dev.h).
-//   2. route_scatter: workgroup c first reads the whole [chunks][E] histogram (it is in L2) to
-//                     get each expert's count, its own chunk's base per expert and the
-//                     block_m-padded expert offsets (a wavefront scan); workgroup 0 also writes
+//   2. route_scatter: workgroup c first reads the whole histogram (it is in L2; stored expert
+//                     by expert, [E][kMaxChunks], so each thread's run of chunk counts is a few
+//                     16-byte loads issued together) to get each expert's count, its own chunk's
+//                     base per expert and the block_m-padded expert offsets (a wavefront scan);
+//                     workgroup 0 also writes
 //                     counts, offsets, padded offsets, the row-tile table, the tile count and
 //                     the -1 fill of padding rows. It then walks its pairs in flat order, 256 at
 //                     a time; a pair's rank among equal keys inside its wavefront comes from 9
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
   }
   __syncthreads();
   for (int e = threadIdx.x; e < num_local; e += kRouteThreads)
-    hist[int64_t(blockIdx.x) * num_local + e] = cnt[e];
+    hist[int64_t(e) * kMaxChunks + blockIdx.x] = cnt[e];
 }
 
 __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
@@ -90,21 +92,30 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   const int c = blockIdx.x;
   const int64_t lo = int64_t(c) * chunk;
   const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
-  // the chunk's first 256 ids are loaded now, so their latency overlaps the histogram pass
-  const int id_first = lo + t < hi ? ids[lo + t] : 0;
+  // the chunk's first two batches of 256 ids are loaded now, so their latency overlaps the
+  // histogram pass; each later batch is loaded two batches ahead
+  int id_cur = lo + t < hi ? ids[lo + t] : 0;
+  int id_nxt = lo + kRouteThreads + t < hi ? ids[lo + kRouteThreads + t] : 0;
   // Expert e's chunks are split over G = kRouteThreads / num_local threads (e, g), each summing
-  // a contiguous run of them: the counts in all chunks and in the chunks before this one.
+  // a contiguous run of them (a multiple of 4 long, so 16-byte loads of the expert's row of the
+  // histogram; entries at or past `chunks` are never written and are masked): the counts in
+  // all chunks and in the chunks before this one.
   const int G = kRouteThreads / num_local;
-  const int per = (chunks + G - 1) / G;
+  const int per = ((chunks + G - 1) / G + 3) & ~3;
   const int e = t % num_local, g = t / num_local;
   const bool active = g < G;
   const int c0 = active ? g * per : 0, c1 = active ? min(c0 + per, chunks) : 0;
   int all = 0, before = 0;
-#pragma unroll 4
-  for (int k = c0; k < c1; ++k) {
-    const int h = hist[int64_t(k) * num_local + e];
-    all += h;
-    before += k < c ? h : 0;
+  const int32_t* hrow = hist + int64_t(e) * kMaxChunks;
+#pragma unroll 8
+  for (int k4 = c0; k4 < c1; k4 += 4) {
+    const v4i h = *reinterpret_cast<const v4i*>(hrow + k4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int v = k4 + j < c1 ? h[j] : 0;
+      all += v;
+      before += k4 + j < c ? v : 0;
+    }
   }
   part_all[t] = all;
   part_before[t] = before;
@@ -178,7 +189,9 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   for (int64_t base = lo; base < hi; base += kRouteThreads) {
     const int64_t i = base + t;
     const bool live = i < hi;
-    const int id = base == lo ? id_first : live ? ids[i] : 0;
+    const int id = id_cur;
+    id_cur = id_nxt;
+    id_nxt = i + 2 * kRouteThreads < hi ? ids[i + 2 * kRouteThreads] : 0;
     const int key = live ? pair_key(id, e_lo, num_local) : num_local;
     // lanes with the same key (dead lanes join the "not local" key and are ignored)
     uint64_t peers = __ballot(1);
