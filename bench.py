@@ -46,6 +46,10 @@ def parse():
                     "GEMM shapes, a ceiling to compare the grouped GEMMs with")
     ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
     ap.add_argument("--jobs", type=int, default=32, help="stream: jobs in the stream")
+    ap.add_argument("--batch-tokens", type=int, default=32768,
+                    help="stream: token capacity of the scheduler's batched expert calls in the "
+                         "'batched' pass (the jobs of one poll packed into calls of at most this "
+                         "many tokens)")
     ap.add_argument("--f-streams", type=int, default=None,
                     help="stream / loop: F streams the eager jobs alternate over (default: the loop's)")
     ap.add_argument("--tokens", type=int, default=None)
@@ -283,11 +287,11 @@ def bench_stream(args) -> dict:
             "job_tokens": sizes,
         },
     }
-    for mode, graph_max in (("graphs", n_max), ("eager", 0)):
+    for mode, graph_max, batch in (("graphs", n_max, 0), ("eager", 0, 0), ("batched", 0, args.batch_tokens)):
         experts = {0: _mxfp4_layer(W, shape, dev, n_max)}
         t0 = time.perf_counter()
         afd = OneGpuAfd(experts, n_max=n_max, slots=2, replicas=2, graph_max_tokens=graph_max, timing=True,
-                        **_f_streams(args))
+                        batch_tokens=batch, **_f_streams(args))
         setup_s = time.perf_counter() - t0
         sends = [torch.cuda.Stream() for _ in range(2)]
         main = torch.cuda.current_stream()
@@ -325,6 +329,8 @@ def bench_stream(args) -> dict:
             "host_enqueue_ms": round(host_ms, 3),
             "setup_s": round(setup_s, 2),
             "f_streams": len(afd.scheduler.streams),
+            "expert_calls_per_pass": afd.scheduler.expert_calls // 2,
+            "batch_tokens": batch,
             "jobs_per_bucket": {str(b): v["jobs"] for b, v in afd.scheduler.clock.summary().items()},
             "job_clock": afd.scheduler.clock.summary(),
         }

@@ -60,7 +60,7 @@
 extern "C" {
 #endif
 
-#define AFD_ABI_VERSION 2
+#define AFD_ABI_VERSION 3
 
 typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
 
@@ -238,6 +238,36 @@ int afd_moe_ffn_answer(const afd_moe_cfg* cfg, const afd_expert_weights* weights
                        const uint16_t* x, const uint8_t* xq, const void* xs, const int32_t* ids,
                        const float* w, int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
                        uint64_t* done, uint64_t value, afd_stream_t stream);
+
+/* One job of a batched expert call: x bf16 [n][H], ids i32 [n][k], w f32 [n][k], out bf16
+ * [n][H]; done: NULL, or an 8-byte aligned counter (pinned host or device memory) that the
+ * call sets to `value` once this job's output rows are visible device-wide. */
+#define AFD_MAX_BATCH 8
+typedef struct afd_batch_job {
+  const uint16_t* x;
+  const int32_t* ids;
+  const float* w;
+  uint16_t* out;
+  uint64_t* done;
+  uint64_t value;
+  int32_t n;
+  int32_t reserved; /* 0 */
+} afd_batch_job;
+
+/* One expert call over up to AFD_MAX_BATCH jobs of the same layer, as if their tokens were
+ * one job: the routing, both GEMMs and the finalize run once over the concatenated tokens
+ * (each expert's weights stream once for all the jobs, and its rows from different jobs share
+ * row tiles), while every job reads its own x, ids and w and gets its own out. Each job's out
+ * equals afd_moe_ffn on that job alone, bit for bit (a token's output depends on its own row
+ * only). ws_bytes from afd_workspace_layout(cfg, sum of n), at most 131071 tokens in all. If
+ * any job has a done counter, every job's counter is stored by the last workgroup of the
+ * call's final launch (as afd_moe_ffn_answer does), after all the jobs' rows are visible.
+ * Extends the FFN rank's per-job expert call (P/srt/managers/scheduler.py:410-412), which
+ * concatenates the rows of one job's A ranks, to jobs of several replicas and slots that are
+ * pending together. */
+int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                      const afd_batch_job* jobs, int32_t num_jobs, void* ws, uint64_t ws_bytes,
+                      afd_stream_t stream);
 
 /* The expert call without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid

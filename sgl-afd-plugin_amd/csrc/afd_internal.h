@@ -11,11 +11,14 @@ namespace afd {
 constexpr int kMaxLocalExperts = 256;
 constexpr int kMaxTopk = 32;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
+constexpr int kMaxBatch = AFD_MAX_BATCH;  // jobs of one batched call
 
 
 // Where a launch finds its job: the fields by value, or (desc != nullptr) read from the job
 // descriptor in device memory when the kernel runs, its n then clamped to [0, n], n being
-// here the n_cap the grids and the workspace were sized for.
+// here the n_cap the grids and the workspace were sized for. A batch (batch > 1) is one call
+// over several jobs: job b holds the call's tokens [first[b], first[b + 1]) and its rows are
+// read and written through bx[b], bids[b], bw[b] and bout[b]; n is the total.
 struct JobIn {
   const afd_job* desc;
   const uint16_t* x;
@@ -23,7 +26,43 @@ struct JobIn {
   const float* w;
   uint16_t* out;
   int64_t n;
+  int32_t batch;
+  int32_t first[kMaxBatch + 1];
+  const uint16_t* bx[kMaxBatch];
+  const int32_t* bids[kMaxBatch];
+  const float* bw[kMaxBatch];
+  uint16_t* bout[kMaxBatch];
 };
+
+// Row `t` of a batch's per-job arrays `ptrs` (rows of row_elems elements; `unit` = 1 for
+// token rows, k for the flat pair index of ids / w). The selects are unrolled, so every index
+// into the tables is a constant and they stay in scalar registers.
+template <typename T>
+__device__ __forceinline__ T* batch_row(const JobIn& j, T* const (&ptrs)[kMaxBatch], int64_t t,
+                                        int64_t row_elems, int unit = 1) {
+  T* p = ptrs[0];
+  int64_t base = 0;
+#pragma unroll
+  for (int b = 1; b < kMaxBatch; ++b)
+    if (b < j.batch && t >= int64_t(j.first[b]) * unit) {
+      p = ptrs[b];
+      base = int64_t(j.first[b]) * unit;
+    }
+  return p + (t - base) * row_elems;
+}
+// token t's x row, its out row, and the id / weight of flat pair i (= t * k + kk)
+__device__ __forceinline__ const uint16_t* job_x_row(const JobIn& j, int64_t t, int cols) {
+  return j.batch > 1 ? batch_row(j, j.bx, t, cols) : j.x + t * cols;
+}
+__device__ __forceinline__ uint16_t* job_out_row(const JobIn& j, int64_t t, int cols) {
+  return j.batch > 1 ? batch_row(j, j.bout, t, cols) : j.out + t * cols;
+}
+__device__ __forceinline__ int32_t job_id(const JobIn& j, int64_t i, int k) {
+  return j.batch > 1 ? *batch_row(j, j.bids, i, 1, k) : j.ids[i];
+}
+__device__ __forceinline__ const float* job_w_row(const JobIn& j, int64_t t, int k) {
+  return j.batch > 1 ? batch_row(j, j.bw, t, k) : j.w + t * k;
+}
 
 __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   if (j.desc != nullptr) {
@@ -48,12 +87,14 @@ inline uint32_t* call_counters(uint8_t* ws, const afd_ws_layout& L) {
   return reinterpret_cast<uint32_t*>(ws + L.num_tiles);
 }
 
-// The reply an expert call can carry (afd_moe_ffn_answer): once every output row of the call
-// is visible device-wide, *done := value, stored by the last workgroup of the finalize launch
-// to finish. arrive counts the finished workgroups. done == nullptr: no reply.
+// The reply an expert call can carry (afd_moe_ffn_answer, afd_moe_ffn_batch): once every
+// output row of the call is visible device-wide, *done[b] := value[b] for b < count (null
+// counters skipped), stored by the last workgroup of the finalize launch to finish. arrive
+// counts the finished workgroups. count == 0: no reply.
 struct Reply {
-  uint64_t* done;
-  uint64_t value;
+  uint64_t* done[kMaxBatch];
+  uint64_t value[kMaxBatch];
+  int32_t count;
   uint32_t* arrive;
 };
 

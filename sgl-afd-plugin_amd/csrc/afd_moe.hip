@@ -45,15 +45,16 @@ static uint64_t align256(uint64_t v) { return (v + 255) & ~uint64_t(255); }
 constexpr int kFinThreads = 256;
 constexpr int kFinElems = 8;  // bf16 per lane = one 16-byte vector
 
-// One (token, column block) item: out[tok, col .. col + 7]. kWriteThrough: the 16 bytes go out
-// with the system-scope cache bits, which write them through the L2 to memory, so they are
-// visible device-wide once acknowledged.
+// One (token, column block) item: out_row[col .. col + 7] of the call's token tok, whose k
+// weights are w_row. kWriteThrough: the 16 bytes go out with the system-scope cache bits,
+// which write them through the L2 to memory, so they are visible device-wide once
+// acknowledged.
 template <bool kWriteThrough>
 __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
                                               const int32_t* __restrict__ pair_pos,
-                                              const float* __restrict__ w,
-                                              uint16_t* __restrict__ out, int64_t tok, int col,
-                                              int k, int hidden) {
+                                              const float* __restrict__ w_row,
+                                              uint16_t* __restrict__ out_row, int64_t tok,
+                                              int col, int k, int hidden) {
   // products and sums round separately: no contraction of w * y + acc into an fma
 #pragma clang fp contract(off)
   float acc[kFinElems];
@@ -71,7 +72,7 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
     for (int j = 0; j < kBatch; ++j) {
       const bool in = k0 + j < k;
       pos[j] = in ? pair_pos[tok * k + k0 + j] : -1;
-      wk[j] = in ? w[tok * k + k0 + j] : 0.0f;
+      wk[j] = in ? w_row[k0 + j] : 0.0f;
     }
     v4i raw[kBatch];
 #pragma unroll
@@ -98,10 +99,10 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
   if constexpr (kWriteThrough) {
     // one 16-byte vector store per lane (a wavefront writes 1 KiB of whole lines), with the
     // system-scope cache bits; the caller waits for its acknowledgement
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(out + tok * hidden + col), "v"(o)
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(out_row + col), "v"(o)
                  : "memory");
   } else {
-    *reinterpret_cast<v4i*>(out + tok * hidden + col) = o;
+    *reinterpret_cast<v4i*>(out_row + col) = o;
   }
 }
 
@@ -121,15 +122,22 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
     const uint32_t tok = item / static_cast<uint32_t>(col_blocks);
     const int col = static_cast<int>((item - tok * col_blocks) * kFinThreads + threadIdx.x) * kFinElems;
-    if (col < hidden) finalize_item<kReply>(y, pair_pos, job.w, job.out, tok, col, k, hidden);
+    if (col < hidden)
+      finalize_item<kReply>(y, pair_pos, job_w_row(job, tok, k), job_out_row(job, tok, hidden),
+                            tok, col, k, hidden);
   }
   if constexpr (kReply) {
     wait_vmcnt<0>();  // this lane's output stores are acknowledged (written through)
     __syncthreads();  // and every lane's of the workgroup
     if (threadIdx.x == 0 &&
         __hip_atomic_fetch_add(reply.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            gridDim.x - 1)
-      __hip_atomic_store(reply.done, reply.value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            gridDim.x - 1) {
+#pragma unroll
+      for (int b = 0; b < kMaxBatch; ++b)
+        if (b < reply.count && reply.done[b] != nullptr)
+          __hip_atomic_store(reply.done[b], reply.value[b], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
@@ -142,7 +150,7 @@ static int launch_finalize(const uint16_t* y, const int32_t* pair_pos, const Job
   if (job.n == 0) return AFD_OK;
   const int col_blocks = (hidden / kFinElems + kFinThreads - 1) / kFinThreads;
   const int64_t items = col_blocks * job.n;
-  if (reply.done != nullptr) {
+  if (reply.count > 0) {
     const int64_t cap = int64_t(kReplyGroupsPerCu) * device_cu_count();
     hipLaunchKernelGGL(finalize_kernel<true>, dim3(static_cast<unsigned>(items < cap ? items : cap)),
                        dim3(kFinThreads), 0, stream, y, pair_pos, job, k, hidden, col_blocks,
@@ -299,7 +307,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                         const JobIn& job, bool quantized, const uint8_t* xq, const void* xs,
                         void* ws, uint64_t ws_bytes, afd_stream_t stream, void* const* ev,
-                        uint64_t* done = nullptr, uint64_t done_value = 0) {
+                        const Reply* answer = nullptr) {
   if (job.n < 0 || job.n > 0x1ffff) return AFD_ERR_ARG;
   const int32_t n = static_cast<int32_t>(job.n);
   afd_ws_layout L;
@@ -324,7 +332,11 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
     const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
     // routing and the activation quantization (one launch beside the expert histogram), then
     // the pair scatter; stage mark 1 falls between the two launches
-    const Reply reply{done, done_value, done ? call_counters(wsb, L) + kArriveWord : nullptr};
+    Reply reply = {};
+    if (answer != nullptr) {
+      reply = *answer;
+      reply.arrive = call_counters(wsb, L) + kArriveWord;
+    }
     st = launch_route_quant(job, !quantized, *cfg, wsb, L, s,
                             ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
     if (st != AFD_OK) return st;
@@ -345,7 +357,8 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   } else {
     for (int i = 1; i < 5; ++i)
       if ((st = mark(i)) != AFD_OK) return st;
-    if (done) AFD_CHECK_HIP(hipStreamWriteValue64(s, done, done_value, 0));
+    for (int b = 0; answer != nullptr && b < answer->count; ++b)
+      if (answer->done[b]) AFD_CHECK_HIP(hipStreamWriteValue64(s, answer->done[b], answer->value[b], 0));
   }
   return mark(5);
 }
@@ -412,8 +425,53 @@ extern "C" int afd_moe_ffn_answer(const afd_moe_cfg* cfg, const afd_expert_weigh
   if (!done || (reinterpret_cast<uintptr_t>(done) & 7) != 0) return AFD_ERR_ARG;
   if ((x == nullptr) == (xq == nullptr)) return AFD_ERR_ARG;  // exactly one activation form
   const JobIn job{nullptr, x, ids, w, out, n};
+  Reply answer = {};
+  answer.done[0] = done;
+  answer.value[0] = value;
+  answer.count = 1;
   return moe_ffn_impl(cfg, weights, job, x == nullptr, xq, xs, ws, ws_bytes, stream, nullptr,
-                      done, value);
+                      &answer);
+}
+
+extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
+                                 const afd_batch_job* jobs, int32_t num_jobs, void* ws,
+                                 uint64_t ws_bytes, afd_stream_t stream) {
+  if (!jobs || num_jobs < 1 || num_jobs > kMaxBatch) return AFD_ERR_ARG;
+  JobIn job = {};
+  Reply answer = {};
+  int64_t total = 0;
+  bool any_done = false;
+  for (int b = 0; b < num_jobs; ++b) {
+    const afd_batch_job& jb = jobs[b];
+    if (jb.n < 0 || jb.reserved != 0) return AFD_ERR_ARG;
+    if (jb.n > 0 && (!jb.x || !jb.ids || !jb.w || !jb.out)) return AFD_ERR_ARG;
+    if (jb.done && (reinterpret_cast<uintptr_t>(jb.done) & 7) != 0) return AFD_ERR_ARG;
+    job.first[b] = static_cast<int32_t>(total);
+    job.bx[b] = jb.x;
+    job.bids[b] = jb.ids;
+    job.bw[b] = jb.w;
+    job.bout[b] = jb.out;
+    answer.done[b] = jb.done;
+    answer.value[b] = jb.value;
+    any_done = any_done || jb.done != nullptr;
+    total += jb.n;
+    if (total > 0x1ffff) return AFD_ERR_ARG;
+  }
+  job.first[num_jobs] = static_cast<int32_t>(total);
+  job.batch = num_jobs;
+  job.n = total;
+  // job 0's pointers also stand as the call's (moe_ffn_impl checks them for a non-empty call)
+  for (int b = 0; b < num_jobs; ++b)
+    if (jobs[b].n > 0) {
+      job.x = jobs[b].x;
+      job.ids = jobs[b].ids;
+      job.w = jobs[b].w;
+      job.out = jobs[b].out;
+      break;
+    }
+  answer.count = any_done ? num_jobs : 0;
+  return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream, nullptr,
+                      any_done ? &answer : nullptr);
 }
 
 extern "C" int afd_moe_ffn_job(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
@@ -463,8 +521,7 @@ extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const fl
   if (n > 0 && (!y || !pair_pos || !w || !out)) return AFD_ERR_ARG;
   if (hidden <= 0 || hidden % kFinElems) return AFD_ERR_SHAPE;
   const JobIn job{nullptr, nullptr, nullptr, w, out, n};
-  return launch_finalize(y, pair_pos, job, k, hidden, Reply{nullptr, 0, nullptr},
-                         static_cast<hipStream_t>(stream));
+  return launch_finalize(y, pair_pos, job, k, hidden, Reply{}, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int afd_combine(const uint16_t* const* parts, int32_t num_parts,

@@ -23,7 +23,7 @@ template <bool kStageOrder>
 __global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
     const uint16_t* __restrict__ x, int64_t blocks, int cols, uint8_t* __restrict__ q,
     uint8_t* __restrict__ s) {
-  quant_mxfp8_items<kStageOrder>(x, blocks, cols, q, s,
+  quant_mxfp8_items<kStageOrder>([=](int64_t r) { return x + r * cols; }, blocks, cols, q, s,
                                  blockIdx.x * int64_t(kQuantThreads) + threadIdx.x,
                                  int64_t(gridDim.x) * kQuantThreads);
 }
@@ -31,7 +31,8 @@ __global__ __launch_bounds__(kQuantThreads) void quant_mxfp8_kernel(
 __global__ __launch_bounds__(kQuantThreads) void quant_fp8_1x128_kernel(
     const uint16_t* __restrict__ x, int64_t quarters, int cols, uint8_t* __restrict__ q,
     float* __restrict__ s) {
-  quant_fp8_1x128_items(x, quarters, cols, q, s, blockIdx.x * int64_t(kQuantThreads) + threadIdx.x,
+  quant_fp8_1x128_items([=](int64_t r) { return x + r * cols; }, quarters, cols, q, s,
+                        blockIdx.x * int64_t(kQuantThreads) + threadIdx.x,
                         int64_t(gridDim.x) * kQuantThreads);
 }
 

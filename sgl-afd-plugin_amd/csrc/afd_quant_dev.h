@@ -1,6 +1,8 @@
 // Device loops of the activation quantizers, shared by their kernels (afd_quant.hip) and the
 // router's prep kernel (afd_route.hip), which runs one of them beside the expert histogram.
-// Every loop is grid-stride over items from `first` with step `stride` (threads).
+// Every loop is grid-stride over items from `first` with step `stride` (threads). `xrow(r)`
+// gives the start of input row r (the rows of a batched call belong to different jobs); the
+// outputs q / s are one array over all rows.
 #pragma once
 
 #include "afd_common.h"
@@ -18,15 +20,15 @@ inline int grid_for(int64_t items) {
 
 // MXFP8: one lane per 32-element block. kStageOrder stores a row's scales as the MX GEMM reads
 // them: within each group of 4 blocks (one 128-wide K stage), block j at byte scale_byte(j).
-template <bool kStageOrder>
-__device__ __forceinline__ void quant_mxfp8_items(const uint16_t* __restrict__ x, int64_t blocks,
+template <bool kStageOrder, typename XRow>
+__device__ __forceinline__ void quant_mxfp8_items(XRow xrow, int64_t blocks,
                                                   int cols, uint8_t* __restrict__ q,
                                                   uint8_t* __restrict__ s, int64_t first,
                                                   int64_t stride) {
   const int bpr = cols / kMxBlock;
   for (int64_t b = first; b < blocks; b += stride) {
     int64_t row = b / bpr, cb = b % bpr;
-    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cb * kMxBlock);
+    const v4i* src = reinterpret_cast<const v4i*>(xrow(row) + cb * kMxBlock);
     v4i raw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) raw[i] = src[i];
@@ -59,8 +61,8 @@ __device__ __forceinline__ void quant_mxfp8_items(const uint16_t* __restrict__ x
 
 // FP8 1x128: 4 consecutive lanes own one group of 128 (32 elements each); amax via two xor
 // shuffles, so all lanes of a wavefront iterate together (stride a multiple of 64).
-__device__ __forceinline__ void quant_fp8_1x128_items(const uint16_t* __restrict__ x,
-                                                      int64_t quarters, int cols,
+template <typename XRow>
+__device__ __forceinline__ void quant_fp8_1x128_items(XRow xrow, int64_t quarters, int cols,
                                                       uint8_t* __restrict__ q,
                                                       float* __restrict__ s, int64_t first,
                                                       int64_t stride) {
@@ -70,7 +72,7 @@ __device__ __forceinline__ void quant_fp8_1x128_items(const uint16_t* __restrict
     bool live = b < quarters;
     int64_t bb = live ? b : 0;
     int64_t row = bb / qpr, cq = bb % qpr;
-    const v4i* src = reinterpret_cast<const v4i*>(x + row * cols + cq * kMxBlock);
+    const v4i* src = reinterpret_cast<const v4i*>(xrow(row) + cq * kMxBlock);
     float v[32];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

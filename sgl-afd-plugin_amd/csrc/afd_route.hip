@@ -49,15 +49,14 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
     const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
     const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;
     const int64_t items = job.n * (pq.cols / kMxBlock);
+    const int cols = pq.cols;
+    auto xrow = [&job, cols](int64_t r) { return job_x_row(job, r, cols); };
     if constexpr (QUANT == kPrepMxfp8)
-      quant_mxfp8_items<true>(job.x, items, pq.cols, pq.q, static_cast<uint8_t*>(pq.s), first,
-                              stride);
+      quant_mxfp8_items<true>(xrow, items, cols, pq.q, static_cast<uint8_t*>(pq.s), first, stride);
     else if constexpr (QUANT == kPrepFp8)
-      quant_fp8_1x128_items(job.x, items, pq.cols, pq.q, static_cast<float*>(pq.s), first,
-                            stride);
+      quant_fp8_1x128_items(xrow, items, cols, pq.q, static_cast<float*>(pq.s), first, stride);
     return;
   }
-  const int32_t* __restrict__ ids = job.ids;
   const int64_t pairs = job.n * topk;
   __shared__ int cnt[kMaxLocalExperts];
   for (int e = threadIdx.x; e < num_local; e += kRouteThreads) cnt[e] = 0;
@@ -65,7 +64,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
   const int64_t lo = int64_t(blockIdx.x) * chunk;
   const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
   for (int64_t i = lo + threadIdx.x; i < hi; i += kRouteThreads) {
-    int key = pair_key(ids[i], e_lo, num_local);
+    int key = pair_key(job_id(job, i, topk), e_lo, num_local);
     if (key < num_local) atomicAdd(&cnt[key], 1);
   }
   __syncthreads();
@@ -80,7 +79,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
     int32_t* __restrict__ pair_pos, int32_t* __restrict__ tile_expert,
     int32_t* __restrict__ num_tiles) {
   const JobIn job = resolve_job(jin);
-  const int32_t* __restrict__ ids = job.ids;
   const int64_t pairs = job.n * topk;
   constexpr int kWaves = kRouteThreads / 64;
   __shared__ int run[kMaxLocalExperts + 1];
@@ -94,8 +92,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
   const int64_t hi = lo + chunk < pairs ? lo + chunk : pairs;
   // the chunk's first two batches of 256 ids are loaded now, so their latency overlaps the
   // histogram pass; each later batch is loaded two batches ahead
-  int id_cur = lo + t < hi ? ids[lo + t] : 0;
-  int id_nxt = lo + kRouteThreads + t < hi ? ids[lo + kRouteThreads + t] : 0;
+  int id_cur = lo + t < hi ? job_id(job, lo + t, topk) : 0;
+  int id_nxt = lo + kRouteThreads + t < hi ? job_id(job, lo + kRouteThreads + t, topk) : 0;
   // Expert e's chunks are split over G = kRouteThreads / num_local threads (e, g), each summing
   // a contiguous run of them (a multiple of 4 long, so 16-byte loads of the expert's row of the
   // histogram; entries at or past `chunks` are never written and are masked): the counts in
@@ -191,7 +189,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(
     const bool live = i < hi;
     const int id = id_cur;
     id_cur = id_nxt;
-    id_nxt = i + 2 * kRouteThreads < hi ? ids[i + 2 * kRouteThreads] : 0;
+    id_nxt = i + 2 * kRouteThreads < hi ? job_id(job, i + 2 * kRouteThreads, topk) : 0;
     const int key = live ? pair_key(id, e_lo, num_local) : num_local;
     // lanes with the same key (dead lanes join the "not local" key and are ignored)
     uint64_t peers = __ballot(1);

@@ -34,7 +34,7 @@ AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 AFD_WALK_STATIC, AFD_WALK_DYNAMIC = 0, 1
 
 # afd_abi_version() of the library these structures match
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every entry point include/afd.h declares; tests check the library exports all of them.
 EXPORTED = (
@@ -53,6 +53,7 @@ EXPORTED = (
     "afd_moe_ffn",
     "afd_moe_ffn_q",
     "afd_moe_ffn_answer",
+    "afd_moe_ffn_batch",
     "afd_moe_ffn_noalloc",
     "afd_moe_ffn_job",
     "afd_job_set",
@@ -116,6 +117,24 @@ class AfdJob(ctypes.Structure):
         ("w", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
         ("n", ctypes.c_int64),
+    ]
+
+
+AFD_MAX_BATCH = 8
+
+
+class AfdBatchJob(ctypes.Structure):
+    """afd_batch_job: one job of a batched expert call (afd_moe_ffn_batch)."""
+
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("ids", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("done", ctypes.c_void_p),
+        ("value", ctypes.c_uint64),
+        ("n", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -208,6 +227,11 @@ _SIGS = {
     ),
     "afd_moe_ffn_answer": (
         [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), _P, _P, _P, _P, _P, _I32, _P, _U64, _P, _P,
+         _U64, _P],
+        _I32,
+    ),
+    "afd_moe_ffn_batch": (
+        [ctypes.POINTER(AfdMoeCfg), ctypes.POINTER(AfdExpertWeights), ctypes.POINTER(AfdBatchJob), _I32, _P,
          _U64, _P],
         _I32,
     ),

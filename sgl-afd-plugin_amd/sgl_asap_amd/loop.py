@@ -37,12 +37,15 @@ class OneGpuAfd:
     ``AsapBuffer``; the others are driven through ``channels[a]`` directly (``AttnChannel.send`` / ``wait``, pump with ``serve_pending``).
     ``act``: the activation format on the wire ("bf16", or the experts' "mxfp8" /
     "fp8_1x128": A quantizes before the copy). ``f_streams``: the F streams eager jobs
-    alternate over (default: replicas x slots, one per job that can be in flight)."""
+    alternate over (default: replicas x slots, one per job that can be in flight).
+    ``batch_tokens``: serve the bf16 jobs pending together in batched expert calls of up to
+    that many tokens (0: one call per job)."""
 
     def __init__(self, experts: Dict[int, torch.nn.Module], *, n_max: int, slots: int = 2,
                  replicas: int = 1, group: int = 1, seq_base: int = 0, graph_max_tokens: int = 0,
                  timeout_s: float = 60.0, device: int = 0, act: str = "bf16",
-                 timing: bool = False, f_streams: Optional[int] = None, _backpressure: bool = True,
+                 timing: bool = False, f_streams: Optional[int] = None, batch_tokens: int = 0,
+                 _backpressure: bool = True,
                  _epoch_override: Optional[int] = None):
         first = next(iter(experts.values()))
         if first.n_max < n_max:
@@ -54,7 +57,7 @@ class OneGpuAfd:
             raise ValueError(f"activations on the wire as {act}, but the experts read {sorted(reads)}")
         self.server = FfnServer(0, self.geometry, device=device, seq_base=seq_base).start()
         self.scheduler = FfnScheduler(self.server, experts, graph_max_tokens=graph_max_tokens, timing=timing,
-                                      streams=f_streams)
+                                      streams=f_streams, batch_tokens=batch_tokens)
         self.channels = [
             AttnChannel(a, self.geometry, [self.server], device=device, seq_base=seq_base,
                         timeout_s=timeout_s, _backpressure=_backpressure,

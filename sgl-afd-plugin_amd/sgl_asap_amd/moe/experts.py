@@ -368,6 +368,7 @@ class AfdExperts(torch.nn.Module):
         self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit)
         self.tile_walk = tile_walk
         self.layout = workspace_layout(self.cfg, n_max)
+        self._batch_bytes = {n_max: self.layout["total"]}  # workspace bytes per batch capacity
         self._wstruct = weights.as_struct()
 
     @property
@@ -464,6 +465,63 @@ class AfdExperts(torch.nn.Module):
         else:
             _lib.call("afd_moe_ffn", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), x_ptr, ids_ptr, w_ptr, n,
                       ws.data_ptr(), ws.numel(), out_ptr, stream)
+
+    # ---- several jobs of this layer in one call ----
+    def forward_batch(self, jobs, outs: Optional[list] = None) -> list:
+        """One expert call over several jobs of this layer (afd_moe_ffn_batch), on the current
+        stream: ``jobs`` is a list of (hidden_states, topk_output), at most AFD_MAX_BATCH of
+        them and n_max tokens in all. Returns their outputs (or fills ``outs``), each equal
+        bit for bit to ``forward`` on that job alone: the routing, the GEMMs and the finalize
+        run once over the concatenated tokens, so each expert's weights stream once and its
+        rows from different jobs share row tiles."""
+        if not 1 <= len(jobs) <= _lib.AFD_MAX_BATCH:
+            raise ValueError(f"a batch holds 1 to {_lib.AFD_MAX_BATCH} jobs, got {len(jobs)}")
+        if outs is not None and len(outs) != len(jobs):
+            raise ValueError(f"{len(jobs)} jobs but {len(outs)} outputs")
+        descs = (_lib.AfdBatchJob * len(jobs))()
+        keep, results, total = [], [], 0
+        for b, (x, topk_output) in enumerate(jobs):
+            if x.dtype != torch.bfloat16:
+                raise TypeError(f"the expert path takes bf16 activations, got {x.dtype}")
+            if x.dim() != 2 or x.shape[1] != self.hidden_size or not x.is_cuda:
+                raise ValueError(f"x must be a device tensor [n, {self.hidden_size}], got {tuple(x.shape)} on {x.device}")
+            n = x.shape[0]
+            ids, w = self._topk(n, topk_output, x.device)
+            x = x.contiguous()
+            out = self._out(None if outs is None else outs[b], n, x.device)
+            keep += [x, ids, w]
+            results.append(out)
+            d = descs[b]
+            d.x, d.ids, d.w, d.out, d.n = x.data_ptr(), ids.data_ptr(), w.data_ptr(), out.data_ptr(), n
+            total += n
+        if total > self.n_max:
+            raise ValueError(f"{total} tokens in the batch exceed n_max={self.n_max}")
+        ws = self.workspace()
+        _lib.call("afd_moe_ffn_batch", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), descs, len(jobs),
+                  ws.data_ptr(), ws.numel(), _stream_handle())
+        return results
+
+    def call_batch_ptrs(self, rows, stream: int, capacity: Optional[int] = None) -> None:
+        """``call_ptrs`` for several bf16 jobs in one call (afd_moe_ffn_batch): ``rows`` is a
+        list of (n, x_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value); each job's output
+        goes to its out_ptr and, with done_ptr, its counter becomes done_value once all the
+        batch's output is visible. ``capacity``: the most tokens a batch holds (default
+        n_max), which sizes the stream's workspace."""
+        capacity = self.n_max if capacity is None else capacity
+        total = sum(r[0] for r in rows)
+        if not 1 <= len(rows) <= _lib.AFD_MAX_BATCH or not 0 < total <= capacity:
+            raise ValueError(f"{len(rows)} jobs of {total} tokens: a batch holds 1 to "
+                             f"{_lib.AFD_MAX_BATCH} jobs and 1 to {capacity} tokens")
+        nbytes = self._batch_bytes.get(capacity)
+        if nbytes is None:
+            nbytes = self._batch_bytes[capacity] = workspace_layout(self.cfg, capacity)["total"]
+        ws = stream_workspace(self.weights.w13.device, stream, nbytes)
+        descs = (_lib.AfdBatchJob * len(rows))()
+        for d, (n, x_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value) in zip(descs, rows):
+            d.x, d.ids, d.w, d.out, d.n = x_ptr, ids_ptr, w_ptr, out_ptr, n
+            d.done, d.value = done_ptr or None, done_value
+        _lib.call("afd_moe_ffn_batch", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), descs, len(rows),
+                  ws.data_ptr(), ws.numel(), stream)
 
     # ---- graph replay: the job is read from a device descriptor when the calls run ----
     def call_job(self, desc: torch.Tensor, n_cap: int, quantized: bool = False,

@@ -21,6 +21,14 @@ call, so the default is eager. A job of several rows
 same stream, so one output buffer is enough and its memory is never handed out while a copy
 still reads it. With fp8 activations on the wire (``Geometry.act``) the rows arrive as e4m3
 codes plus scales and the expert call runs on them as they are.
+
+Batching (``batch_tokens`` > 0; the reference runs one expert call per job): the single-row
+bf16 jobs of one poll that belong to the same layer are packed, largest first, into batches
+of at most ``batch_tokens`` tokens and AFD_MAX_BATCH jobs, each served by one expert call
+(afd_moe_ffn_batch) on one F stream after gating on every job's doorbell. Every job still gets
+its own output in its A rank's segment and its own done counter, and its output is the same
+bit for bit as when served alone; the batch streams each expert's weights once for all its
+jobs and fills their row tiles together.
 """
 
 from __future__ import annotations
@@ -32,6 +40,7 @@ from typing import Dict, List, Optional
 import numpy as np
 import torch
 
+from .. import _lib
 from ..moe.experts import act_scale_shape
 from ..moe.topk import StandardTopKOutput
 from .graph_runner import FfnGraphRunner, graph_buckets
@@ -107,8 +116,13 @@ class FfnScheduler:
     """Serves the jobs an ``FfnServer`` discovers with the routed experts of every layer."""
 
     def __init__(self, server, experts: Dict[int, torch.nn.Module], *, graph_max_tokens: int = 0,
-                 timing: bool = False, streams: Optional[int] = None):
+                 timing: bool = False, streams: Optional[int] = None, batch_tokens: int = 0):
         self.server, self.g = server, server.g
+        if batch_tokens < 0:
+            raise ValueError(f"batch_tokens must be >= 0, got {batch_tokens}")
+        self.batch_tokens = batch_tokens
+        self.batch_calls = 0  # expert calls that served more than one job
+        self.expert_calls = 0  # expert calls (or graph replays) of any kind
         self.experts = experts
         self.local = next(iter(experts.values())).local
         # A serving GPU is shared: the attention side's kernels and its parked stream waits
@@ -242,9 +256,7 @@ class FfnScheduler:
     def run_job(self, job) -> None:
         """Gate, expert call and reply of one job, all enqueued on one F stream (the next in
         turn)."""
-        turn = self._turn
-        self._turn = (turn + 1) % len(self.streams)
-        stream = self.streams[turn]
+        turn, stream = self._next_stream()
         runner = self.graph_runners[turn] if self.graph_runners else None
         self.server.gate(job, stream.cuda_stream)
         token = self.clock.start(stream) if self.clock is not None else None
@@ -254,9 +266,73 @@ class FfnScheduler:
             with torch.cuda.stream(stream):
                 n = self._run_rows(job, stream, runner)
         self.layer_calls[job.layer_id] += 1
+        self.expert_calls += 1
         if token is not None:
             self.clock.stop(token, n, stream)
 
+    def _next_stream(self):
+        turn = self._turn
+        self._turn = (turn + 1) % len(self.streams)
+        return turn, self.streams[turn]
+
+    def _batchable(self, job) -> bool:
+        return len(job.rows) == 1 and self.g.act == "bf16" and job.rows[0].n_tokens <= self.batch_tokens
+
+    def _pack(self, jobs) -> List[list]:
+        """First-fit decreasing: jobs (of one layer) into batches of at most batch_tokens
+        tokens and AFD_MAX_BATCH jobs."""
+        bins: List[list] = []
+        room: List[int] = []
+        for job in sorted(jobs, key=lambda j: -j.rows[0].n_tokens):
+            n = job.rows[0].n_tokens
+            for b, free in enumerate(room):
+                if n <= free and len(bins[b]) < _lib.AFD_MAX_BATCH:
+                    bins[b].append(job)
+                    room[b] = free - n
+                    break
+            else:
+                bins.append([job])
+                room.append(self.batch_tokens - n)
+        return bins
+
+    @torch.no_grad()
+    def run_batch(self, jobs) -> None:
+        """Gates, one expert call and the replies of several single-row bf16 jobs of one
+        layer, all on one F stream (the next in turn); a batch of one is ``run_job``."""
+        if len(jobs) == 1:
+            self.run_job(jobs[0])
+            return
+        layer_id = jobs[0].layer_id
+        if any(job.layer_id != layer_id or not self._batchable(job) for job in jobs):
+            raise ValueError("a batch holds single-row bf16 jobs of one layer within batch_tokens")
+        _, stream = self._next_stream()
+        rows = []
+        for job in jobs:
+            self.server.gate(job, stream.cuda_stream)
+            row = job.rows[0]
+            rows.append((row.n_tokens, row.x_ptr, row.ids_ptr, row.w_ptr, self.server.seg_ptr(row),
+                         self.server.done_addr(row), row.seq))
+        token = self.clock.start(stream) if self.clock is not None else None
+        self.experts[layer_id].call_batch_ptrs(rows, stream.cuda_stream, capacity=self.batch_tokens)
+        self.layer_calls[layer_id] += len(jobs)
+        self.batch_calls += 1
+        self.expert_calls += 1
+        if token is not None:
+            self.clock.stop(token, sum(r[0] for r in rows), stream)
+
     def serve_pending(self) -> int:
-        """Poll once and run every complete job (the one-GPU form of serve_forever)."""
-        return self.server.serve_pending(self.run_job)
+        """Poll once and run every complete job (the one-GPU form of serve_forever); with
+        ``batch_tokens``, the batchable jobs of the poll in batches per layer."""
+        if not self.batch_tokens:
+            return self.server.serve_pending(self.run_job)
+        jobs = self.server.poll()
+        by_layer: Dict[int, list] = collections.defaultdict(list)
+        for job in jobs:
+            if self._batchable(job):
+                by_layer[job.layer_id].append(job)
+            else:
+                self.run_job(job)
+        for layer_jobs in by_layer.values():
+            for batch in self._pack(layer_jobs):
+                self.run_batch(batch)
+        return len(jobs)

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_functions():
         assert hasattr(L, name), name
-    assert L.afd_abi_version() == _lib.ABI_VERSION == 2
+    assert L.afd_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_status_strings():
