@@ -161,7 +161,8 @@ class FfnScheduler:
         uniformly over all experts, weights ~ U(0,1)), on the first layer at every size and on
         every other layer at the smallest size, on the first F stream; on every other F stream
         each layer at the smallest size. So every kernel and every workspace has been used
-        before serving. Synchronizes; returns the sizes run."""
+        before serving; with ``batch_tokens``, also a batched call on every F stream (its
+        workspace). Synchronizes; returns the sizes run."""
         order = sorted(self.experts)
         first = self.experts[order[0]]
         sizes = graph_buckets(n_max)
@@ -184,6 +185,16 @@ class FfnScheduler:
             with torch.cuda.stream(stream):
                 for layer_id in order:
                     self.experts[layer_id](x[: sizes[0]], topk)
+        if self.batch_tokens:
+            # the batched calls' workspaces (one per F stream, batch_tokens tokens) are made now,
+            # not by the first batch while serving: a batch of two one-token jobs on each stream
+            out = torch.empty(2, first.hidden_size, dtype=torch.bfloat16, device=device)
+            rows = [(1, x[i].data_ptr(), ids[i].data_ptr(), w[i].data_ptr(), out[i].data_ptr(), 0, 0)
+                    for i in range(2)]
+            for stream in self.streams:
+                with torch.cuda.stream(stream):
+                    for layer_id in order:
+                        self.experts[layer_id].call_batch_ptrs(rows, stream.cuda_stream, capacity=self.batch_tokens)
         torch.cuda.synchronize()
         return sizes
 

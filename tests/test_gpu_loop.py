@@ -340,12 +340,13 @@ def test_stall_releases_the_parked_wait_and_poisons():
         assert np.array_equal(bits16(out), direct(experts, 0, x, topk))
 
 
-def test_warmup_then_serve():
-    """The F scheduler's warm-up runs every bucket size on two layers, then jobs are served
-    as before."""
-    say("loop: scheduler warm-up up to 64 tokens, two layers")
+@pytest.mark.parametrize("batch_tokens", [0, 128])
+def test_warmup_then_serve(batch_tokens):
+    """The F scheduler's warm-up runs every bucket size on two layers (and, with batching, a
+    batched call on every F stream), then jobs are served as before."""
+    say(f"loop: scheduler warm-up up to 64 tokens, two layers, batch_tokens={batch_tokens}")
     experts = make_experts(64, layers=(0, 1))
-    with OneGpuAfd(experts, n_max=64, graph_max_tokens=64) as afd:
+    with OneGpuAfd(experts, n_max=64, graph_max_tokens=64, batch_tokens=batch_tokens) as afd:
         assert afd.scheduler.warmup(64) == [1, 2, 4, 8, 16, 32, 64]
         for lid in (0, 1):
             x, topk = job(40, 990 + lid)
