@@ -239,12 +239,15 @@ int afd_moe_ffn_answer(const afd_moe_cfg* cfg, const afd_expert_weights* weights
                        const float* w, int32_t n, void* ws, uint64_t ws_bytes, uint16_t* out,
                        uint64_t* done, uint64_t value, afd_stream_t stream);
 
-/* One job of a batched expert call: x bf16 [n][H], ids i32 [n][k], w f32 [n][k], out bf16
+/* One job of a batched expert call: x bf16 [n][H] (or x = NULL and the rows quantized by
+ * afd_quant_act: xq e4m3 [n][H] and xs their scales), ids i32 [n][k], w f32 [n][k], out bf16
  * [n][H]; done: NULL, or an 8-byte aligned counter (pinned host or device memory) that the
  * call sets to `value` once this job's output rows are visible device-wide. */
 #define AFD_MAX_BATCH 8
 typedef struct afd_batch_job {
   const uint16_t* x;
+  const uint8_t* xq;
+  const void* xs;
   const int32_t* ids;
   const float* w;
   uint16_t* out;
@@ -258,8 +261,10 @@ typedef struct afd_batch_job {
  * one job: the routing, both GEMMs and the finalize run once over the concatenated tokens
  * (each expert's weights stream once for all the jobs, and its rows from different jobs share
  * row tiles), while every job reads its own x, ids and w and gets its own out. Each job's out
- * equals afd_moe_ffn on that job alone, bit for bit (a token's output depends on its own row
- * only). ws_bytes from afd_workspace_layout(cfg, sum of n), at most 131071 tokens in all. If
+ * equals afd_moe_ffn (or, for quantized rows, afd_moe_ffn_q) on that job alone, bit for bit
+ * (a token's output depends on its own row only). Every job gives its rows in the same form;
+ * quantized rows are first copied into the workspace's activation buffers (device-to-device,
+ * on `stream`). ws_bytes from afd_workspace_layout(cfg, sum of n), at most 131071 tokens. If
  * any job has a done counter, every job's counter is stored by the last workgroup of the
  * call's final launch (as afd_moe_ffn_answer does), after all the jobs' rows are visible.
  * Extends the FFN rank's per-job expert call (P/srt/managers/scheduler.py:410-412), which

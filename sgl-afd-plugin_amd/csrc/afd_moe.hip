@@ -441,10 +441,12 @@ extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weight
   Reply answer = {};
   int64_t total = 0;
   bool any_done = false;
+  const bool quantized = jobs[0].x == nullptr;  // every job: x, or xq and xs
   for (int b = 0; b < num_jobs; ++b) {
     const afd_batch_job& jb = jobs[b];
     if (jb.n < 0 || jb.reserved != 0) return AFD_ERR_ARG;
-    if (jb.n > 0 && (!jb.x || !jb.ids || !jb.w || !jb.out)) return AFD_ERR_ARG;
+    const bool rows_ok = quantized ? (!jb.x && jb.xq && jb.xs) : (jb.x && !jb.xq && !jb.xs);
+    if (jb.n > 0 && (!rows_ok || !jb.ids || !jb.w || !jb.out)) return AFD_ERR_ARG;
     if (jb.done && (reinterpret_cast<uintptr_t>(jb.done) & 7) != 0) return AFD_ERR_ARG;
     job.first[b] = static_cast<int32_t>(total);
     job.bx[b] = jb.x;
@@ -460,7 +462,7 @@ extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weight
   job.first[num_jobs] = static_cast<int32_t>(total);
   job.batch = num_jobs;
   job.n = total;
-  // job 0's pointers also stand as the call's (moe_ffn_impl checks them for a non-empty call)
+  // the first non-empty job's pointers also stand as the call's (moe_ffn_impl checks them)
   for (int b = 0; b < num_jobs; ++b)
     if (jobs[b].n > 0) {
       job.x = jobs[b].x;
@@ -470,8 +472,32 @@ extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weight
       break;
     }
   answer.count = any_done ? num_jobs : 0;
-  return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream, nullptr,
-                      any_done ? &answer : nullptr);
+  if (!quantized)
+    return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream,
+                        nullptr, any_done ? &answer : nullptr);
+  // quantized rows: staged one job after another into the workspace's xq / xs, which the
+  // call then reads as one job's
+  afd_ws_layout L;
+  int st = afd_workspace_layout(cfg, static_cast<int32_t>(total), &L);
+  if (st != AFD_OK) return st;
+  if (!ws) return AFD_ERR_ARG;
+  if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
+  const uint64_t q_row = uint64_t(cfg->hidden);
+  const uint64_t s_row = cfg->weight_fmt == AFD_W_MXFP4 ? uint64_t(cfg->hidden / 32)
+                                                        : uint64_t(cfg->hidden / 128) * 4;
+  uint8_t* wsb = static_cast<uint8_t*>(ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int b = 0; b < num_jobs; ++b) {
+    const uint64_t n = static_cast<uint64_t>(jobs[b].n);
+    if (n == 0) continue;
+    const uint64_t t0 = static_cast<uint64_t>(job.first[b]);
+    AFD_CHECK_HIP(hipMemcpyAsync(wsb + L.xq + t0 * q_row, jobs[b].xq, n * q_row,
+                                 hipMemcpyDeviceToDevice, s));
+    AFD_CHECK_HIP(hipMemcpyAsync(wsb + L.xs + t0 * s_row, jobs[b].xs, n * s_row,
+                                 hipMemcpyDeviceToDevice, s));
+  }
+  return moe_ffn_impl(cfg, weights, job, true, wsb + L.xq, wsb + L.xs, ws, ws_bytes, stream,
+                      nullptr, any_done ? &answer : nullptr);
 }
 
 extern "C" int afd_moe_ffn_job(const afd_moe_cfg* cfg, const afd_expert_weights* weights,

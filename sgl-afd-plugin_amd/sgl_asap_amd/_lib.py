@@ -128,6 +128,8 @@ class AfdBatchJob(ctypes.Structure):
 
     _fields_ = [
         ("x", ctypes.c_void_p),
+        ("xq", ctypes.c_void_p),
+        ("xs", ctypes.c_void_p),
         ("ids", ctypes.c_void_p),
         ("w", ctypes.c_void_p),
         ("out", ctypes.c_void_p),

@@ -64,6 +64,8 @@ class OneGpuAfd:
                         _epoch_override=_epoch_override).connect()
             for a in range(replicas * group)
         ]
+        for channel in self.channels:
+            channel.pump = self.scheduler.serve_pending
         self.channel = self.channels[0]
         self.buffer = AsapBuffer.install(self.channel, device, pump=self.scheduler.serve_pending)
 

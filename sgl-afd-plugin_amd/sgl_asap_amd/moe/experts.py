@@ -502,11 +502,12 @@ class AfdExperts(torch.nn.Module):
         return results
 
     def call_batch_ptrs(self, rows, stream: int, capacity: Optional[int] = None) -> None:
-        """``call_ptrs`` for several bf16 jobs in one call (afd_moe_ffn_batch): ``rows`` is a
-        list of (n, x_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value); each job's output
-        goes to its out_ptr and, with done_ptr, its counter becomes done_value once all the
-        batch's output is visible. ``capacity``: the most tokens a batch holds (default
-        n_max), which sizes the stream's workspace."""
+        """``call_ptrs`` for several jobs in one call (afd_moe_ffn_batch): ``rows`` is a list
+        of (n, x_ptr, xs_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value), x_ptr being bf16
+        rows (xs_ptr = 0) or, for every job alike, the e4m3 rows whose scales are at xs_ptr;
+        each job's output goes to its out_ptr and, with done_ptr, its counter becomes
+        done_value once all the batch's output is visible. ``capacity``: the most tokens a
+        batch holds (default n_max), which sizes the stream's workspace."""
         capacity = self.n_max if capacity is None else capacity
         total = sum(r[0] for r in rows)
         if not 1 <= len(rows) <= _lib.AFD_MAX_BATCH or not 0 < total <= capacity:
@@ -517,8 +518,12 @@ class AfdExperts(torch.nn.Module):
             nbytes = self._batch_bytes[capacity] = workspace_layout(self.cfg, capacity)["total"]
         ws = stream_workspace(self.weights.w13.device, stream, nbytes)
         descs = (_lib.AfdBatchJob * len(rows))()
-        for d, (n, x_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value) in zip(descs, rows):
-            d.x, d.ids, d.w, d.out, d.n = x_ptr, ids_ptr, w_ptr, out_ptr, n
+        for d, (n, x_ptr, xs_ptr, ids_ptr, w_ptr, out_ptr, done_ptr, done_value) in zip(descs, rows):
+            if xs_ptr:
+                d.xq, d.xs = x_ptr, xs_ptr
+            else:
+                d.x = x_ptr
+            d.ids, d.w, d.out, d.n = ids_ptr, w_ptr, out_ptr, n
             d.done, d.value = done_ptr or None, done_value
         _lib.call("afd_moe_ffn_batch", ctypes.byref(self.cfg), ctypes.byref(self._wstruct), descs, len(rows),
                   ws.data_ptr(), ws.numel(), stream)

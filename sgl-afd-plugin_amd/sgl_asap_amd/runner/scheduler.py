@@ -23,7 +23,7 @@ still reads it. With fp8 activations on the wire (``Geometry.act``) the rows arr
 codes plus scales and the expert call runs on them as they are.
 
 Batching (``batch_tokens`` > 0; the reference runs one expert call per job): the single-row
-bf16 jobs of one poll that belong to the same layer are packed, largest first, into batches
+jobs of one poll that belong to the same layer are packed, largest first, into batches
 of at most ``batch_tokens`` tokens and AFD_MAX_BATCH jobs, each served by one expert call
 (afd_moe_ffn_batch) on one F stream after gating on every job's doorbell. Every job still gets
 its own output in its A rank's segment and its own done counter, and its output is the same
@@ -189,7 +189,7 @@ class FfnScheduler:
             # the batched calls' workspaces (one per F stream, batch_tokens tokens) are made now,
             # not by the first batch while serving: a batch of two one-token jobs on each stream
             out = torch.empty(2, first.hidden_size, dtype=torch.bfloat16, device=device)
-            rows = [(1, x[i].data_ptr(), ids[i].data_ptr(), w[i].data_ptr(), out[i].data_ptr(), 0, 0)
+            rows = [(1, x[i].data_ptr(), 0, ids[i].data_ptr(), w[i].data_ptr(), out[i].data_ptr(), 0, 0)
                     for i in range(2)]
             for stream in self.streams:
                 with torch.cuda.stream(stream):
@@ -287,7 +287,7 @@ class FfnScheduler:
         return turn, self.streams[turn]
 
     def _batchable(self, job) -> bool:
-        return len(job.rows) == 1 and self.g.act == "bf16" and job.rows[0].n_tokens <= self.batch_tokens
+        return len(job.rows) == 1 and job.rows[0].n_tokens <= self.batch_tokens
 
     def _pack(self, jobs) -> List[list]:
         """First-fit decreasing: jobs (of one layer) into batches of at most batch_tokens
@@ -308,20 +308,21 @@ class FfnScheduler:
 
     @torch.no_grad()
     def run_batch(self, jobs) -> None:
-        """Gates, one expert call and the replies of several single-row bf16 jobs of one
-        layer, all on one F stream (the next in turn); a batch of one is ``run_job``."""
+        """Gates, one expert call and the replies of several single-row jobs of one layer,
+        all on one F stream (the next in turn); a batch of one is ``run_job``."""
         if len(jobs) == 1:
             self.run_job(jobs[0])
             return
         layer_id = jobs[0].layer_id
         if any(job.layer_id != layer_id or not self._batchable(job) for job in jobs):
-            raise ValueError("a batch holds single-row bf16 jobs of one layer within batch_tokens")
+            raise ValueError("a batch holds single-row jobs of one layer within batch_tokens")
         _, stream = self._next_stream()
         rows = []
         for job in jobs:
             self.server.gate(job, stream.cuda_stream)
             row = job.rows[0]
-            rows.append((row.n_tokens, row.x_ptr, row.ids_ptr, row.w_ptr, self.server.seg_ptr(row),
+            xs_ptr = row.x_ptr + self.g.xs_off if self.g.act != "bf16" else 0
+            rows.append((row.n_tokens, row.x_ptr, xs_ptr, row.ids_ptr, row.w_ptr, self.server.seg_ptr(row),
                          self.server.done_addr(row), row.seq))
         token = self.clock.start(stream) if self.clock is not None else None
         self.experts[layer_id].call_batch_ptrs(rows, stream.cuda_stream, capacity=self.batch_tokens)

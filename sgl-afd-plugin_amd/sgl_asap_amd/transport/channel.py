@@ -137,6 +137,9 @@ class AttnChannel:
         self.segments = None  # device uint8 tensor: num_f * slots result segments
         self.watch: Optional[StallWatch] = None
         self._poison: Optional[ChannelPoisoned] = None
+        # with the F rank in this process: its serve call (FfnScheduler.serve_pending), run by
+        # send before a backpressure wait the host does not see satisfied yet
+        self.pump: Optional[Callable[[], object]] = None
         self._count: List[int] = []
         self._epochs: List[int] = []
         self._desc: List[_lib.AfdSendDesc] = []
@@ -258,6 +261,12 @@ class AttnChannel:
                 answered = self.flags.load(g.done_off(f, slot)) >= seq - 1
                 d.done[f] = None if answered else self._done_addrs[slot][f]
                 pending = pending or not answered
+        if pending and self.pump is not None and any(sv.unserved(self.a, slot) for sv in self.servers):
+            # in-process F side that has not taken the slot's previous message yet: serve what
+            # is pending before this send's stream waits for that message's answer, so the
+            # wait is enqueued after the work that satisfies it even when the two streams share
+            # a hardware queue
+            self.pump()
         hip.send(d, stream.cuda_stream)
         self._count[slot] = seq
         for f, server in enumerate(self.servers):

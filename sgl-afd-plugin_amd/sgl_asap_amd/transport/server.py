@@ -161,6 +161,11 @@ class FfnServer:
         """Post the doorbell word A's producer stream will write to bell(a, slot)."""
         self._inbox.append((a, slot, int(word)))
 
+    def unserved(self, a: int, slot: int) -> bool:
+        """Whether a word A rank ``a`` posted for ``slot`` still waits in the inbox (no poll
+        has taken it, so no job for it has been enqueued)."""
+        return any(m[0] == a and m[1] == slot for m in self._inbox)
+
     def poll(self) -> List[Job]:
         """Every job completed by the words posted since the last call; never blocks."""
         jobs = []

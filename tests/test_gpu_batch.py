@@ -90,7 +90,7 @@ def test_batch_answers_every_job(dsv4_layer):
         rows = []
         for b, ((x, t), out) in enumerate(zip(jobs, outs)):
             done = page.addr(64 * b) if b != 1 else 0
-            rows.append((x.shape[0], x.data_ptr(), t.topk_ids.data_ptr(), t.topk_weights.data_ptr(),
+            rows.append((x.shape[0], x.data_ptr(), 0, t.topk_ids.data_ptr(), t.topk_weights.data_ptr(),
                          out.data_ptr(), done, 1000 + b))
         stream = torch.cuda.current_stream().cuda_stream
         dsv4_layer.call_batch_ptrs(rows, stream, capacity=8192)
@@ -187,3 +187,64 @@ def test_scheduler_batches_the_jobs_of_one_poll(dsv4_layer):
         assert afd.scheduler.batch_calls == 4
     for i, c in enumerate(copies):
         assert np.array_equal(bits16(c), eager[i % 4]), (i, sizes[i % 4])
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_quantized_rows_batch_equals_single_calls(fmt):
+    """Rows quantized by the A side (fp8 on the wire): the batch stages them into its
+    workspace and every job's output equals afd_moe_ffn_q on that job alone."""
+    hidden, inter, num_experts, num_local, k = (1024, 512, 64, 16, 6)
+    say(f"batch: quantized rows, {fmt} H={hidden} I={inter} E={num_experts} local={num_local} k={k}")
+    gen = W.generator("cpu", 51)
+    w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
+    pack = pack_fp8_block_experts if fmt == "fp8_block" else pack_mxfp4_experts
+    layer = AfdExperts(num_experts, k, 0, range(0, num_local), pack(w13, w2, device=dev()), n_max=4096)
+    jobs, single = [], []
+    for j, n in enumerate((700, 1, 0, 1300, 64)):
+        g = W.generator("cpu", 60 + j)
+        x = W.tokens(n, hidden, g, "cpu").to(dev())
+        ids, w = W.route_zipf(n, num_experts, k, 1.2, g, "cpu")
+        topk = StandardTopKOutput(w.to(dev()), ids.to(dev()))
+        xq, xs = layer.quant_act(x)
+        jobs.append((xq, xs, topk, torch.empty(n, hidden, dtype=torch.bfloat16, device=dev())))
+        single.append(bits16(layer.forward_q(xq, xs, topk)))
+    rows = [(xq.shape[0], xq.data_ptr(), xs.data_ptr(), t.topk_ids.data_ptr(), t.topk_weights.data_ptr(),
+             out.data_ptr(), 0, 0) for xq, xs, t, out in jobs if xq.shape[0] > 0]
+    layer.call_batch_ptrs(rows, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    outs = [out for xq, _, _, out in jobs if xq.shape[0] > 0]
+    want = [s for s, (xq, _, _, _) in zip(single, jobs) if xq.shape[0] > 0]
+    for b, (s, o) in enumerate(zip(want, outs)):
+        assert np.array_equal(s, bits16(o)), b
+
+
+def test_scheduler_batches_fp8_wire_jobs(dsv4_layer):
+    """MXFP8 on the wire: the A side quantizes before the copy and the scheduler's batched
+    calls stage the arena's e4m3 rows; every answer equals the plain bf16 call's."""
+    sizes = (3000, 700, 5000, 2100)
+    say(f"batch: scheduler with MXFP8 on the wire, jobs {sizes}")
+    jobs = make_jobs(DSV4, sizes, 990, dev())
+    eager = [bits16(dsv4_layer(x, t)) for x, t in jobs]
+    order = [(r, mb) for r in range(2) for mb in range(2)]
+    with OneGpuAfd({0: dsv4_layer}, n_max=16384, slots=2, replicas=2, act="mxfp8", batch_tokens=16384) as afd:
+        main = torch.cuda.current_stream()
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        for s in sends:
+            s.wait_stream(main)
+        quantized = [dsv4_layer.quant_act(x) for x, _ in jobs]  # the A side's quantizer
+        for s in sends:
+            s.wait_stream(main)
+        tickets = []
+        for (r, mb), (x, t), (xq, xs) in zip(order, jobs, quantized):
+            tickets.append((r, afd.channels[r].send(0, mb, xq.data_ptr(), t.topk_ids.data_ptr(),
+                                                    t.topk_weights.data_ptr(), x.shape[0], sends[r],
+                                                    xs_ptr=xs.data_ptr())))
+        afd.scheduler.serve_pending()
+        got = []
+        for r, t in tickets:
+            afd.channels[r].wait(t, main)
+            got.append(afd.channels[r].result_view(0, t.slot, t.n_tokens).clone())
+        torch.cuda.synchronize()
+        assert afd.scheduler.batch_calls == 1  # 10800 tokens in one call
+    for i, c in enumerate(got):
+        assert np.array_equal(bits16(c), eager[i]), (i, sizes[i])

@@ -281,9 +281,10 @@ def test_group_jobs_served_back_to_back():
 
 
 def test_two_sends_on_one_slot_before_serving():
-    """The producer posts message 2 of a slot before the F host polled message 1 (its stream
-    then waits for the answer to 1 before overwriting the region): F serves 1, then 2, and the
-    answer to 2 is right."""
+    """The producer posts message 2 of a slot before anything served message 1: its stream
+    must wait for the answer to 1 before overwriting the region, so the send first serves
+    what is pending (message 1's job is enqueued before that wait, whatever hardware queues
+    the streams share), then F serves 2, and the answer to 2 is right."""
     say("loop: two sends on one slot before a poll")
     experts = make_experts(64)
     with OneGpuAfd(experts, n_max=64, slots=1) as afd:
@@ -293,7 +294,9 @@ def test_two_sends_on_one_slot_before_serving():
         t1, h1 = _send(afd, 0, 0, x1, k1, send)
         t2, h2 = _send(afd, 0, 0, x2, k2, send)
         assert (t1.seq, t2.seq) == (1, 2)
-        assert afd.scheduler.serve_pending() == 2
+        assert afd.server.stats["jobs"] == 1  # message 1, served by the second send
+        assert afd.scheduler.serve_pending() == 1
+        assert afd.server.stats["jobs"] == 2
         afd.channel.wait(t2, main)
         got = afd.channel.result_view(0, 0, t2.n_tokens).clone()
         torch.cuda.synchronize()

@@ -173,9 +173,11 @@ def test_two_sends_on_one_slot_before_a_poll_are_both_served_in_order():
     e = connect(s, g, 0)
     s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
     s.announce(0, 0, L.pack_doorbell(2, 7, 1, e))
+    assert s.unserved(0, 0) and not s.unserved(0, 1)
     jobs = s.poll()
     assert served(jobs) == [(0, 0, 0, [1]), (0, 0, 1, [2])]
     assert s.stats["lost_messages"] == 0
+    assert not s.unserved(0, 0)
 
 
 def test_gaps_count_as_lost_and_old_words_are_ignored():
