@@ -60,7 +60,7 @@
 extern "C" {
 #endif
 
-#define AFD_ABI_VERSION 3
+#define AFD_ABI_VERSION 4
 
 typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
 
@@ -74,10 +74,22 @@ enum afd_status {
   AFD_ERR_WORKSPACE = -5    /* the workspace is smaller than afd_workspace_layout().total */
 };
 
-/* Expert weight formats (the activation format follows from it). */
+/* Expert weight formats. */
 enum afd_weight_fmt {
-  AFD_W_MXFP4 = 1,    /* E2M1 + UE8M0 per 32 along K; activations MXFP8 (e4m3 + UE8M0/32) */
-  AFD_W_FP8_BLOCK = 2 /* e4m3 + fp32 per 128x128; activations e4m3 + fp32 per 1x128 */
+  AFD_W_MXFP4 = 1,    /* E2M1 + UE8M0 per 32 along K; fp8 activations MXFP8 (e4m3 + UE8M0/32) */
+  AFD_W_FP8_BLOCK = 2 /* e4m3 + fp32 per 128x128; fp8 activations e4m3 + fp32 per 1x128 */
+};
+
+/* Activation format of the expert GEMMs (the precision the MoE method runs its GEMMs in:
+ * SGLang's MXFP4 method quantizes the input to MXFP8 under its default
+ * flashinfer_mxfp4_moe_precision and has others, python/sgl_asap_plugin/srt/layers/
+ * quantization/mxfp4_flashinfer_trtllm_moe.py:49-61; the reference also runs W4A16 experts,
+ * MXFP4 weights with bf16 activations, through humming: scripts/run_ep.sh:4, README.md:25). */
+enum afd_act_fmt {
+  AFD_A_FP8 = 0, /* the weight format's fp8 activations (above): x and h are quantized */
+  AFD_A_BF16 = 1 /* bf16 activations (MXFP4 weights only): x is read as it is, h is rounded
+                    to bf16, and the GEMMs run on bf16 MFMA with the weights expanded in
+                    registers */
 };
 
 /* Stream-wait conditions, as HIP's hipStreamWaitValue flags. */
@@ -123,6 +135,7 @@ typedef struct afd_moe_cfg {
   float act_alpha;    /* SiTU: A > 0 (unused otherwise) */
   float act_limit;    /* SiTU, SwiGLU with limit: L > 0 and finite (unused for SwiGLU) */
   int32_t tile_walk;  /* enum afd_tile_walk (0: static) */
+  int32_t act_fmt;    /* enum afd_act_fmt (0: fp8) */
 } afd_moe_cfg;
 
 /* Packed expert weights of one layer (device pointers), as afd_pack_* writes them.
@@ -148,7 +161,8 @@ typedef struct afd_ws_layout {
   uint64_t total;          /* bytes the workspace must have */
   uint64_t xq, xs;         /* quantized activations [n][H] and their scales (MXFP4: e4m3 and
                               UE8M0 per 32, the 4 of each 128-wide K stage in stage order;
-                              FP8 block: e4m3 and f32 per 1x128) */
+                              FP8 block: e4m3 and f32 per 1x128); bf16 activations: xq holds
+                              a batched call's bf16 rows [n][H], xs is empty */
   uint64_t counts;         /* i32 [E] pairs per local expert */
   uint64_t offsets;        /* i32 [E+1] exclusive prefix of counts */
   uint64_t padded_offsets; /* i32 [E+1] the same with every segment padded to block_m */
@@ -158,7 +172,8 @@ typedef struct afd_ws_layout {
   uint64_t num_tiles;      /* i32 [1] row tiles in use */
   uint64_t hist;           /* i32 router scratch */
   uint64_t hq, hs;         /* intermediate activations and their scales (MXFP4: down A tile
-                              images, scales inside, hs empty) */
+                              images, scales inside, hs empty; bf16 activations: 32 KiB bf16
+                              images of 128 rows x 128 K, hs empty) */
   uint64_t y;              /* bf16 [np_max][H] per-pair down outputs */
   int64_t np_max;          /* padded rows reserved: n*k + E*(block_m-1), rounded up */
   int32_t block_m;         /* row tile of the grouped GEMMs */
@@ -219,6 +234,7 @@ int afd_moe_ffn(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const
 /* The expert call on activations already quantized by afd_quant_act (fp8 activations on
  * the wire: A quantizes before the arena copy, the arena carries xq and xs, F reads them in
  * place). Same output as afd_moe_ffn on the bf16 x that afd_quant_act was given, bit for bit.
+ * A configuration with bf16 activations has no quantized form (AFD_ERR_UNSUPPORTED).
  * The activation format on the wire is the reference's TODO (scripts/run_asap.sh:110-111,
  * P/transport/layout.py:64 ACT_BYTES = 2). */
 int afd_moe_ffn_q(const afd_moe_cfg* cfg, const afd_expert_weights* weights, const uint8_t* xq,
@@ -320,7 +336,8 @@ int afd_job_set(afd_job* job, const afd_job* value, afd_stream_t stream);
 /* The activation quantizer of the expert call (quantize_routed_input,
  * mxfp4_flashinfer_trtllm_moe.py:59-61) on its own: x bf16 [n][H] -> q e4m3 [n][H] and s:
  * MXFP4 weights: u8 [n][H/32] UE8M0, the 4 of each 128-wide K stage as blocks 0, 2, 1, 3
- * (block j at byte 2(j & 1) | (j >> 1) of its group); FP8 block weights: f32 [n][H/128]. */
+ * (block j at byte 2(j & 1) | (j >> 1) of its group); FP8 block weights: f32 [n][H/128].
+ * Bf16 activations are not quantized (AFD_ERR_UNSUPPORTED). */
 int afd_quant_act(const afd_moe_cfg* cfg, const uint16_t* x, int32_t n, uint8_t* q, void* s,
                   afd_stream_t stream);
 

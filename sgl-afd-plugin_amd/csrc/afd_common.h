@@ -298,6 +298,9 @@ constexpr int kImgARows = 128, kImgBRows = 256;
 constexpr int kImgA = kImgData + kImgARows * 4;  // 16896
 constexpr int kImgB = kImgData + kImgBRows * 4;  // 17408
 constexpr int kImgK = 128;                        // K values per image
+// The W4A16 GEMMs' bf16 A block of one K stage (128 rows x 128 bf16, rows XOR-swizzled by
+// 16-byte chunk; afd_gemm_a16.hip): 32 KiB, no scales.
+constexpr int kImgA16 = kImgARows * kImgK * 2;
 // The MX GEMM copies an A image's 512 B of scales as a 1 KiB piece, reading the 512 B that
 // follow; buffers of A images keep that much readable memory after their last image.
 constexpr int kImgReadSlack = 512;
@@ -353,6 +356,9 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+
+// Every LDS read of this wavefront complete (lgkmcnt 0), copies left in flight.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 // wait_vmcnt<N> plus every LDS read of this wavefront complete (lgkmcnt 0).
 template <int N>

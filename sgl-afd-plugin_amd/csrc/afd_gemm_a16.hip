@@ -1,0 +1,509 @@
+// Grouped MXFP4-weight x bf16-activation GEMMs of the expert FFN on gfx950 (W4A16: the
+// activations stay bf16, nothing is quantized on the activation side).
+//
+//   gate_up: h[p, :] = bf16(act(x_t . Wg_e^T, x_t . Wu_e^T)) for every padded row p of expert
+//            e (t = token of the pair at row p), written as the down GEMM's bf16 A images.
+//   down:    y[p, :] = bf16(h_p . W2_e^T).
+//
+// The weights are the same MXFP4 tile images the W4A8 GEMMs read (afd_pack_mxfp4: 256 rows x
+// 128 K of e2m1 codes + UE8M0 scales per image). The matrix op is v_mfma_f32_32x32x16_bf16;
+// its weight operand is expanded in registers, right before the MFMAs that use it, by
+// v_cvt_scalef32_pk_bf16_fp4 (two e2m1 codes and the block scale -> two bf16, exact: every
+// e2m1 value times a power of two is a bf16), so the LDS and HBM keep 4.25 bits per weight.
+//
+// Tiling: a workgroup of 2 x WN wavefronts owns a 128 x (128 WN) output tile; wavefront
+// (wm, wn) owns 64 x 128 = 2 x 4 MFMA tiles of 32x32. A K stage is 128 wide: the bf16 A block
+// (128 rows x 256 B = 32 KiB, "A16 image") and the tile's WN/2 B images (17 KiB each) move
+// HBM -> LDS with direct global_load_lds copies in 1 KiB pieces into a ring of 2 stages (WN = 4,
+// 132 KiB) or 3 (WN = 2). The two wavefronts of a SIMD ping-pong at half-stage granularity (K
+// 64: 32 MFMAs of 32 clk per wavefront, the same phase length as the W4A8 kernel's 16 MFMAs of
+// 64 clk), so one of them always feeds the matrix pipe while the other reads its fragments.
+//
+// K order inside a 64-wide half stage c: lane half lk of an MFMA operand holds, in k-step s
+// (0..3), K [64 c + 32 lk + 8 s, +8): for the weights that is dword s of the lane's 16-byte
+// e2m1 chunk 2 c + lk of the row (one MX block, one scale), for the activations the bf16
+// chunk 8 c + 4 lk + s of the row. Both operands use the same K for the same (lane half,
+// element), so every product pairs matching elements.
+//
+// Persistent workgroups, the XCD-aware tile walk (static or dynamic) and the metadata
+// prefetch are those of the W4A8 kernels (afd_gemm_mx.hip).
+#include <type_traits>
+
+#include "afd_common.h"
+#include "afd_internal.h"
+
+namespace afd {
+
+namespace {
+
+enum { kGateUp = 0, kDown = 1, kGateUpParam = 2 };
+
+constexpr int kA16WalkRows = 4;
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+struct A16GemmArgs {
+  const uint8_t* a_img;         // down: bf16 A images [row tiles][K/128] of kImgA16 bytes
+  const uint16_t* a_rows;       // gate_up: bf16 token rows [n][K], gathered by sorted_pairs
+  const afd_job* rows_desc;     // gate_up: if set, a_rows is its x (read when the kernel runs)
+  int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
+  uint32_t topk_magic;          // div_magic(topk)
+  uint32_t ncb_magic;           // div_magic(walk_col_blocks<kA16WalkRows>(N / BN))
+  const uint8_t* b_img;         // B images [E][N/256][K/128]
+  const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
+  const int32_t* tile_expert;   // [row tiles]
+  const int32_t* num_tiles;     // [1]
+  const int32_t* padded_offsets;  // [E + 1]
+  const int32_t* counts;          // [E]
+  uint32_t* walk_ctr;             // [8] zeroed tile counters; nullptr: static walk
+  int K, N;
+  uint8_t* h_img;  // gate_up out: the down GEMM's A16 images [row tiles][N/256]
+  ActParams act;   // gate_up: the activation
+  uint16_t* y;     // down out: bf16 [np][N]
+};
+
+// byte offset of logical 16-byte chunk c (0..15, 8 bf16 each) of row r in an A16 image: the
+// 16 rows one 16-lane pass of an operand read covers (same logical chunk) land on 16 distinct
+// 16-byte bank groups
+__host__ __device__ __forceinline__ int img_a16_off(int r, int c) {
+  return r * 256 + ((c ^ (r & 15)) << 4);
+}
+
+template <int WN>
+struct A16Tile {
+  static_assert(WN == 2 || WN == 4, "tiles are 256 or 512 columns wide");
+  static constexpr int kWaves = 2 * WN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBM = kBlockM;  // 128 rows = one A16 image
+  static constexpr int kBN = 128 * WN;
+  static constexpr int kBImgs = WN / 2;  // 256-row B images per tile
+  static constexpr int kLdsA = kImgA16;
+  static constexpr int kStage = kLdsA + kBImgs * kImgB;
+  static constexpr int kStages = WN == 4 ? 2 : 3;
+  static constexpr int kLds = kStages * kStage;
+  // per wavefront and stage: kAQ pieces of the A block (4 rows each), kQP data pieces of each
+  // B image, and (wavefronts below kBImgs) the scale piece of image w
+  static constexpr int kAQ = (kImgA16 / 1024) / kWaves;
+  static constexpr int kQP = 16 / kWaves;
+  static constexpr int kPiecesMin = kAQ + kBImgs * kQP;  // pieces of a wavefront without scales
+  static constexpr int kYChunks = kBN / 8;
+  static_assert(kBM * kBN * 2 <= kLds, "down epilogue tile must fit the stages");
+  static_assert(kLds <= 160 * 1024, "LDS of one CU");
+  static_assert(2 * (kPiecesMin + 1) < 64, "vmcnt is a 6-bit counter");
+};
+
+// the 8 e2m1 codes of dword d (element 2i in the low nibble of byte i) times 2^(code - 127),
+// as the 8 bf16 of an MFMA operand (element i in half i % 2 of dword i / 2). The instruction
+// takes the scale's exponent field as the UE8M0 code, so `scale` is the code shifted into it.
+__device__ __forceinline__ v8bf expand_fp4(uint32_t d, float scale) {
+  v4i r;
+  r[0] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 0));
+  r[1] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 1));
+  r[2] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 2));
+  r[3] = __builtin_bit_cast(int, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(d, scale, 3));
+  return __builtin_bit_cast(v8bf, r);
+}
+
+template <int MODE, int WN>
+__global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16GemmArgs p) {
+  using T = A16Tile<WN>;
+  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[T::kLds];
+  const int t = threadIdx.x, lane = t & 63;
+  const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
+  const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
+  const int nt256 = p.N / kImgBRows;
+  const TileWalk<kA16WalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  __shared__ int claimed[2];
+  const int KT = p.K / kImgK;
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
+  const uint32_t voff = static_cast<uint32_t>(lane) * 16;
+  const uint16_t* a_rows = p.a_rows;
+  if (MODE != kDown && p.rows_desc != nullptr) a_rows = p.rows_desc->x;
+  const int bimg = wn / 2, brow = (wn % 2) * 128;
+
+  // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A block from the
+  // token rows: lane l copies, for its piece q, physical chunk l % 16 of row 4 (w kAQ + q) +
+  // l / 16, i.e. logical chunk (l % 16) ^ (row % 16), from the row's token. Padding rows (-1)
+  // read token 0; their results are never stored.
+  int sp_next[T::kAQ], e_next = 0, own_next = -1;
+  auto load_next = [&](int ii) {
+    int m, nn;
+    walk.at_dense(ii, m, nn);
+    e_next = p.tile_expert[m];
+    own_next = p.sorted_pairs[m * kBM + 64 * wm + lane];
+    if constexpr (MODE != kDown) {
+#pragma unroll
+      for (int q = 0; q < T::kAQ; ++q)
+        sp_next[q] = p.sorted_pairs[m * kBM + 4 * (w_u * T::kAQ + q) + (lane >> 4)];
+    }
+  };
+  int e_cur = 0, live_cur = 0;
+  uint32_t a_voff[T::kAQ] = {};
+  auto decode_next = [&]() {
+    e_cur = __builtin_amdgcn_readfirstlane(e_next);
+    live_cur = __popcll(__ballot(own_next >= 0));
+    if constexpr (MODE != kDown) {
+#pragma unroll
+      for (int q = 0; q < T::kAQ; ++q) {
+        const int r = 4 * (w_u * T::kAQ + q) + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        const uint32_t tok = sp_next[q] >= 0 ? div_by_magic(static_cast<uint32_t>(sp_next[q]), p.topk_magic) : 0u;
+        a_voff[q] = tok * static_cast<uint32_t>(p.K) * 2u + c * 16;
+      }
+    }
+  };
+  constexpr bool kEarlyStart = MODE != kDown;
+  const uint8_t* a_tile = nullptr;
+  const uint8_t* b_tile = nullptr;
+  auto copy_tile = [&](int mt, int nt, int64_t e) {
+    a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * kImgA16
+                           : reinterpret_cast<const uint8_t*>(a_rows);
+    b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
+  };
+  // this wavefront's copies of stage kt into ring slot kt % kStages: its A pieces, its data
+  // pieces of every B image, and for w < kBImgs the scale piece of image w
+  auto issue = [&](int kt) {
+    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+    static_for<T::kAQ>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int off = (w_u * T::kAQ + q) * 1024;
+      if constexpr (MODE != kDown)
+        lds_dma16(st + off, a_tile + int64_t(kt) * (kImgK * 2), a_voff[q]);
+      else
+        lds_dma16(st + off, a_tile + int64_t(kt) * kImgA16 + off, voff);
+    });
+    static_for<T::kBImgs * T::kQP>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int img = q / T::kQP;
+      const int off = (w_u * T::kQP + q % T::kQP) * 1024;
+      lds_dma16(st + T::kLdsA + img * kImgB + off, b_tile + (int64_t(img) * KT + kt) * kImgB + off, voff);
+    });
+    if (w_u < T::kBImgs)
+      lds_dma16(st + T::kLdsA + w_u * kImgB + kImgData,
+                b_tile + (int64_t(w_u) * KT + kt) * kImgB + kImgData, voff);
+  };
+  const int last = KT - 1;
+
+  const bool dynamic = p.walk_ctr != nullptr;
+  int i = walk.first, i_next = walk.first + walk.stride;
+  if (dynamic) {
+    if (t == 0) {
+      const uint32_t a = walk.claim_ticket(), b = walk.claim_ticket();
+      claimed[0] = walk.resolve(a);
+      claimed[1] = walk.resolve(b);
+    }
+    __syncthreads();
+    i = __builtin_amdgcn_readfirstlane(claimed[0]);
+    i_next = __builtin_amdgcn_readfirstlane(claimed[1]);
+  }
+  i = min(i, walk.tiles);
+  i_next = min(i_next, walk.tiles);
+  uint32_t ticket = 0;
+  // A tile's K loop starts with every ring slot filled: stages 0 .. kStages - 1 (clamped to
+  // the last stage) are issued before it, either during the previous tile's epilogue (gate_up)
+  // or at the start of the tile (down, whose epilogue stages its output through the ring).
+  auto issue_first = [&]() {
+    static_for<kStages>([&](auto sc) { issue(min(static_cast<int>(decltype(sc)::value), last)); });
+  };
+  if (i < walk.tiles) {
+    load_next(i);
+    decode_next();
+    if constexpr (kEarlyStart) {
+      int mt, nt;
+      walk.at_dense(i, mt, nt);
+      copy_tile(mt, nt, e_cur);
+      issue_first();
+    }
+  }
+  for (int i_after = walk.tiles; i < walk.tiles; i = i_next, i_next = i_after) {
+    int mt, nt;
+    walk.at_dense(i, mt, nt);
+    const bool has_next = i_next < walk.tiles;
+    const bool claims = dynamic && t == 0 && has_next;
+    const int m0 = mt * kBM, n0 = nt * kBN;
+    const int64_t e = e_cur;
+    int row_end = 0;
+    if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
+    const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
+    if (has_next) load_next(i_next);
+    if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
+
+    v16f acc[2][4];
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
+
+    // fragments of one half stage (K 64): A [s][i2] (8 bf16 each), the e2m1 chunks [j] and
+    // their scale codes
+    struct Frag {
+      v4i a[4][2];
+      v4i b[4];
+      uint32_t sb[4];
+    };
+    Frag f;
+    auto read_half = [&](int slot, int c) {
+      const uint8_t* abase = lds + slot * kStage;
+      const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
+      const int r0 = wm * 64 + lr;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2)
+          f.a[s][i2] = *reinterpret_cast<const v4i*>(abase + img_a16_off(r0 + 32 * i2, 8 * c + 4 * lk + s));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = brow + j * 32 + lr;
+        f.b[j] = *reinterpret_cast<const v4i*>(bbase + img_b_off(n, 2 * c + lk));
+        // block 2 c + lk of row n sits at byte scale_byte(2 c + lk) = 2 lk + c
+        f.sb[j] = bbase[kImgData + 4 * n + 2 * lk + c];
+      }
+    };
+    // the 32 MFMAs of a half stage (blocks of padding rows skipped)
+    auto mma_half = [&]() {
+      static_for<4>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        const float scale = __uint_as_float(f.sb[j] << 23);
+        static_for<4>([&](auto sc) {
+          constexpr int s = decltype(sc)::value;
+          const v8bf wb = expand_fp4(static_cast<uint32_t>(f.b[j][s]), scale);
+          static_for<2>([&](auto i2c) {
+            constexpr int i2 = decltype(i2c)::value;
+            if (i2 == 0 ? live_i0 : live_i1)
+              acc[i2][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                  wb, __builtin_bit_cast(v8bf, f.a[s][i2]), acc[i2][j], 0, 0, 0);
+          });
+        });
+      });
+    };
+
+    // Ping-pong over half stages hf = 2 kt + c (as the W4A8 kernel over stages): group 0 reads
+    // half hf + 1 while group 1 multiplies half hf, and the other way round; every wavefront
+    // meets the others at a barrier every phase. At the first half of stage kt >= 1 each group
+    // copies its pieces of stage kt + kStages - 1 into the slot of stage kt - 1, which both
+    // groups finished reading before the barrier that started the phase (clamped to the last
+    // stage: a clamped copy rewrites a slot with its own bytes, and keeps every wavefront's
+    // count of copies in flight the same at each wait). Before the barrier after which group
+    // 0 reads the first half of stage kt + 1, both groups have waited for their pieces of it:
+    // group 0 after its MFMAs of the half before, group 1 after its reads of it. The counted
+    // waits allow the kStages - 2 later stages in flight (a wavefront that also copies a
+    // scale piece waits for one piece more than it needs).
+    if constexpr (!kEarlyStart) issue_first();
+    wait_vmcnt<(kStages - 1) * T::kPiecesMin>();  // own pieces of stage 0 landed
+    __syncthreads();
+    const int halves = 2 * KT;
+    if (wm == 0) {
+      for (int hf = 0; hf < halves; ++hf) {
+        const int kt = hf >> 1, c = hf & 1;
+        if (claims && hf == halves - 1) ticket = walk.claim_ticket();
+        if (c == 0 && kt >= 1) issue(min(kt + kStages - 1, last));
+        read_half(kt % kStages, c);
+        wait_lds();  // own reads done (copies may be in flight)
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_half();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (c == 1) wait_vmcnt<(kStages - 2) * T::kPiecesMin>();  // own pieces of stage kt + 1
+        __syncthreads();
+      }
+      __syncthreads();
+    } else {
+      __syncthreads();
+      for (int hf = 0; hf < halves; ++hf) {
+        const int kt = hf >> 1, c = hf & 1;
+        if (c == 0 && kt >= 1) issue(min(kt + kStages - 1, last));
+        read_half(kt % kStages, c);
+        if (c == 1)
+          wait_vmcnt_lds<(kStages - 2) * T::kPiecesMin>();  // own reads, own pieces of stage kt + 1
+        else
+          wait_lds();
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_setprio(1);
+        mma_half();
+        __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+      }
+    }
+    wait_vmcnt<0>();  // every copy of this tile landed
+    if (claims) claimed[0] = walk.resolve(ticket);
+    __syncthreads();  // and every wavefront is done reading the stages
+    if (has_next) {
+      i_after = dynamic ? __builtin_amdgcn_readfirstlane(claimed[0])
+                        : min(i_next + walk.stride, walk.tiles);
+      decode_next();
+      if constexpr (kEarlyStart) {
+        int mt2, nt2;
+        walk.at_dense(i_next, mt2, nt2);
+        copy_tile(mt2, nt2, e_cur);
+        issue_first();
+      }
+    }
+
+    // Accumulator q of tile (i2, j): activation row 64 wm + 32 i2 + lane % 32, output column
+    // 128 wn + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4. Lane half lk holds columns
+    // 8 q4 + 4 lk .. + 3 of each 32-column tile; one v_permlane32_swap per pair of bf16 pairs
+    // gives lane half lk the whole 16-byte chunks 2 pr + lk (pr = 0, 1), in column order.
+    auto chunks_of = [&](const float (&h)[16], v4i (&chunk)[2]) {
+      uint32_t hb[4][2];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        hb[q4][0] = pk_bf16(h[4 * q4], h[4 * q4 + 1]);
+        hb[q4][1] = pk_bf16(h[4 * q4 + 2], h[4 * q4 + 3]);
+      }
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const auto d0 = __builtin_amdgcn_permlane32_swap(hb[2 * pr][0], hb[2 * pr + 1][0], false, false);
+        const auto d1 = __builtin_amdgcn_permlane32_swap(hb[2 * pr][1], hb[2 * pr + 1][1], false, false);
+        chunk[pr] = v4i{static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
+                        static_cast<int>(d1[1])};
+      }
+    };
+    if constexpr (MODE != kDown) {
+      // Column tiles j = 2 jj and 2 jj + 1 are the gate and up halves of one 64-row group of
+      // interleaved W13: the same 32 intermediate columns n0 / 2 + 64 wn + 32 jj + [0, 32).
+      // Their bf16 h chunks go to the down GEMM's A16 image of row tile mt and K stage
+      // column / 128, row 64 wm + 32 i2 + lr.
+      const int kt_down = p.N / kImgBRows;  // K stages of the down GEMM (I / 128)
+      auto store_h = [&](auto fn) {
+        static_for<2>([&](auto ic) {
+          constexpr int i2 = decltype(ic)::value;
+          const int row = wm * 64 + i2 * 32 + lr;
+          static_for<2>([&](auto jjc) {
+            constexpr int jj = decltype(jjc)::value;
+            float h[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) h[q] = fn(acc[i2][2 * jj][q], acc[i2][2 * jj + 1][q]);
+            v4i chunk[2];
+            chunks_of(h, chunk);
+            const int col0 = n0 / 2 + 64 * wn + 32 * jj;  // multiple of 32
+            uint8_t* img = p.h_img + (int64_t(mt) * kt_down + col0 / kImgK) * kImgA16;
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+              const int c = (col0 % kImgK) / 8 + 2 * pr + lk;
+              *reinterpret_cast<v4i*>(img + img_a16_off(row, c)) = chunk[pr];
+            }
+          });
+        });
+      };
+      if constexpr (MODE == kGateUpParam) {
+        if (p.act.act == AFD_ACT_SITU)
+          store_h([&](float g, float u) {
+            return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+          });
+        else
+          store_h([&](float g, float u) { return act_swiglu_limit(g, u, p.act.l); });
+      } else {
+        store_h([](float g, float u) { return act_swiglu(g, u); });
+      }
+    } else {
+      // bf16 y rows through LDS so the stores write whole rows (as the W4A8 down GEMM):
+      // chunk c of row r at physical chunk c ^ (r % 16); rows [0, nvalid) are real; the
+      // stores are non-temporal (y is read once, by the finalize).
+      const int nvalid = min(kBM, row_end - m0);
+      auto y_chunk = [](int r, int c) { return (r * T::kYChunks + (c ^ (r & 15))) * 16; };
+      static_for<2>([&](auto ic) {
+        constexpr int i2 = decltype(ic)::value;
+        const int row = wm * 64 + i2 * 32 + lr;
+        static_for<4>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          float h[16];
+#pragma unroll
+          for (int q = 0; q < 16; ++q) h[q] = acc[i2][j][q];
+          v4i chunk[2];
+          chunks_of(h, chunk);
+#pragma unroll
+          for (int pr = 0; pr < 2; ++pr)
+            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 128 + j * 32) / 8 + 2 * pr + lk)) = chunk[pr];
+        });
+      });
+      __syncthreads();
+#pragma unroll 4
+      for (int q = 0; q < kBM * T::kYChunks / T::kThreads; ++q) {
+        const int idx = q * T::kThreads + t;
+        const int row = idx / T::kYChunks, c = idx % T::kYChunks;
+        if (row < nvalid)
+          __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
+                                      reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int MODE, int WN>
+int launch_a16(const A16GemmArgs& p, int max_row_tiles, hipStream_t stream) {
+  using T = A16Tile<WN>;
+  static const int per_cu = [] {
+    int b = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, a16_gemm_kernel<MODE, WN>, T::kThreads,
+                                                     0) != hipSuccess ||
+        b < 1)
+      b = 1;
+    return b;
+  }();
+  const int max_tiles = max_row_tiles * (p.N / T::kBN);
+  A16GemmArgs a = p;
+  a.ncb_magic = div_magic(walk_col_blocks<kA16WalkRows>(p.N / T::kBN));
+  int grid = device_cu_count() * per_cu;
+  if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
+  hipLaunchKernelGGL((a16_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
+}
+
+template <int MODE>
+int launch_a16_any(const A16GemmArgs& p, int max_row_tiles, hipStream_t stream) {
+  if (p.N % A16Tile<4>::kBN == 0) return launch_a16<MODE, 4>(p, max_row_tiles, stream);
+  return launch_a16<MODE, 2>(p, max_row_tiles, stream);
+}
+
+A16GemmArgs a16_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws_layout& L) {
+  A16GemmArgs p = {};
+  p.topk = cfg.topk;
+  p.topk_magic = div_magic(cfg.topk);
+  p.act = act_params(cfg);
+  p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
+  p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
+  p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
+  p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
+  p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
+  return p;
+}
+
+}  // namespace
+
+int launch_a16_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                       const afd_ws_layout& L, const uint16_t* x, const afd_job* rows_desc,
+                       hipStream_t stream) {
+  A16GemmArgs p = a16_args(cfg, ws, L);
+  p.a_rows = x;
+  p.rows_desc = rows_desc;
+  p.b_img = static_cast<const uint8_t*>(wt.w13);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kGateUpWalkWord : nullptr;
+  p.K = cfg.hidden;
+  p.N = 2 * cfg.inter;
+  p.h_img = ws + L.hq;
+  return cfg.activation != AFD_ACT_SWIGLU ? launch_a16_any<kGateUpParam>(p, L.max_tiles, stream)
+                                         : launch_a16_any<kGateUp>(p, L.max_tiles, stream);
+}
+
+int launch_a16_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                    const afd_ws_layout& L, hipStream_t stream) {
+  A16GemmArgs p = a16_args(cfg, ws, L);
+  p.a_img = ws + L.hq;
+  p.b_img = static_cast<const uint8_t*>(wt.w2);
+  p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kDownWalkWord : nullptr;
+  p.K = cfg.inter;
+  p.N = cfg.hidden;
+  p.y = reinterpret_cast<uint16_t*>(ws + L.y);
+  return launch_a16_any<kDown>(p, L.max_tiles, stream);
+}
+
+}  // namespace afd

@@ -121,6 +121,15 @@ int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint
 int launch_mx_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                    const afd_ws_layout& L, int32_t n, hipStream_t stream);
 
+// Grouped MXFP4-weight x bf16-activation GEMMs (afd_gemm_a16.hip). x: the bf16 token rows
+// [n][H] (the job's, or a batch's staged in the workspace); with rows_desc != nullptr they are
+// that job descriptor's x, read when the kernel runs.
+int launch_a16_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                       const afd_ws_layout& L, const uint16_t* x, const afd_job* rows_desc,
+                       hipStream_t stream);
+int launch_a16_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
+                    const afd_ws_layout& L, hipStream_t stream);
+
 // Grouped FP8 128x128-block GEMMs (afd_gemm_fp8.hip).
 int launch_fp8_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,
                        const afd_ws_layout& L, const uint8_t* xq, const void* xs,

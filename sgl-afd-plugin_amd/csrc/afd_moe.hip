@@ -237,8 +237,12 @@ static int check_cfg(const afd_moe_cfg* cfg) {
   if (cfg->activation == AFD_ACT_SWIGLU_LIMIT && !(cfg->act_limit > 0.0f && cfg->act_limit < INFINITY))
     return AFD_ERR_ARG;
   if (cfg->tile_walk != AFD_WALK_STATIC && cfg->tile_walk != AFD_WALK_DYNAMIC) return AFD_ERR_ARG;
+  if (cfg->act_fmt != AFD_A_FP8 && cfg->act_fmt != AFD_A_BF16) return AFD_ERR_UNSUPPORTED;
+  if (cfg->act_fmt == AFD_A_BF16 && cfg->weight_fmt != AFD_W_MXFP4) return AFD_ERR_UNSUPPORTED;
   return AFD_OK;
 }
+
+static bool bf16_act(const afd_moe_cfg& cfg) { return cfg.act_fmt == AFD_A_BF16; }
 
 }  // namespace afd
 
@@ -267,6 +271,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   const int64_t H = cfg->hidden, I = cfg->inter, E = cfg->num_local;
   const int64_t pairs = int64_t(n) * cfg->topk;
   const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
+  const bool a16 = bf16_act(*cfg);
   const int64_t np_max = (pairs + E * (kBlockM - 1) + kBlockM - 1) / kBlockM * kBlockM;
   uint64_t o = 0;
   auto take = [&](uint64_t bytes) {
@@ -279,9 +284,10 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   // xq / xs: the per-token e4m3 rows and their scales (MXFP4: UE8M0 per 32, in stage order;
   // FP8 block: fp32 per 1x128). MXFP4: hq holds the down GEMM's A images (the h rows in
   // expert order, scales inside, hs empty); FP8 block: hq / hs the padded-row intermediate
-  // and its scales.
-  L.xq = take(uint64_t(n) * H);
-  L.xs = take(mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
+  // and its scales. bf16 activations: xq holds a batched call's bf16 rows (a single job's
+  // are read in place), hq the down GEMM's bf16 A images, xs and hs are empty.
+  L.xq = take(a16 ? uint64_t(n) * H * 2 : uint64_t(n) * H);
+  L.xs = take(a16 ? 0 : mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
   L.counts = take(E * 4);
   L.offsets = take((E + 1) * 4);
   L.padded_offsets = take((E + 1) * 4);
@@ -290,7 +296,9 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.tile_expert = take(uint64_t(np_max / kBlockM) * 4);
   L.num_tiles = take(4);
   L.hist = take(uint64_t(128) * E * 4);
-  L.hq = take(mx ? max_tiles * (I / kImgK) * kImgA + kImgReadSlack : uint64_t(np_max) * I);
+  L.hq = take(a16  ? max_tiles * (I / kImgK) * kImgA16
+               : mx ? max_tiles * (I / kImgK) * kImgA + kImgReadSlack
+                    : uint64_t(np_max) * I);
   L.hs = take(mx ? 0 : uint64_t(np_max) * (I / 128) * 4);
   L.y = take(uint64_t(np_max) * H * 2);
   L.total = o;
@@ -303,16 +311,19 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
 
 // job: the job's pointers and n by value, or its descriptor with job.n = n_cap. quantized:
 // the rows come quantized by afd_quant_act (xq / xs, or the descriptor's) instead of as bf16
-// x, which is quantized here.
+// x, which is quantized here. With bf16 activations the GEMMs read bf16 rows: staged_x (a
+// batch's rows, staged in the workspace) or else the job's x (or the descriptor's).
 static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weights,
                         const JobIn& job, bool quantized, const uint8_t* xq, const void* xs,
                         void* ws, uint64_t ws_bytes, afd_stream_t stream, void* const* ev,
-                        const Reply* answer = nullptr) {
+                        const Reply* answer = nullptr, const uint16_t* staged_x = nullptr) {
   if (job.n < 0 || job.n > 0x1ffff) return AFD_ERR_ARG;
   const int32_t n = static_cast<int32_t>(job.n);
   afd_ws_layout L;
   int st = afd_workspace_layout(cfg, n, &L);
   if (st != AFD_OK) return st;
+  const bool a16 = bf16_act(*cfg);
+  if (a16 && quantized) return AFD_ERR_UNSUPPORTED;  // bf16 activations have no quantized form
   if (!weights || !weights->w13 || !weights->w2) return AFD_ERR_ARG;
   if (cfg->weight_fmt == AFD_W_FP8_BLOCK && (!weights->s13 || !weights->s2)) return AFD_ERR_ARG;
   const bool rows_ok = quantized ? (xq && xs) : job.x != nullptr;
@@ -320,7 +331,7 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
   // the gate_up GEMMs address token rows with 32-bit byte offsets
-  if (uint64_t(n) * cfg->hidden > 0xffffffffull) return AFD_ERR_SHAPE;
+  if (uint64_t(n) * cfg->hidden * (a16 ? 2 : 1) > 0xffffffffull) return AFD_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto mark = [&](int i) -> int {
     if (ev && ev[i]) AFD_CHECK_HIP(hipEventRecord(static_cast<hipEvent_t>(ev[i]), s));
@@ -337,18 +348,24 @@ static int moe_ffn_impl(const afd_moe_cfg* cfg, const afd_expert_weights* weight
       reply = *answer;
       reply.arrive = call_counters(wsb, L) + kArriveWord;
     }
-    st = launch_route_quant(job, !quantized, *cfg, wsb, L, s,
+    st = launch_route_quant(job, !quantized && !a16, *cfg, wsb, L, s,
                             ev && ev[1] ? static_cast<hipEvent_t>(ev[1]) : nullptr);
     if (st != AFD_OK) return st;
     if ((st = mark(2)) != AFD_OK) return st;
-    const uint8_t* aq = quantized ? xq : wsb + L.xq;
-    const void* as = quantized ? xs : static_cast<const void*>(wsb + L.xs);
-    const afd_job* rows_desc = quantized ? job.desc : nullptr;
-    st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s)
-            : launch_fp8_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s);
+    if (a16) {
+      const uint16_t* rows = staged_x != nullptr ? staged_x : job.x;
+      st = launch_a16_gate_up(*cfg, *weights, wsb, L, rows, staged_x ? nullptr : job.desc, s);
+    } else {
+      const uint8_t* aq = quantized ? xq : wsb + L.xq;
+      const void* as = quantized ? xs : static_cast<const void*>(wsb + L.xs);
+      const afd_job* rows_desc = quantized ? job.desc : nullptr;
+      st = mx ? launch_mx_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s)
+              : launch_fp8_gate_up(*cfg, *weights, wsb, L, aq, as, rows_desc, s);
+    }
     if (st != AFD_OK || (st = mark(3)) != AFD_OK) return st;
-    st = mx ? launch_mx_down(*cfg, *weights, wsb, L, n, s)
-            : launch_fp8_down(*cfg, *weights, wsb, L, n, s);
+    st = a16  ? launch_a16_down(*cfg, *weights, wsb, L, s)
+         : mx ? launch_mx_down(*cfg, *weights, wsb, L, n, s)
+              : launch_fp8_down(*cfg, *weights, wsb, L, n, s);
     if (st != AFD_OK || (st = mark(4)) != AFD_OK) return st;
     st = launch_finalize(reinterpret_cast<const uint16_t*>(wsb + L.y),
                          reinterpret_cast<const int32_t*>(wsb + L.pair_pos), job, cfg->topk,
@@ -441,7 +458,14 @@ extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weight
   Reply answer = {};
   int64_t total = 0;
   bool any_done = false;
-  const bool quantized = jobs[0].x == nullptr;  // every job: x, or xq and xs
+  // every non-empty job gives x, or xq and xs, as the first non-empty one does (an empty job's
+  // pointers may be null and say nothing)
+  bool quantized = false;
+  for (int b = 0; b < num_jobs; ++b)
+    if (jobs[b].n > 0) {
+      quantized = jobs[b].x == nullptr;
+      break;
+    }
   for (int b = 0; b < num_jobs; ++b) {
     const afd_batch_job& jb = jobs[b];
     if (jb.n < 0 || jb.reserved != 0) return AFD_ERR_ARG;
@@ -472,21 +496,37 @@ extern "C" int afd_moe_ffn_batch(const afd_moe_cfg* cfg, const afd_expert_weight
       break;
     }
   answer.count = any_done ? num_jobs : 0;
-  if (!quantized)
-    return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream,
-                        nullptr, any_done ? &answer : nullptr);
-  // quantized rows: staged one job after another into the workspace's xq / xs, which the
-  // call then reads as one job's
   afd_ws_layout L;
   int st = afd_workspace_layout(cfg, static_cast<int32_t>(total), &L);
   if (st != AFD_OK) return st;
+  const bool a16 = bf16_act(*cfg);
+  if (!quantized && !a16)
+    return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream,
+                        nullptr, any_done ? &answer : nullptr);
+  if (quantized && a16) return AFD_ERR_UNSUPPORTED;
   if (!ws) return AFD_ERR_ARG;
   if (ws_bytes < L.total) return AFD_ERR_WORKSPACE;
+  uint8_t* wsb = static_cast<uint8_t*>(ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a16) {
+    // bf16 rows of the GEMMs: staged one job after another into the workspace's xq, which the
+    // gate_up GEMM then gathers from as one job's rows (the router, the finalize and the output
+    // rows still go through each job's own ids, w and out)
+    const uint64_t row = uint64_t(cfg->hidden) * 2;
+    for (int b = 0; b < num_jobs; ++b) {
+      const uint64_t n = static_cast<uint64_t>(jobs[b].n);
+      if (n == 0) continue;
+      AFD_CHECK_HIP(hipMemcpyAsync(wsb + L.xq + uint64_t(job.first[b]) * row, jobs[b].x, n * row,
+                                   hipMemcpyDeviceToDevice, s));
+    }
+    return moe_ffn_impl(cfg, weights, job, false, nullptr, nullptr, ws, ws_bytes, stream, nullptr,
+                        any_done ? &answer : nullptr, reinterpret_cast<const uint16_t*>(wsb + L.xq));
+  }
+  // quantized rows: staged one job after another into the workspace's xq / xs, which the
+  // call then reads as one job's
   const uint64_t q_row = uint64_t(cfg->hidden);
   const uint64_t s_row = cfg->weight_fmt == AFD_W_MXFP4 ? uint64_t(cfg->hidden / 32)
                                                         : uint64_t(cfg->hidden / 128) * 4;
-  uint8_t* wsb = static_cast<uint8_t*>(ws);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   for (int b = 0; b < num_jobs; ++b) {
     const uint64_t n = static_cast<uint64_t>(jobs[b].n);
     if (n == 0) continue;
@@ -526,6 +566,7 @@ extern "C" int afd_quant_act(const afd_moe_cfg* cfg, const uint16_t* x, int32_t 
                              void* s, afd_stream_t stream) {
   int st = check_cfg(cfg);
   if (st != AFD_OK) return st;
+  if (bf16_act(*cfg)) return AFD_ERR_UNSUPPORTED;  // bf16 activations are not quantized
   if (n < 0 || n > 0x1ffff) return AFD_ERR_ARG;
   if (n > 0 && (!x || !q || !s)) return AFD_ERR_ARG;
   return launch_quant_act(*cfg, x, n, q, s, static_cast<hipStream_t>(stream));

@@ -25,6 +25,8 @@ AFD_ERR_WORKSPACE = -5
 AFD_W_MXFP4 = 1
 AFD_W_FP8_BLOCK = 2
 
+AFD_A_FP8, AFD_A_BF16 = 0, 1
+
 AFD_ACT_SWIGLU = 0
 AFD_ACT_SITU = 1
 AFD_ACT_SWIGLU_LIMIT = 2
@@ -34,7 +36,7 @@ AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 AFD_WALK_STATIC, AFD_WALK_DYNAMIC = 0, 1
 
 # afd_abi_version() of the library these structures match
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # Every entry point include/afd.h declares; tests check the library exports all of them.
 EXPORTED = (
@@ -94,6 +96,7 @@ class AfdMoeCfg(ctypes.Structure):
         ("act_alpha", ctypes.c_float),
         ("act_limit", ctypes.c_float),
         ("tile_walk", ctypes.c_int32),
+        ("act_fmt", ctypes.c_int32),
     ]
 
 

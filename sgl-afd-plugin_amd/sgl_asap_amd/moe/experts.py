@@ -171,6 +171,10 @@ def repack_fp8_block_experts(w13: torch.Tensor, s13: torch.Tensor, w2: torch.Ten
 ACTIVATIONS = {"silu": _lib.AFD_ACT_SWIGLU, "situ": _lib.AFD_ACT_SITU}
 
 
+# the fp8 activation format each weight format's GEMMs read by default
+FP8_ACT = {"mxfp4": "mxfp8", "fp8_block": "fp8_1x128"}
+
+
 def moe_cfg(
     weights: ExpertWeights,
     top_k: int,
@@ -178,12 +182,23 @@ def moe_cfg(
     activation: str = "silu",
     gemm1_alpha: Optional[float] = None,
     gemm1_clamp_limit: Optional[float] = None,
+    act_format: Optional[str] = None,
 ) -> _lib.AfdMoeCfg:
     """The C config of a layer. ``activation`` is FusedMoE's ("silu": SwiGLU; "situ": SiTU
     with ``gemm1_alpha`` = its beta and ``gemm1_clamp_limit`` = its linear_beta, as the
     reference's ERNIE 5.5 experts pass them, P/srt/models/ernie55.py:43-55). "silu" with a
     ``gemm1_clamp_limit`` L is SwiGLU with a limit, silu(min(gate, L)) * clamp(up, -L, L):
-    DeepSeek-V4's ``swiglu_limit`` (P/srt/models/deepseek_v4.py:63)."""
+    DeepSeek-V4's ``swiglu_limit`` (P/srt/models/deepseek_v4.py:63). ``act_format``: the
+    precision of the GEMMs' activations, the weight format's fp8 form by default ("mxfp8" for
+    MXFP4, "fp8_1x128" for FP8 blocks, the MoE methods' default quantization) or "bf16" for
+    MXFP4 weights (W4A16: the reference's humming experts, scripts/run_ep.sh:4, README.md:25)."""
+    fp8 = FP8_ACT[weights.fmt]
+    if act_format not in (None, fp8, "bf16"):
+        raise ValueError(f"activation format {act_format!r} for {weights.fmt} weights "
+                         f"(supported: {fp8!r}, 'bf16')")
+    if act_format == "bf16" and weights.fmt != "mxfp4":
+        raise NotImplementedError(f"bf16 activations with {weights.fmt} weights")
+    act_fmt = _lib.AFD_A_BF16 if act_format == "bf16" else _lib.AFD_A_FP8
     if activation not in ACTIVATIONS:
         raise NotImplementedError(f"activation {activation!r} (supported: {sorted(ACTIVATIONS)})")
     alpha = limit = 0.0
@@ -204,7 +219,7 @@ def moe_cfg(
             raise ValueError(f"SiTU constants must be positive and finite, got {alpha}, {limit}")
     return _lib.AfdMoeCfg(
         weights.hidden, weights.inter, top_k, expert_lo, weights.num_local, WEIGHT_FORMATS[weights.fmt],
-        code, alpha, limit,
+        code, alpha, limit, _lib.AFD_WALK_STATIC, act_fmt,
     )
 
 
@@ -334,6 +349,10 @@ class AfdExperts(torch.nn.Module):
     fixed share of the tiles, best when the call has the GPU to itself; "dynamic" hands them
     out from per-XCD counters, for a GPU shared with other streams' kernels or parked stream
     waits (the FFN scheduler's setting). Results are identical bit for bit.
+
+    ``act_format``: the activation precision of the GEMMs (``moe_cfg``): by default the
+    weight format's fp8 form, which the call quantizes x and h to; "bf16" (MXFP4 weights)
+    keeps x as it is and rounds h to bf16 (W4A16).
     """
 
     def __init__(
@@ -349,6 +368,7 @@ class AfdExperts(torch.nn.Module):
         gemm1_clamp_limit: Optional[float] = None,
         swiglu_limit: Optional[float] = None,
         tile_walk: str = "static",
+        act_format: Optional[str] = None,
     ):
         super().__init__()
         if swiglu_limit is not None:  # DeepSeek-V4's FusedMoE argument: the SwiGLU clamp limit
@@ -365,7 +385,7 @@ class AfdExperts(torch.nn.Module):
         self.weights = weights
         self.n_max = n_max
         self.activation = activation
-        self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit)
+        self.cfg = moe_cfg(weights, top_k, local.start, activation, gemm1_alpha, gemm1_clamp_limit, act_format)
         self.tile_walk = tile_walk
         self.layout = workspace_layout(self.cfg, n_max)
         self._batch_bytes = {n_max: self.layout["total"]}  # workspace bytes per batch capacity
@@ -560,11 +580,15 @@ class AfdExperts(torch.nn.Module):
     @property
     def act_format(self) -> str:
         """The activation format of this layer's expert call: "mxfp8" (e4m3 + UE8M0 per 32,
-        MXFP4 weights) or "fp8_1x128" (e4m3 + fp32 per 128, FP8 block weights)."""
-        return "mxfp8" if self.weights.fmt == "mxfp4" else "fp8_1x128"
+        MXFP4 weights), "fp8_1x128" (e4m3 + fp32 per 128, FP8 block weights) or "bf16"."""
+        if self.cfg.act_fmt == _lib.AFD_A_BF16:
+            return "bf16"
+        return FP8_ACT[self.weights.fmt]
 
     def act_scale_shape(self, n: int):
-        """Shape and dtype of the activation scales of n tokens."""
+        """Shape and dtype of the activation scales of n tokens (fp8 activation formats)."""
+        if self.act_format == "bf16":
+            raise NotImplementedError("bf16 activations are not quantized: they have no scales")
         return act_scale_shape(self.act_format, n, self.hidden_size)
 
     def quant_act(self, x: torch.Tensor, q: Optional[torch.Tensor] = None, s: Optional[torch.Tensor] = None):
@@ -572,6 +596,8 @@ class AfdExperts(torch.nn.Module):
         stream: bf16 x [n, H] -> (q e4m3 codes uint8 [n, H], s scales)."""
         if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.hidden_size:
             raise TypeError(f"the expert path takes bf16 [n, {self.hidden_size}] activations, got {x.dtype} {tuple(x.shape)}")
+        if self.act_format == "bf16":
+            raise NotImplementedError("a layer with bf16 activations does not quantize them")
         return _quant_act(self.cfg, self.act_format, x, q, s, None)
 
     def forward_q(self, xq: torch.Tensor, xs: torch.Tensor, topk_output, out: Optional[torch.Tensor] = None):

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_functions():
         assert hasattr(L, name), name
-    assert L.afd_abi_version() == _lib.ABI_VERSION == 3
+    assert L.afd_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_status_strings():
@@ -56,6 +56,48 @@ def test_workspace_layout_dsv4_rank():
                            "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert L["total"] >= L["y"] + L["np_max"] * 4096 * 2
+
+
+def test_workspace_layout_bf16_activations():
+    """W4A16 (MXFP4 weights, bf16 activations): xq holds a batch's bf16 rows, xs is empty, hq
+    one 32 KiB bf16 A image per row tile and 128-wide K stage of h, hs empty."""
+    cfg = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_MXFP4, _lib.AFD_ACT_SWIGLU, 0.0, 0.0,
+                         _lib.AFD_WALK_STATIC, _lib.AFD_A_BF16)
+    L = workspace_layout(cfg, 16384)
+    tiles = L["max_tiles"]
+    assert L["xq"] == 0 and L["xs"] == 16384 * 4096 * 2
+    assert L["counts"] == L["xs"]  # no scales
+    assert L["hs"] - L["hq"] == tiles * (2048 // 128) * 128 * 128 * 2
+    assert L["y"] == L["hs"]
+    fp8 = workspace_layout(_lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_MXFP4), 16384)
+    assert (fp8["np_max"], fp8["max_tiles"]) == (L["np_max"], L["max_tiles"])
+
+
+def test_activation_format_checks():
+    out = _lib.AfdWsLayout()
+    L = _lib.lib()
+    bf16_fp8w = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_FP8_BLOCK, 0, 0.0, 0.0, 0, _lib.AFD_A_BF16)
+    unknown = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_MXFP4, 0, 0.0, 0.0, 0, 2)
+    for cfg in (bf16_fp8w, unknown):
+        assert L.afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) == _lib.AFD_ERR_UNSUPPORTED
+    # bf16 activations are not quantized: afd_quant_act refuses before touching any pointer
+    a16 = _lib.AfdMoeCfg(256, 128, 2, 0, 8, _lib.AFD_W_MXFP4, 0, 0.0, 0.0, 0, _lib.AFD_A_BF16)
+    assert L.afd_quant_act(ctypes.byref(a16), None, 0, None, None, None) == _lib.AFD_ERR_UNSUPPORTED
+
+
+def test_python_activation_formats():
+    from sgl_asap_amd.moe.experts import ExpertWeights, moe_cfg
+
+    mx = ExpertWeights("mxfp4", 4, 256, 128, None, None, None, None)
+    fp8 = ExpertWeights("fp8_block", 4, 256, 128, None, None, None, None)
+    assert moe_cfg(mx, 2, 0).act_fmt == _lib.AFD_A_FP8
+    assert moe_cfg(mx, 2, 0, act_format="mxfp8").act_fmt == _lib.AFD_A_FP8
+    assert moe_cfg(mx, 2, 0, act_format="bf16").act_fmt == _lib.AFD_A_BF16
+    assert moe_cfg(fp8, 2, 0, act_format="fp8_1x128").act_fmt == _lib.AFD_A_FP8
+    with pytest.raises(ValueError):
+        moe_cfg(mx, 2, 0, act_format="fp8_1x128")
+    with pytest.raises(NotImplementedError):
+        moe_cfg(fp8, 2, 0, act_format="bf16")
 
 
 def test_bad_configs_rejected_on_host():

@@ -1,0 +1,293 @@
+"""GPU parity of the expert call with bf16 activations (W4A16: MXFP4 weights, the activations
+kept bf16, h rounded to bf16) against the fp32 CPU oracle run with ``act="bf16"``.
+
+Bars: routing bit-exact (the same router as the fp8 path); the output within rel-L2 <= 1e-2 of
+the oracle (the weight expansion is exact, so the remaining difference is fp32 summation order
+and the bf16 rounding of h and y at different sums); tokens with no local expert exactly 0;
+the h images decoded from the workspace within the same bar of the oracle's h. At the
+DeepSeek-V4 F-rank size (16384 tokens): the tokens of 4 experts against the oracle, and the
+size-independent properties of the fp8 path's full-size test (subset and permutation rows,
+doubling the weights, the descriptor call, the static and dynamic walks bit-identical).
+Batched, answering and descriptor calls are bit-identical to the plain call.
+"""
+
+import ctypes
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import bits16, dev, rel_l2, say
+from oracle import experts as OX
+from oracle import formats as F
+from sgl_asap_amd import workloads as W
+from sgl_asap_amd.moe.experts import AfdExperts, new_job_desc, pack_mxfp4_experts, release_workspaces, set_job
+from sgl_asap_amd.moe.topk import StandardTopKOutput
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 1e-2
+
+
+def mx_deq(w13, w2):
+    c13, s13 = F.mx_quantize(w13.numpy(), "e2m1")
+    c2, s2 = F.mx_quantize(w2.numpy(), "e2m1")
+    return F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1")
+
+
+def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed, zipf=None, situ=None,
+             swiglu_limit=None, tile_walk="static"):
+    say(f"a16 H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} "
+        f"seed={seed} zipf={zipf} situ={situ} swiglu_limit={swiglu_limit} walk={tile_walk}")
+    gen = W.generator("cpu", seed)
+    x = W.tokens(n, hidden, gen, "cpu")
+    if zipf is None:
+        ids, w = W.route_uniform(n, num_experts, k, gen, "cpu")
+    else:
+        ids, w = W.route_zipf(n, num_experts, k, zipf, gen, "cpu")
+    w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
+    weights = pack_mxfp4_experts(w13, w2, device=dev())
+    act_kw, oact = {}, {}
+    if situ is not None:
+        act_kw = dict(activation="situ", gemm1_alpha=situ[0], gemm1_clamp_limit=situ[1])
+        oact = dict(activation="situ", act_alpha=situ[0], act_limit=situ[1])
+    if swiglu_limit is not None:
+        act_kw = dict(swiglu_limit=swiglu_limit)
+        oact = dict(activation="swiglu_limit", act_limit=swiglu_limit)
+    experts = AfdExperts(num_experts, k, 0, range(e_lo, e_lo + num_local), weights, n_max=max(n, 1),
+                         act_format="bf16", tile_walk=tile_walk, **act_kw)
+    assert experts.act_format == "bf16"
+    out = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
+    torch.cuda.synchronize()
+    w13d, w2d = mx_deq(w13, w2)
+    ref, parts = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13d, w2d, e_lo, act="bf16", return_parts=True, **oact)
+    return experts, out, ref, parts, (x, ids, w)
+
+
+def assert_close(out, ref, ids, local):
+    got = F.bf16_to_f32(bits16(out))
+    want = F.bf16_to_f32(ref)
+    err = rel_l2(got, want)
+    say(f"rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL, err
+    none_local = ~((ids >= local.start) & (ids < local.stop)).any(axis=1)
+    assert not got[none_local].any(), "tokens with no local expert must be exactly 0"
+    return err
+
+
+def h_from_images(experts, n, rows):
+    """The gate_up GEMM's h rows in padded expert order, decoded from the workspace's bf16 A
+    images: one 32 KiB image per (row tile, 128-wide K stage), row r at r * 256 B, logical
+    16-byte chunk c at physical chunk c ^ (r % 16)."""
+    inter = experts.intermediate_size
+    stages = inter // 128
+    tiles = (rows + 127) // 128
+    raw = experts.ws_view("hq", torch.uint8, tiles * stages * 32768, n).cpu().numpy()
+    img = raw.reshape(tiles, stages, 128, 16, 16)  # [tile][stage][row][physical chunk][byte]
+    r = np.arange(128)
+    logical = np.arange(16)[None, :] ^ (r[:, None] & 15)  # physical chunk of logical chunk c
+    ordered = img[:, :, r[:, None], logical, :]  # [tile][stage][row][logical chunk][byte]
+    h = ordered.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, stages * 256).view(np.uint16)
+    return F.bf16_to_f32(h[:rows])
+
+
+def test_tiny_layer_a16():
+    """The tiny CPU-runnable layer (H256 I128, 8 experts, top-2, 64 tokens) with bf16
+    activations: output and h against the oracle, routing bit-exact."""
+    s = W.SHAPES["tiny"]
+    experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k,
+                                                     s.tokens, seed=0)
+    assert_close(out, ref, ids.numpy(), s.local)
+    n, k = ids.shape
+    pos = experts.ws_view("pair_pos", torch.int32, n * k, n).cpu().numpy()
+    assert np.array_equal(pos, parts["route"]["pair_pos"])
+    sp = parts["route"]["sorted_pairs"]
+    real = sp >= 0
+    h = h_from_images(experts, n, len(sp))
+    err = rel_l2(h[real], parts["h"][real])
+    say(f"h rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+
+
+def test_a16_differs_from_fp8_activations():
+    """The bf16 path is not the fp8 path under another name: the same layer with MXFP8
+    activations gives different bits, and lies farther from the bf16 oracle."""
+    s = W.SHAPES["tiny"]
+    experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k,
+                                                     s.tokens, seed=1)
+    fp8 = AfdExperts(s.num_experts, s.top_k, 0, s.local, experts.weights, n_max=s.tokens)
+    out8 = fp8(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
+    torch.cuda.synchronize()
+    assert not np.array_equal(bits16(out), bits16(out8))
+    want = F.bf16_to_f32(ref)
+    assert rel_l2(F.bf16_to_f32(bits16(out)), want) < rel_l2(F.bf16_to_f32(bits16(out8)), want)
+
+
+@pytest.mark.parametrize(
+    "hidden,inter,num_experts,e_lo,num_local,k,n,seed",
+    [
+        (512, 256, 32, 8, 16, 4, 300, 1),      # down N = 512: 512-column tiles; gate_up N = 512
+        (256, 128, 16, 0, 16, 8, 1, 2),        # one token; 256-column tiles in both GEMMs
+        (1024, 512, 64, 16, 16, 6, 513, 3),
+        (2048, 1024, 32, 0, 8, 8, 256, 4),
+        (4096, 512, 256, 0, 4, 8, 64, 10),
+        (768, 384, 16, 0, 16, 2, 129, 5),      # down N = 768 (256-column tiles), K stages 6 / 3
+    ],
+)
+def test_a16_layers(hidden, inter, num_experts, e_lo, num_local, k, n, seed):
+    experts, out, ref, parts, (x, ids, w) = run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed)
+    assert_close(out, ref, ids.numpy(), range(e_lo, e_lo + num_local))
+
+
+def draw(case: int) -> dict:
+    rng = random.Random(5100 + case)
+    num_experts = rng.choice([8, 16, 32, 64])
+    num_local = rng.randint(1, min(num_experts, 24))
+    spec = dict(
+        hidden=256 * rng.randint(1, 6),
+        inter=128 * rng.randint(1, 6),
+        num_experts=num_experts,
+        num_local=num_local,
+        e_lo=rng.randint(0, num_experts - num_local),
+        k=rng.randint(1, min(8, num_experts)),
+        n=rng.choice([1, 2, 31, 64, 127, 128, 129, 255, 300, 777]),
+        zipf=rng.choice([None, 1.2]),
+        tile_walk=rng.choice(["static", "dynamic"]),
+    )
+    act = rng.choice(["silu", "situ", "limit"])
+    if act == "situ":
+        spec["situ"] = (rng.choice([0.5, 2.0]), rng.choice([0.25, 3.0]))
+    if act == "limit":
+        spec["swiglu_limit"] = rng.choice([0.3, 1.0])
+    return spec
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_a16_random_layer(case):
+    """Seeded random shapes: hidden 256-1536, inter 128-768 (both tile widths, 1-12 K stages),
+    token counts around the 128-row tile edge, partial local ranges, top-1 to top-8, uniform
+    and Zipf routing, the three activations, both tile walks."""
+    s = draw(case)
+    extra = {k: s[k] for k in ("situ", "swiglu_limit") if k in s}
+    experts, out, ref, parts, (x, ids, w) = run_case(
+        s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], 9100 + case,
+        zipf=s["zipf"], tile_walk=s["tile_walk"], **extra)
+    assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
+
+
+def test_a16_walks_batch_answer_descriptor_identical():
+    """Static and dynamic walks, a batched call (with an empty first job), the answering call
+    and the descriptor call all give the plain call's bits."""
+    experts, out, ref, parts, (x, ids, w) = run_case(1024, 512, 32, 0, 16, 8, 700, seed=41, zipf=1.2)
+    xd, idsd, wd = x.to(dev()), ids.to(torch.int32).to(dev()), w.to(dev())
+    base = bits16(out)
+    experts.tile_walk = "dynamic"
+    dyn = experts(xd, StandardTopKOutput(wd, idsd))
+    experts.tile_walk = "static"
+    cuts = [0, 0, 250, 251, 700]  # an empty first job, then 250, 1 and 449 tokens
+    jobs = [(xd[a:b], StandardTopKOutput(wd[a:b], idsd[a:b])) for a, b in zip(cuts[:-1], cuts[1:])]
+    outs = experts.forward_batch(jobs)
+    done = torch.zeros(1, dtype=torch.int64, device=dev())
+    ans = torch.empty_like(out)
+    experts.call_ptrs(700, xd.data_ptr(), 0, idsd.data_ptr(), wd.data_ptr(), ans.data_ptr(),
+                      torch.cuda.current_stream().cuda_stream, done_ptr=done.data_ptr(), done_value=7)
+    desc = new_job_desc(dev())
+    got = torch.empty_like(out)
+    set_job(desc, x=xd, ids=idsd, w=wd, out=got)
+    experts.call_job(desc, 700)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits16(dyn), base)
+    assert np.array_equal(np.concatenate([bits16(o) for o in outs]), base)
+    assert np.array_equal(bits16(ans), base) and int(done.item()) == 7
+    assert np.array_equal(bits16(got), base)
+
+
+def test_a16_has_no_quantized_form():
+    s = W.SHAPES["tiny"]
+    gen = W.generator("cpu", 3)
+    w13, w2 = W.expert_weights(s.num_local, s.hidden, s.inter, gen, "cpu")
+    experts = AfdExperts(s.num_experts, s.top_k, 0, s.local, pack_mxfp4_experts(w13, w2, device=dev()),
+                         n_max=s.tokens, act_format="bf16")
+    x = W.tokens(4, s.hidden, gen, "cpu").to(dev())
+    with pytest.raises(NotImplementedError):
+        experts.quant_act(x)
+    q = torch.zeros(4, s.hidden, dtype=torch.uint8, device=dev())
+    sc = torch.zeros(4, s.hidden // 32, dtype=torch.uint8, device=dev())
+    ids = torch.zeros(4, s.top_k, dtype=torch.int32, device=dev())
+    w = torch.ones(4, s.top_k, device=dev())
+    ws = experts.workspace()
+    out = torch.empty(4, s.hidden, dtype=torch.bfloat16, device=dev())
+    from sgl_asap_amd import _lib
+    st = _lib.lib().afd_moe_ffn_q(ctypes.byref(experts.cfg), ctypes.byref(experts._wstruct), q.data_ptr(),
+                                  sc.data_ptr(), ids.data_ptr(), w.data_ptr(), 4, ws.data_ptr(), ws.numel(),
+                                  out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.AFD_ERR_UNSUPPORTED
+
+
+@pytest.fixture(scope="module")
+def dsv4_a16():
+    shape = W.SHAPES["dsv4_rank"]
+    say(f"full-size W4A16 layer {shape.name}: packing weights")
+    gen = W.generator("cpu", 1)
+    w13, w2 = W.expert_weights(shape.num_local, shape.hidden, shape.inter, gen, "cpu")
+    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, pack_mxfp4_experts(w13, w2, device=dev()),
+                         n_max=shape.tokens, act_format="bf16")
+    x, ids, w = W.job(shape, seed=0, device="cpu")
+    job = (x.to(dev()), ids.to(torch.int32).to(dev()), w.to(torch.float32).to(dev()))
+    out = experts(job[0], StandardTopKOutput(job[2], job[1]))
+    torch.cuda.synchronize()
+    yield shape, experts, (w13, w2), (x, ids, w), job, out
+    del experts
+    release_workspaces()
+    torch.cuda.empty_cache()
+
+
+def call(experts, x, ids, w):
+    out = experts(x.contiguous(), StandardTopKOutput(w.contiguous(), ids.contiguous()))
+    torch.cuda.synchronize()
+    return out
+
+
+def test_dsv4_a16_properties(dsv4_a16):
+    shape, experts, _, _, (x, ids, w), out = dsv4_a16
+    say(f"{shape.name} W4A16: subset / permutation rows, doubled weights, descriptor, dynamic walk")
+    full = bits16(out)
+    g = torch.Generator().manual_seed(5)
+    sub = torch.randperm(shape.tokens, generator=g)[:3000].sort().values.to(dev())
+    assert np.array_equal(bits16(call(experts, x[sub], ids[sub], w[sub])), full[sub.cpu().numpy()])
+    perm = torch.randperm(shape.tokens, generator=g).to(dev())
+    assert np.array_equal(bits16(call(experts, x[perm], ids[perm], w[perm])), full[perm.cpu().numpy()])
+    assert np.array_equal(bits16(call(experts, x, ids, 2 * w)), bits16(out * 2))
+    desc = new_job_desc(dev())
+    got = torch.empty_like(out)
+    set_job(desc, x=x, ids=ids, w=w, out=got)
+    experts.call_job(desc, shape.tokens)
+    experts.tile_walk = "dynamic"
+    dyn = call(experts, x, ids, w)
+    experts.tile_walk = "static"
+    assert np.array_equal(bits16(got), full)
+    assert np.array_equal(bits16(dyn), full)
+
+
+def test_dsv4_a16_subset_against_oracle(dsv4_a16):
+    """Tokens whose local experts all lie in [0, 4) (plus tokens with no local expert) against
+    the oracle run with those 4 experts only."""
+    shape, experts, (w13, w2), (xc, idsc, wc), _, out = dsv4_a16
+    say(f"{shape.name} W4A16: tokens of 4 experts against the oracle")
+    lo, keep = shape.local.start, 4
+    ids = idsc.numpy()
+    rel = ids - lo
+    local = (rel >= 0) & (rel < len(shape.local))
+    only_kept = ~(local & (rel >= keep)).any(axis=1)
+    has_kept = (local & (rel < keep)).any(axis=1)
+    sub = np.concatenate([np.nonzero(only_kept & has_kept)[0][:448], np.nonzero(only_kept & ~has_kept)[0][:64]])
+    assert len(sub) >= 256
+    w13d, w2d = mx_deq(w13[:keep], w2[:keep])
+    ref = OX.moe_ffn(xc[sub], ids[sub].astype(np.int32), wc.numpy()[sub].astype(np.float32), w13d, w2d, lo,
+                     act="bf16")
+    got = bits16(out)[sub]
+    err = rel_l2(F.bf16_to_f32(got), F.bf16_to_f32(ref))
+    say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
+    assert err <= REL_L2_TOL
+    assert not got[~has_kept[sub]].any()
