@@ -45,6 +45,9 @@ def parse():
                     "library's dense fp8 GEMM (torch._scaled_mm, hipBLASLt) at the layer's padded "
                     "GEMM shapes, a ceiling to compare the grouped GEMMs with")
     ap.add_argument("--config", default="dsv4_rank", choices=["dsv4_rank", "ernie_fp8", "tiny"])
+    ap.add_argument("--act", default=None, choices=["bf16"],
+                    help="layer: the GEMMs' activation format (default: the weight format's fp8 "
+                    "form; bf16 = W4A16 for MXFP4 weights)")
     ap.add_argument("--jobs", type=int, default=32, help="stream: jobs in the stream")
     ap.add_argument("--batch-tokens", type=int, default=32768,
                     help="stream: token capacity of the scheduler's batched expert calls in the "
@@ -147,7 +150,7 @@ def load_traffic(workload: str, kernel_key: str):
     return hits[0]["bytes"] if len(hits) == 1 else None
 
 
-def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
+def cpu_baseline(shape, sample_tokens: int, sample_experts: int, act=None):
     """The fp32 CPU oracle on a bounded sample: the first ``sample_tokens`` tokens of the
     same seeded job, with only experts [0, sample_experts) treated as local (so the sample
     keeps the per-pair work of the full layer). 1 warm-up + 3 timed reps, median."""
@@ -167,12 +170,13 @@ def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
         c13, s13 = F.mx_quantize(w13.numpy(), "e2m1")
         c2, s2 = F.mx_quantize(w2.numpy(), "e2m1")
         w13d, w2d = F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1")
-        act = "mxfp8"
+        act_fp8 = "mxfp8"
     else:
         c13, s13 = F.fp8_block_quantize_2d(w13.numpy())
         c2, s2 = F.fp8_block_quantize_2d(w2.numpy())
         w13d, w2d = F.fp8_block_dequantize_2d(c13, s13), F.fp8_block_dequantize_2d(c2, s2)
-        act = "fp8_1x128"
+        act_fp8 = "fp8_1x128"
+    act = act or act_fp8
     ids_np, w_np = ids.numpy(), w.numpy()
     np_pairs = int(((ids_np >= 0) & (ids_np < sample_experts)).sum())
     times = []
@@ -191,7 +195,7 @@ def cpu_baseline(shape, sample_tokens: int, sample_experts: int):
         "kind": "port",
         "sample": (
             f"{sample_tokens} tokens of the same seeded job, experts [0,{sample_experts}) local "
-            f"({np_pairs} pairs), fp32 torch CPU oracle incl. act quant/routing/finalize; "
+            f"({np_pairs} pairs), fp32 torch CPU oracle ({act} activations) incl. act quant/routing/finalize; "
             f"median of 3 reps = {t * 1e3:.1f} ms"
         ),
     }
@@ -585,7 +589,8 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
-    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n)
+    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, weights, n_max=n, act_format=args.act)
+    a16 = experts.act_format == "bf16"
     np_pairs = W.pair_count(ids, shape.local)
     flops = W.flops(shape.hidden, shape.inter, np_pairs)
     gate_up_flops = 4 * shape.hidden * shape.inter * np_pairs
@@ -672,13 +677,18 @@ def main():
     k, h = shape.top_k, shape.hidden
     xs_bytes = n * h // 32 if shape.fmt == "mxfp4" else n * h // 128 * 4
     phase_bytes = {
-        "hist_quant": n * k * 4 + n * h * 2 + n * h + xs_bytes,  # ids; x in; codes + scales out
+        # ids; x in; codes + scales out (bf16 activations: the histogram of the ids only)
+        "hist_quant": n * k * 4 if a16 else n * k * 4 + n * h * 2 + n * h + xs_bytes,
         "scatter": n * k * 4 + n * k * 4 + np_pairs * 4,  # ids in; pair_pos, sorted pairs out
         "finalize": np_pairs * h * 2 + n * k * 8 + n * h * 2,  # y rows, pair_pos + w; out
     }
     phase_gbps = {s: round(b / (stage_avg[s] * 1e-3) / 1e9, 1) for s, b in phase_bytes.items()}
     gu_tflops = gate_up_flops / (gu_ms * 1e-3) / 1e12
-    issued = "fp8" if shape.fmt in ("mxfp4", "fp8_block") else "bf16"
+    issued = "bf16" if a16 else "fp8"
+    kernel = ("a16_gemm_kernel<gate_up>" if a16 else "mx_gemm_kernel<gate_up>") if shape.fmt == "mxfp4" \
+        else "fp8_gemm_kernel<gate_up>"
+    kernel_key = ("a16_gemm_kernel<0" if a16 else "mx_gemm_kernel<0") if shape.fmt == "mxfp4" else "fp8_gemm_kernel<0"
+    traffic_name = shape.name + ("_a16" if a16 else "")
     result = {
         "metric": "MoE-layer TFLOPS + tokens/s at 16k-token dispatch, 1 MI355X; MFMA util %",
         "value": round(tflops, 2),
@@ -691,12 +701,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "mxfp4xmxfp8" if shape.fmt == "mxfp4" else "fp8xfp8(block)",
+        "dtype": ("mxfp4xbf16" if a16 else "mxfp4xmxfp8") if shape.fmt == "mxfp4" else "fp8xfp8(block)",
         "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) expert weights, random-init)",
         "config": {
             "workload": f"{shape.name}: one F rank, H={shape.hidden} I={shape.inter}, "
             f"{shape.num_local} local of {shape.num_experts} experts, top-{shape.top_k}, "
-            f"{'uniform' if shape.zipf is None else f'Zipf({shape.zipf})'} routing, {n} tokens, {shape.fmt} weights",
+            f"{'uniform' if shape.zipf is None else f'Zipf({shape.zipf})'} routing, {n} tokens, {shape.fmt} weights, "
+            f"{experts.act_format} activations",
             "tokens": n,
             "local_pairs": np_pairs,
             "algorithmic_tflop": round(flops / 1e12, 4),
@@ -714,8 +725,7 @@ def main():
         "histogram and the activation quantization in one launch; scatter: the router's scan and "
         "pair scatter",
         "roofline": {
-            "kernel": "grouped gate_up GEMM + SwiGLU (mx_gemm_kernel<gate_up>)"
-            if shape.fmt == "mxfp4" else "grouped gate_up GEMM + SwiGLU (fp8_gemm_kernel<gate_up>)",
+            "kernel": f"grouped gate_up GEMM + SwiGLU ({kernel})",
             "bound": "mfma",
             "achieved": round(gu_tflops, 2),
             "kernel_ms": round(gu_ms, 5),
@@ -723,11 +733,12 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / (PEAK_TFLOPS["fp4"] if shape.fmt == "mxfp4" else PEAK_TFLOPS["fp8"]), 4),
             "frac_vs_issued_format_peak": round(gu_tflops / PEAK_TFLOPS[issued], 4),
-            "traffic": load_traffic(shape.name, "mx_gemm_kernel<0" if shape.fmt == "mxfp4" else "fp8_gemm_kernel<0"),
+            "traffic": load_traffic(traffic_name, kernel_key),
         },
     }
     if args.cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(shape, min(args.cpu_sample_tokens, n), min(args.cpu_sample_experts, shape.num_local))
+        result["cpu_baseline"] = cpu_baseline(shape, min(args.cpu_sample_tokens, n), min(args.cpu_sample_experts, shape.num_local),
+                                              experts.act_format)
     print(json.dumps(result), flush=True)
 
 

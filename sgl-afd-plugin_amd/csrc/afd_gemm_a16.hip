@@ -225,7 +225,8 @@ __global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16Gemm
     const int64_t e = e_cur;
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
+    // this group has a real row (padding rows come last in a segment)
+    const bool live_i0 = live_cur > 0;
     if (has_next) load_next(i_next);
     if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
@@ -262,22 +263,38 @@ __global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16Gemm
         f.sb[j] = bbase[kImgData + 4 * n + 2 * lk + c];
       }
     };
-    // the 32 MFMAs of a half stage (blocks of padding rows skipped)
+    // The 32 MFMAs of a half stage: 16 steps (j, s), step st expanding the weight fragment of
+    // step st + 1 into the other of two register sets while its own 2 MFMAs run, so the
+    // converts issue in the MFMAs' shadow. A group whose 64 rows are all padding skips the
+    // phase (one uniform branch per phase: branches between the steps, or a second copy of the
+    // phase for groups with one live 32-row block, cost more registers than there are).
     auto mma_half = [&]() {
-      static_for<4>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const float scale = __uint_as_float(f.sb[j] << 23);
-        static_for<4>([&](auto sc) {
-          constexpr int s = decltype(sc)::value;
-          const v8bf wb = expand_fp4(static_cast<uint32_t>(f.b[j][s]), scale);
-          static_for<2>([&](auto i2c) {
-            constexpr int i2 = decltype(i2c)::value;
-            if (i2 == 0 ? live_i0 : live_i1)
-              acc[i2][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                  wb, __builtin_bit_cast(v8bf, f.a[s][i2]), acc[i2][j], 0, 0, 0);
-          });
-        });
+      float scale[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) scale[j] = __uint_as_float(f.sb[j] << 23);
+      v8bf wb[2];
+      wb[0] = expand_fp4(static_cast<uint32_t>(f.b[0][0]), scale[0]);
+      static_for<16>([&](auto stc) {
+        constexpr int st = decltype(stc)::value, j = st / 4, s = st % 4;
+        if constexpr (st + 1 < 16)
+          wb[(st + 1) & 1] = expand_fp4(static_cast<uint32_t>(f.b[(st + 1) / 4][(st + 1) % 4]), scale[(st + 1) / 4]);
+        acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[st & 1], __builtin_bit_cast(v8bf, f.a[s][0]),
+                                                             acc[0][j], 0, 0, 0);
+        acc[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[st & 1], __builtin_bit_cast(v8bf, f.a[s][1]),
+                                                             acc[1][j], 0, 0, 0);
       });
+      // issue order: the scale shifts and step 0's expansion, then per step its MFMAs followed
+      // by the next step's 4 converts (left to itself the scheduler hoists every expansion
+      // ahead of the MFMAs, which needs 64 more registers than there are)
+      __builtin_amdgcn_sched_group_barrier(0x2, 8, 0);
+      static_for<16>([&](auto stc) {
+        constexpr int st = decltype(stc)::value;
+        __builtin_amdgcn_sched_group_barrier(0x8, 2, 0);
+        if constexpr (st + 1 < 16) __builtin_amdgcn_sched_group_barrier(0x2, 4, 0);
+      });
+    };
+    auto mma_live = [&]() {
+      if (live_i0) mma_half();
     };
 
     // Ping-pong over half stages hf = 2 kt + c (as the W4A8 kernel over stages): group 0 reads
@@ -305,7 +322,7 @@ __global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16Gemm
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_half();
+        mma_live();
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         if (c == 1) wait_vmcnt<(kStages - 2) * T::kPiecesMin>();  // own pieces of stage kt + 1
@@ -325,7 +342,7 @@ __global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16Gemm
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_half();
+        mma_live();
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
