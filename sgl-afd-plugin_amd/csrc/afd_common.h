@@ -184,52 +184,48 @@ __device__ __forceinline__ uint32_t div_by_magic(uint32_t n, uint32_t magic) {
 // tiles [0, ntn). The dispatcher deals workgroups to the 8 XCDs round robin (workgroup b runs
 // on XCD b % 8), and each XCD has its own L2. With a grid that is a multiple of 8 and at
 // least kWalkSplitRows row tiles, XCD x takes the contiguous row tiles
-// [rows x / 8, rows (x + 1) / 8), else every workgroup walks all of them. A workgroup visits
-// walk positions first, first + stride, ...; 32 consecutive positions form a block of BR row
-// tiles x 32 / BR column tiles (row tiles fastest; row blocks outer, column blocks inner), so
-// the ~32 workgroups of an XCD run about one block at a time and share each activation slice
-// 32 / BR ways and each weight slice BR ways in their L2. Positions past the last row or
-// column tile are holes and are skipped.
+// [rows x / 8, rows (x + 1) / 8), else every workgroup walks all of them. The tiles of a
+// walk are numbered densely (`at_dense`) in blocks of BR row tiles x 32 / BR column tiles (row
+// tiles fastest inside a block; row blocks outer, column blocks inner; the last row block and
+// the last column block may be partial), so the ~32 workgroups of an XCD run about one block
+// at a time and share each activation slice 32 / BR ways and each weight slice BR ways in
+// their L2.
+//
+// The dense positions are handed out in one of two ways: statically (workgroup k of a walk
+// takes positions first, first + stride, ...) or dynamically, from one counter per walk (per
+// XCD when the rows are split), one lane of a workgroup taking the next position with an
+// atomic increment (`claim_ticket`) and `resolve` mapping positions past the last tile to
+// `tiles`. The tiles then stay on the XCD whose L2 shares their operands, while a workgroup
+// that starts late (its CU held by another kernel, e.g. a parked stream wait) takes fewer
+// tiles instead of adding a whole round at the end. Everything but the claim itself is host
+// code too, so the walk's coverage is checked on the CPU (tests/walk_model.cpp).
 constexpr int kWalkSplitRows = 32;
-template <int BR>
-inline int walk_col_blocks(int ntn) {
-  return (ntn + 32 / BR - 1) / (32 / BR);
-}
 
-// Tiles can also be handed out dynamically: one counter per XCD (one in all if the rows are
-// not split) counts the XCD's tiles in walk order with the holes left out (`at_dense`), and
-// one lane of a workgroup takes the next with an atomic increment (`claim_ticket`). The
-// tiles then stay on the XCD whose L2 shares their operands, while a workgroup that starts
-// late (its CU held by another kernel, e.g. a parked stream wait) takes fewer tiles instead
-// of adding a whole round at the end.
 template <int BR>
 struct TileWalk {
   static_assert(BR == 1 || BR == 2 || BR == 4 || BR == 8 || BR == 16 || BR == 32, "BR divides 32");
   static constexpr int kBC = 32 / BR;
-  int mt0, rows_here, ntn, ncb, first, stride, count;
+  int mt0, rows_here, ntn, first, stride;
   int tiles;  // rows_here * ntn: the dense positions of at_dense
-  uint32_t ncb_magic;
   uint32_t* ctr;
-  // ncb_magic_ = div_magic(walk_col_blocks<BR>(ntn_)); counters: 8 zeroed words for claim()
-  __device__ __forceinline__ TileWalk(int rows, int ntn_, uint32_t ncb_magic_,
-                                      uint32_t* counters = nullptr) {
+  // block / grid: this workgroup's index and the grid size; counters: 8 zeroed words for the
+  // dynamic walk (one per XCD)
+  __host__ __device__ __forceinline__ TileWalk(int rows, int ntn_, int block, int grid,
+                                               uint32_t* counters = nullptr) {
     ntn = ntn_;
-    ncb = (ntn_ + kBC - 1) / kBC;
-    ncb_magic = ncb_magic_;
     mt0 = 0;
     rows_here = rows;
-    first = blockIdx.x;
-    stride = gridDim.x;
+    first = block;
+    stride = grid;
     ctr = counters;
-    if ((gridDim.x & 7) == 0 && rows >= kWalkSplitRows) {
-      const int xcd = blockIdx.x & 7;
+    if ((grid & 7) == 0 && rows >= kWalkSplitRows) {
+      const int xcd = block & 7;
       mt0 = (rows * xcd) >> 3;
       rows_here = ((rows * (xcd + 1)) >> 3) - mt0;
-      first = blockIdx.x >> 3;
-      stride = gridDim.x >> 3;
+      first = block >> 3;
+      stride = grid >> 3;
       if (counters != nullptr) ctr = counters + xcd;
     }
-    count = (rows_here + BR - 1) / BR * ncb * 32;
     tiles = rows_here * ntn;
   }
   // the next dense position of this walk's counter, possibly past the last tile
@@ -238,13 +234,13 @@ struct TileWalk {
     return __builtin_amdgcn_atomic_inc32(ctr, 0xffffffffu, __ATOMIC_RELAXED, "agent");
   }
   // a claimed dense position, or `tiles` if it is past the last tile
-  __device__ __forceinline__ int resolve(uint32_t i) const {
+  __host__ __device__ __forceinline__ int resolve(uint32_t i) const {
     return i < static_cast<uint32_t>(tiles) ? static_cast<int>(i) : tiles;
   }
-  // The tile at dense position i < tiles: the i-th tile of at()'s order without its holes.
-  // Row blocks of BR row tiles (the last may have fewer, vr), in each, column blocks of kBC
-  // column tiles (the last may have fewer); inside a block, row tiles fastest.
-  __device__ __forceinline__ void at_dense(int i, int& mt, int& nt) const {
+  // The tile at dense position i < tiles. Row blocks of BR row tiles (the last may have
+  // fewer, vr), in each, column blocks of kBC column tiles (the last may have fewer); inside
+  // a block, row tiles fastest.
+  __host__ __device__ __forceinline__ void at_dense(int i, int& mt, int& nt) const {
     const int full = rows_here / BR;  // full row blocks
     int rb, vr = BR, j = i;
     if (i < full * BR * ntn) {
@@ -258,28 +254,6 @@ struct TileWalk {
     const int cb = j / (vr * kBC), jj = j - cb * vr * kBC;
     mt = mt0 + rb * BR + jj % vr;
     nt = cb * kBC + jj / vr;
-  }
-  // the tile at walk position i; false for a hole
-  __device__ __forceinline__ bool at(int i, int& mt, int& nt) const {
-    const int b = i >> 5, k = i & 31;
-    const int rb = static_cast<int>(div_by_magic(static_cast<uint32_t>(b), ncb_magic));
-    const int r = rb * BR + k % BR;
-    const int c = (b - rb * ncb) * kBC + k / BR;
-    mt = mt0 + r;
-    nt = c;
-    return r < rows_here && c < ntn;
-  }
-  // the next tile position after i (count if none)
-  __device__ __forceinline__ int next(int i) const {
-    int mt, nt;
-    for (i += stride; i < count; i += stride)
-      if (at(i, mt, nt)) break;
-    return i < count ? i : count;
-  }
-  __device__ __forceinline__ int begin() const {
-    int mt, nt;
-    if (first < count && at(first, mt, nt)) return first;
-    return next(first);
   }
 };
 

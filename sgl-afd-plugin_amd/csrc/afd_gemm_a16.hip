@@ -48,7 +48,6 @@ struct A16GemmArgs {
   const afd_job* rows_desc;     // gate_up: if set, a_rows is its x (read when the kernel runs)
   int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
   uint32_t topk_magic;          // div_magic(topk)
-  uint32_t ncb_magic;           // div_magic(walk_col_blocks<kA16WalkRows>(N / BN))
   const uint8_t* b_img;         // B images [E][N/256][K/128]
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
@@ -113,7 +112,7 @@ __global__ __launch_bounds__(A16Tile<WN>::kThreads) void a16_gemm_kernel(A16Gemm
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
   const int nt256 = p.N / kImgBRows;
-  const TileWalk<kA16WalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  const TileWalk<kA16WalkRows> walk(p.num_tiles[0], p.N / kBN, blockIdx.x, gridDim.x, p.walk_ctr);
   __shared__ int claimed[2];
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
@@ -467,7 +466,6 @@ int launch_a16(const A16GemmArgs& p, int max_row_tiles, hipStream_t stream) {
   }();
   const int max_tiles = max_row_tiles * (p.N / T::kBN);
   A16GemmArgs a = p;
-  a.ncb_magic = div_magic(walk_col_blocks<kA16WalkRows>(p.N / T::kBN));
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
   hipLaunchKernelGGL((a16_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);

@@ -84,7 +84,6 @@ struct Fp8GemmArgs {
   const afd_job* rows_desc;  // gate_up: if set, a / as are its xq / xs
   int topk;
   uint32_t topk_magic;  // div_magic(topk)
-  uint32_t ncb_magic;   // div_magic(walk_col_blocks<kWalkRows>(N / 256))
   const uint8_t* b;     // e4m3 [E][N][K] (gate_up rows interleaved gate/up by 32)
   const float* bs;      // [E][N/128][K/128] in logical block order
   const int32_t* sorted_pairs;    // [np] flat pair index per padded row, -1 = pad
@@ -106,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / 4, wn = w_u % 4, lr = lane & 31, lk = lane >> 5;
-  const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, blockIdx.x, gridDim.x, p.walk_ctr);
   __shared__ int claimed[2];  // the claimed walk positions lane 0 publishes (as in the MX kernel)
   const int KT = p.K / kBK;
   const int nblk = p.N / kBK;  // weight scale blocks along N
@@ -527,7 +526,6 @@ static int launch(Fp8GemmArgs p, int max_row_tiles, hipStream_t stream) {
     return b;
   }();
   const int max_tiles = max_row_tiles * (p.N / kBN);
-  p.ncb_magic = div_magic(walk_col_blocks<kWalkRows>(p.N / kBN));
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
   hipLaunchKernelGGL(fp8_gemm_kernel<MODE>, dim3(grid), dim3(kThreads), 0, stream, p);
@@ -540,7 +538,6 @@ static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
   p.act = act_params(cfg);
-  p.ncb_magic = 0;
   p.sorted_pairs = reinterpret_cast<const int32_t*>(ws + L.sorted_pairs);
   p.tile_expert = reinterpret_cast<const int32_t*>(ws + L.tile_expert);
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);

@@ -43,7 +43,6 @@ struct MxGemmArgs {
   const afd_job* rows_desc;     // gate_up: if set, a_rows / a_scales are its xq / xs
   int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
   uint32_t topk_magic;          // div_magic(topk)
-  uint32_t ncb_magic;           // div_magic(walk_col_blocks<kMxWalkRows>(N / BN)), for the tile walk
   const uint8_t* b_img;         // B images [E][N/256][K/128]
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
@@ -107,7 +106,7 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
   const int wm = w_u / WN, wn = w_u % WN, lr = lane & 31, lk = lane >> 5;
   const int nt256 = p.N / kImgBRows;
-  const TileWalk<kMxWalkRows> walk(p.num_tiles[0], p.N / kBN, p.ncb_magic, p.walk_ctr);
+  const TileWalk<kMxWalkRows> walk(p.num_tiles[0], p.N / kBN, blockIdx.x, gridDim.x, p.walk_ctr);
   // lane 0 claims the walk's dense positions (the tile after next, one tile ahead) and
   // publishes them here; every wavefront reads them after a barrier
   __shared__ int claimed[2];
@@ -519,7 +518,6 @@ static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream)
   }();
   const int max_tiles = max_row_tiles * (p.N / T::kBN);
   MxGemmArgs a = p;
-  a.ncb_magic = div_magic(walk_col_blocks<kMxWalkRows>(p.N / T::kBN));
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
   hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);

@@ -289,9 +289,30 @@ class FfnScheduler:
     def _batchable(self, job) -> bool:
         return len(job.rows) == 1 and job.rows[0].n_tokens <= self.batch_tokens
 
+    @staticmethod
+    def _generations(jobs) -> List[list]:
+        """The jobs of one poll by generation: generation g holds the g-th job of each (replica,
+        slot) of the poll, in arrival order. A slot's next message is rung only after the F side
+        answered the one before, so the later job's doorbell gate must not be enqueued ahead of,
+        or in the same batched call as, the earlier job's answer: the scheduler serves the
+        generations one after another, and a batch holds jobs of one generation only."""
+        seen: collections.Counter = collections.Counter()
+        gens: List[list] = []
+        for job in jobs:
+            key = (job.replica, job.slot)
+            gen = seen[key]
+            seen[key] += 1
+            if gen == len(gens):
+                gens.append([])
+            gens[gen].append(job)
+        return gens
+
     def _pack(self, jobs) -> List[list]:
-        """First-fit decreasing: jobs (of one layer) into batches of at most batch_tokens
-        tokens and AFD_MAX_BATCH jobs."""
+        """First-fit decreasing: jobs of one layer and one generation (at most one per
+        (replica, slot)) into batches of at most batch_tokens tokens and AFD_MAX_BATCH jobs."""
+        keys = [(job.replica, job.slot) for job in jobs]
+        if len(set(keys)) != len(keys):
+            raise ValueError("jobs to pack hold two messages of one (replica, slot); pack each generation apart")
         bins: List[list] = []
         room: List[int] = []
         for job in sorted(jobs, key=lambda j: -j.rows[0].n_tokens):
@@ -316,6 +337,10 @@ class FfnScheduler:
         layer_id = jobs[0].layer_id
         if any(job.layer_id != layer_id or not self._batchable(job) for job in jobs):
             raise ValueError("a batch holds single-row jobs of one layer within batch_tokens")
+        if len({(job.replica, job.slot) for job in jobs}) != len(jobs):
+            # the later message's gate would wait, ahead of the call, for a doorbell that is rung
+            # only after the call answers the earlier one
+            raise ValueError("a batch cannot hold two messages of one (replica, slot)")
         _, stream = self._next_stream()
         rows = []
         for job in jobs:
@@ -338,13 +363,14 @@ class FfnScheduler:
         if not self.batch_tokens:
             return self.server.serve_pending(self.run_job)
         jobs = self.server.poll()
-        by_layer: Dict[int, list] = collections.defaultdict(list)
-        for job in jobs:
-            if self._batchable(job):
-                by_layer[job.layer_id].append(job)
-            else:
-                self.run_job(job)
-        for layer_jobs in by_layer.values():
-            for batch in self._pack(layer_jobs):
-                self.run_batch(batch)
+        for generation in self._generations(jobs):
+            by_layer: Dict[int, list] = collections.defaultdict(list)
+            for job in generation:
+                if self._batchable(job):
+                    by_layer[job.layer_id].append(job)
+                else:
+                    self.run_job(job)
+            for layer_jobs in by_layer.values():
+                for batch in self._pack(layer_jobs):
+                    self.run_batch(batch)
         return len(jobs)

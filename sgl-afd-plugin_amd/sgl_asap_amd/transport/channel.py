@@ -37,6 +37,28 @@ from .layout import ID_BYTES, ChannelPoisoned, Geometry, HandshakeError, pack_do
 COUNT_LIMIT = 1 << 63  # the largest base a channel accepts: counts never reach 2^64
 
 
+def serve_before_waiting(servers: Sequence, a: int, slot: int, count: int, pump: Callable[[], object]) -> None:
+    """Make sure an in-process F side has enqueued the job that answers message ``count`` of
+    A rank ``a`` on ``slot`` before a stream is made to wait for that answer (the backpressure
+    wait of the slot's next send, or the reply wait). Streams can share a hardware queue, and
+    a wait enqueued ahead of the job that satisfies it then never ends.
+
+    The message's word may still wait in an inbox, or its row in a half-formed job whose other
+    rows' words are in an inbox: then ``pump`` (the F side's serve_pending) runs first. A row
+    still half-formed after that needs rows that the other A ranks of its group have not sent,
+    so no job can answer it yet and the wait is refused (RuntimeError) instead of enqueued."""
+    states = [sv.pending_state(a, slot, count) for sv in servers]
+    if "inbox" in states or ("forming" in states and any(sv.has_words() for sv in servers)):
+        pump()
+        states = [sv.pending_state(a, slot, count) for sv in servers]
+    if "forming" in states:
+        raise RuntimeError(
+            f"A rank {a}: message #{count} on slot {slot} is waiting for the rows of its group's other A "
+            "ranks; they must send before this rank waits for its answer (a stream parked on an answer "
+            "that no enqueued job can give stalls the GPU queue it shares)"
+        )
+
+
 class StallWatch:
     """Detects a dead F side from the done counters an attention rank waits on.
 
@@ -261,12 +283,10 @@ class AttnChannel:
                 answered = self.flags.load(g.done_off(f, slot)) >= seq - 1
                 d.done[f] = None if answered else self._done_addrs[slot][f]
                 pending = pending or not answered
-        if pending and self.pump is not None and any(sv.unserved(self.a, slot) for sv in self.servers):
-            # in-process F side that has not taken the slot's previous message yet: serve what
-            # is pending before this send's stream waits for that message's answer, so the
-            # wait is enqueued after the work that satisfies it even when the two streams share
-            # a hardware queue
-            self.pump()
+        if pending and self.pump is not None:
+            # in-process F side: the job answering the slot's previous message must be enqueued
+            # before this send's stream waits for the answer
+            serve_before_waiting(self.servers, self.a, slot, seq - 1, self.pump)
         hip.send(d, stream.cuda_stream)
         self._count[slot] = seq
         for f, server in enumerate(self.servers):
@@ -281,6 +301,8 @@ class AttnChannel:
         device addresses of the partial sums (bf16 [n_tokens, hidden] each, F-rank order)."""
         self.check()
         g, slot = self.g, ticket.slot
+        if self.pump is not None and any(self.flags.load(g.done_off(f, slot)) < ticket.seq for f in range(g.num_f)):
+            serve_before_waiting(self.servers, self.a, slot, ticket.seq, self.pump)
         hip.wait_replies(self._done_addrs[slot], ticket.seq, stream.cuda_stream)
         for f in range(g.num_f):
             self.watch.expect(g.done_off(f, slot), ticket.seq,

@@ -161,10 +161,20 @@ class FfnServer:
         """Post the doorbell word A's producer stream will write to bell(a, slot)."""
         self._inbox.append((a, slot, int(word)))
 
-    def unserved(self, a: int, slot: int) -> bool:
-        """Whether a word A rank ``a`` posted for ``slot`` still waits in the inbox (no poll
-        has taken it, so no job for it has been enqueued)."""
-        return any(m[0] == a and m[1] == slot for m in self._inbox)
+    def has_words(self) -> bool:
+        """Whether posted words wait in the inbox for a poll."""
+        return bool(self._inbox)
+
+    def pending_state(self, a: int, slot: int, count: int) -> Optional[str]:
+        """Where message ``count`` (its 64-bit count) that A rank ``a`` posted for ``slot``
+        stands on this host: "inbox" (no poll has taken its word yet), "forming" (taken, its
+        row waiting in a half-formed job for the other rows of its group) or None (handed out
+        in a job, dropped by the poller's rules, or never posted)."""
+        cell = a * self.g.slots + slot
+        if count > self._count[cell]:
+            return "inbox" if any(m[0] == a and m[1] == slot for m in self._inbox) else None
+        row = self._forming.get((a // self.g.group, slot), {}).get(a % self.g.group)
+        return "forming" if row is not None and row.seq == count else None
 
     def poll(self) -> List[Job]:
         """Every job completed by the words posted since the last call; never blocks."""

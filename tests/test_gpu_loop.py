@@ -304,6 +304,46 @@ def test_two_sends_on_one_slot_before_serving():
         assert afd.server.stats["lost_messages"] == 0 and afd.channel.done_count(0, 0) == 2
 
 
+def test_group_of_two_two_sends_per_slot():
+    """A group of 2 A ranks on one slot, two messages each. Rank 0's first row is taken by a
+    poll and waits in a half-formed job; a second send of rank 0 before rank 1's first message
+    is refused (no job could answer its backpressure wait yet) with nothing enqueued. Once rank
+    1's first word is in the inbox, rank 0's second send serves the completed job before its
+    stream waits for the answer, so the wait never sits ahead of its job on a shared hardware
+    queue; the answers to the second messages are right."""
+    say("loop: group of 2, two sends per slot")
+    experts = make_experts(64)
+    with OneGpuAfd(experts, n_max=64, slots=1, group=2) as afd:
+        sends = [torch.cuda.Stream() for _ in range(2)]
+        main = torch.cuda.current_stream()
+        msgs = [[job(11 + 3 * r + 7 * m, 950 + 10 * m + r) for r in range(2)] for m in range(2)]
+        held = []
+        _, h = _send(afd, 0, 0, *msgs[0][0], sends[0])
+        held.append(h)
+        assert afd.scheduler.serve_pending() == 0  # rank 0's row taken: half a job
+        with pytest.raises(RuntimeError, match="other A"):
+            _send(afd, 0, 0, *msgs[1][0], sends[0])
+        assert afd.channels[0]._count[0] == 1  # the refused send took no sequence number
+        _, h = _send(afd, 1, 0, *msgs[0][1], sends[1])  # its word waits in the inbox
+        held.append(h)
+        assert afd.server.stats["jobs"] == 0
+        t0, h = _send(afd, 0, 0, *msgs[1][0], sends[0])  # serves job 1 before its wait
+        held.append(h)
+        assert afd.server.stats["jobs"] == 1 and t0.seq == 2
+        t1, h = _send(afd, 1, 0, *msgs[1][1], sends[1])
+        held.append(h)
+        assert afd.scheduler.serve_pending() == 1
+        got = []
+        for r, t in ((0, t0), (1, t1)):
+            afd.channels[r].wait(t, main)
+            got.append(afd.channels[r].result_view(0, 0, t.n_tokens).clone())
+        torch.cuda.synchronize()
+        for r in range(2):
+            assert np.array_equal(bits16(got[r]), direct(experts, 0, *msgs[1][r])), r
+            assert afd.channels[r].done_count(0, 0) == 2
+        assert afd.server.stats["jobs"] == 2 and afd.server.stats["lost_messages"] == 0
+
+
 def test_stall_releases_the_parked_wait_and_poisons():
     """A message whose doorbell carries a wrong epoch is dropped by the F server, so its reply
     never comes: the compute stream parked on the done counter is released by the stall watch

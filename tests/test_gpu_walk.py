@@ -1,9 +1,17 @@
 """GPU: the two tile walks of the persistent GEMMs give identical results. "dynamic" hands
 the tiles out from per-XCD counters, "static" gives each workgroup a fixed share; both run
-over the same dense tile order, so every output bit must agree, for both weight formats, for
-jobs from one token (8 row tiles, fewer than the 32 needed to split the rows over the XCDs)
-to thousands, for skewed routing, and while another stream holds a parked wait (a CU held by
-a wait kernel: the dynamic walk must still cover every tile)."""
+over the same dense tile order, so every output bit must agree, for both weight formats and
+both MXFP4 activation formats, for jobs from one token (8 row tiles, fewer than the 32 needed
+to split the rows over the XCDs) to thousands, for skewed routing, and while another stream
+holds a parked wait (a CU held by a wait kernel: the dynamic walk must still cover every
+tile).
+
+Before every call the whole workspace and the output are filled with 0xFF bytes, a NaN in
+every format the kernels write there (bf16 y and h, e4m3 h, UE8M0 and fp32 scales), and the
+dynamic walk runs first: a tile that a walk skipped would leave NaN rows behind, which reach
+the output through the finalize, so each output is also checked to hold no NaN. (That every
+tile is taken exactly once is shown on the CPU for the walk code itself,
+tests/test_walk_model.py.)"""
 
 import time
 
@@ -23,9 +31,13 @@ PACK = {"mxfp4": pack_mxfp4_experts, "fp8_block": pack_fp8_block_experts}
 
 
 def layer(fmt, hidden, inter, num_local, n_max, seed=0):
+    """fmt: a weight format, or "mxfp4_a16" for MXFP4 weights with bf16 activations."""
     gen = W.generator("cpu", seed)
     w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
-    return AfdExperts(num_local, 8, 0, range(0, num_local), PACK[fmt](w13, w2, device=dev()), n_max=n_max)
+    act = "bf16" if fmt == "mxfp4_a16" else None
+    pack = PACK[fmt.replace("_a16", "")]
+    return AfdExperts(num_local, 8, 0, range(0, num_local), pack(w13, w2, device=dev()), n_max=n_max,
+                      act_format=act)
 
 
 def job(n, hidden, num_experts, seed, zipf=None):
@@ -38,16 +50,33 @@ def job(n, hidden, num_experts, seed, zipf=None):
     return x, StandardTopKOutput(w.to(torch.float32).to(dev()), ids.to(torch.int32).to(dev()))
 
 
-def both(experts, x, topk):
-    outs = []
-    for walk in ("static", "dynamic"):
-        experts.tile_walk = walk
-        outs.append(bits16(experts(x, topk)))
+def bf16_values(bits):
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def poisoned_call(experts, x, topk):
+    """The expert call with its workspace and its output filled with 0xFF bytes beforehand;
+    fails if any output element is NaN."""
+    experts.workspace().fill_(0xFF)
+    out = torch.empty(x.shape[0], experts.hidden_size, dtype=torch.bfloat16, device=dev())
+    out.view(torch.int16).fill_(-1)
+    experts(x, topk, out=out)
     torch.cuda.synchronize()
-    return outs
+    got = bits16(out)
+    assert not np.isnan(bf16_values(got)).any(), f"the {experts.tile_walk} walk left NaN rows (a skipped tile)"
+    return got
 
 
-@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def both(experts, x, topk):
+    """(static, dynamic) outputs, each from a poisoned workspace; the dynamic walk runs first."""
+    outs = {}
+    for walk in ("dynamic", "static"):
+        experts.tile_walk = walk
+        outs[walk] = poisoned_call(experts, x, topk)
+    return outs["static"], outs["dynamic"]
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block", "mxfp4_a16"])
 def test_walks_agree(fmt):
     experts = layer(fmt, 1024, 512, 32, 4096)
     for n, seed, zipf in ((1, 1, None), (7, 2, None), (300, 3, None), (4096, 4, None), (3000, 5, 1.2)):

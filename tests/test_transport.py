@@ -173,11 +173,85 @@ def test_two_sends_on_one_slot_before_a_poll_are_both_served_in_order():
     e = connect(s, g, 0)
     s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
     s.announce(0, 0, L.pack_doorbell(2, 7, 1, e))
-    assert s.unserved(0, 0) and not s.unserved(0, 1)
+    assert s.pending_state(0, 0, 1) == s.pending_state(0, 0, 2) == "inbox"
+    assert s.has_words()
     jobs = s.poll()
     assert served(jobs) == [(0, 0, 0, [1]), (0, 0, 1, [2])]
     assert s.stats["lost_messages"] == 0
-    assert not s.unserved(0, 0)
+    assert s.pending_state(0, 0, 1) is None and s.pending_state(0, 0, 2) is None and not s.has_words()
+
+
+# ---- serving before a wait (one GPU: a wait must not be enqueued ahead of its job)
+class Pump:
+    """An in-process F side: serve_pending over the servers, recording the jobs."""
+
+    def __init__(self, servers):
+        self.servers, self.jobs, self.calls = servers, [], 0
+
+    def __call__(self):
+        self.calls += 1
+        for sv in self.servers:
+            self.jobs += sv.poll()
+
+
+def test_serve_before_waiting_single_rank_rows():
+    from sgl_asap_amd.transport.channel import serve_before_waiting
+
+    s, g = server()
+    e = connect(s, g, 0)
+    pump = Pump([s])
+    serve_before_waiting([s], 0, 0, 1, pump)  # nothing posted: nothing to do (a dropped or
+    assert pump.calls == 0                     # unknown message is the stall watch's business)
+    s.announce(0, 0, L.pack_doorbell(1, 5, 0, e))
+    serve_before_waiting([s], 0, 0, 1, pump)
+    assert pump.calls == 1 and served(pump.jobs) == [(0, 0, 0, [1])]
+    serve_before_waiting([s], 0, 0, 1, pump)  # already handed out
+    assert pump.calls == 1
+
+
+def test_serve_before_waiting_group_of_two():
+    """group = 2: the message's row may wait in a half-formed job while the word of its
+    group partner is still in the inbox (a poll ran between the two sends): the wait for its
+    answer serves first. With the partner's word not posted at all, no job can answer the
+    message yet: the wait is refused instead of enqueued."""
+    from sgl_asap_amd.transport.channel import serve_before_waiting
+
+    s, g = server(num_a=2, group=2, slots=1)
+    eps = [connect(s, g, a) for a in range(2)]
+    pump = Pump([s])
+    s.announce(0, 0, L.pack_doorbell(1, 4, 3, eps[0]))
+    assert s.poll() == []  # rank 0's row taken, half a job
+    assert s.pending_state(0, 0, 1) == "forming"
+    s.announce(1, 0, L.pack_doorbell(1, 4, 3, eps[1]))  # the partner's word, not yet polled
+    serve_before_waiting([s], 0, 0, 1, pump)
+    assert pump.calls == 1 and served(pump.jobs) == [(0, 0, 3, [1, 1])]
+    assert s.pending_state(0, 0, 1) is None and s.pending_state(1, 0, 1) is None
+    # message 2 of rank 0 posted and taken, rank 1's not posted: refuse the wait
+    s.announce(0, 0, L.pack_doorbell(2, 4, 4, eps[0]))
+    with pytest.raises(RuntimeError, match="other A"):
+        serve_before_waiting([s], 0, 0, 2, pump)
+    assert pump.calls == 2 and s.pending_state(0, 0, 2) == "forming"
+    # once the partner posts, the wait serves the job and goes ahead
+    s.announce(1, 0, L.pack_doorbell(2, 4, 4, eps[1]))
+    serve_before_waiting([s], 0, 0, 2, pump)
+    assert served(pump.jobs)[-1] == (0, 0, 4, [2, 2])
+
+
+def test_serve_before_waiting_ignores_later_messages():
+    """A wait for message m whose job is out does not care that message m + 1 of the slot is
+    still forming (its own wait is the one to check)."""
+    from sgl_asap_amd.transport.channel import serve_before_waiting
+
+    s, g = server(num_a=2, group=2, slots=1)
+    eps = [connect(s, g, a) for a in range(2)]
+    pump = Pump([s])
+    for a in range(2):
+        s.announce(a, 0, L.pack_doorbell(1, 4, 3, eps[a]))
+    pump()
+    s.announce(0, 0, L.pack_doorbell(2, 4, 4, eps[0]))
+    pump()
+    assert s.pending_state(0, 0, 2) == "forming"
+    serve_before_waiting([s], 0, 0, 1, pump)  # message 1's job was handed out: no error
 
 
 def test_gaps_count_as_lost_and_old_words_are_ignored():
