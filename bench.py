@@ -685,9 +685,13 @@ def main():
     phase_gbps = {s: round(b / (stage_avg[s] * 1e-3) / 1e9, 1) for s, b in phase_bytes.items()}
     gu_tflops = gate_up_flops / (gu_ms * 1e-3) / 1e12
     issued = "bf16" if a16 else "fp8"
-    kernel = ("a16_gemm_kernel<gate_up>" if a16 else "mx_gemm_kernel<gate_up>") if shape.fmt == "mxfp4" \
-        else "fp8_gemm_kernel<gate_up>"
-    kernel_key = ("a16_gemm_kernel<0" if a16 else "mx_gemm_kernel<0") if shape.fmt == "mxfp4" else "fp8_gemm_kernel<0"
+    wfmt = 0 if shape.fmt == "mxfp4" else 1
+    if a16:
+        kernel, kernel_key = f"a16_gemm_kernel<{shape.fmt}, gate_up>", f"a16_gemm_kernel<{wfmt}, 0"
+    elif shape.fmt == "mxfp4":
+        kernel, kernel_key = "mx_gemm_kernel<gate_up>", "mx_gemm_kernel<0"
+    else:
+        kernel, kernel_key = "fp8_gemm_kernel<gate_up>", "fp8_gemm_kernel<0"
     traffic_name = shape.name + ("_a16" if a16 else "")
     result = {
         "metric": "MoE-layer TFLOPS + tokens/s at 16k-token dispatch, 1 MI355X; MFMA util %",
@@ -701,7 +705,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("mxfp4xbf16" if a16 else "mxfp4xmxfp8") if shape.fmt == "mxfp4" else "fp8xfp8(block)",
+        "dtype": ("mxfp4xbf16" if a16 else "mxfp4xmxfp8") if shape.fmt == "mxfp4"
+        else ("fp8(block)xbf16" if a16 else "fp8xfp8(block)"),
         "data": "synthetic (seeded N(0,1) tokens, N(0,0.02) expert weights, random-init)",
         "config": {
             "workload": f"{shape.name}: one F rank, H={shape.hidden} I={shape.inter}, "

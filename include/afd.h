@@ -87,9 +87,10 @@ enum afd_weight_fmt {
  * MXFP4 weights with bf16 activations, through humming: scripts/run_ep.sh:4, README.md:25). */
 enum afd_act_fmt {
   AFD_A_FP8 = 0, /* the weight format's fp8 activations (above): x and h are quantized */
-  AFD_A_BF16 = 1 /* bf16 activations (MXFP4 weights only): x is read as it is, h is rounded
-                    to bf16, and the GEMMs run on bf16 MFMA with the weights expanded in
-                    registers */
+  AFD_A_BF16 = 1 /* bf16 activations: x is read as it is, h is rounded to bf16, and the GEMMs
+                    run on bf16 MFMA with the weights expanded to bf16 in registers (W4A16
+                    for MXFP4 weights, W8A16 for FP8 blocks, whose fp32 block scales are
+                    applied to the fp32 sums) */
 };
 
 /* Stream-wait conditions, as HIP's hipStreamWaitValue flags. */
@@ -172,8 +173,8 @@ typedef struct afd_ws_layout {
   uint64_t num_tiles;      /* i32 [1] row tiles in use */
   uint64_t hist;           /* i32 router scratch */
   uint64_t hq, hs;         /* intermediate activations and their scales (MXFP4: down A tile
-                              images, scales inside, hs empty; bf16 activations: 32 KiB bf16
-                              images of 128 rows x 128 K, hs empty) */
+                              images, scales inside, hs empty; bf16 activations: bf16 images
+                              of 128 rows x 128 K (MXFP4) or 64 K (FP8 block), hs empty) */
   uint64_t y;              /* bf16 [np_max][H] per-pair down outputs */
   int64_t np_max;          /* padded rows reserved: n*k + E*(block_m-1), rounded up */
   int32_t block_m;         /* row tile of the grouped GEMMs */

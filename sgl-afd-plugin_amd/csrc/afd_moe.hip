@@ -238,7 +238,6 @@ static int check_cfg(const afd_moe_cfg* cfg) {
     return AFD_ERR_ARG;
   if (cfg->tile_walk != AFD_WALK_STATIC && cfg->tile_walk != AFD_WALK_DYNAMIC) return AFD_ERR_ARG;
   if (cfg->act_fmt != AFD_A_FP8 && cfg->act_fmt != AFD_A_BF16) return AFD_ERR_UNSUPPORTED;
-  if (cfg->act_fmt == AFD_A_BF16 && cfg->weight_fmt != AFD_W_MXFP4) return AFD_ERR_UNSUPPORTED;
   return AFD_OK;
 }
 
@@ -285,7 +284,8 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   // FP8 block: fp32 per 1x128). MXFP4: hq holds the down GEMM's A images (the h rows in
   // expert order, scales inside, hs empty); FP8 block: hq / hs the padded-row intermediate
   // and its scales. bf16 activations: xq holds a batched call's bf16 rows (a single job's
-  // are read in place), hq the down GEMM's bf16 A images, xs and hs are empty.
+  // are read in place), hq the down GEMM's bf16 A images (MXFP4: 32 KiB per 128 K, FP8 block:
+  // 16 KiB per 64 K; the same bytes), xs and hs are empty.
   L.xq = take(a16 ? uint64_t(n) * H * 2 : uint64_t(n) * H);
   L.xs = take(a16 ? 0 : mx ? uint64_t(n) * (H / 32) : uint64_t(n) * (H / 128) * 4);
   L.counts = take(E * 4);
@@ -299,7 +299,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.hq = take(a16  ? max_tiles * (I / kImgK) * kImgA16
                : mx ? max_tiles * (I / kImgK) * kImgA + kImgReadSlack
                     : uint64_t(np_max) * I);
-  L.hs = take(mx ? 0 : uint64_t(np_max) * (I / 128) * 4);
+  L.hs = take(mx || a16 ? 0 : uint64_t(np_max) * (I / 128) * 4);
   L.y = take(uint64_t(np_max) * H * 2);
   L.total = o;
   L.np_max = np_max;

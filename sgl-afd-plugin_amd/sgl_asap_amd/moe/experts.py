@@ -190,14 +190,13 @@ def moe_cfg(
     ``gemm1_clamp_limit`` L is SwiGLU with a limit, silu(min(gate, L)) * clamp(up, -L, L):
     DeepSeek-V4's ``swiglu_limit`` (P/srt/models/deepseek_v4.py:63). ``act_format``: the
     precision of the GEMMs' activations, the weight format's fp8 form by default ("mxfp8" for
-    MXFP4, "fp8_1x128" for FP8 blocks, the MoE methods' default quantization) or "bf16" for
-    MXFP4 weights (W4A16: the reference's humming experts, scripts/run_ep.sh:4, README.md:25)."""
+    MXFP4, "fp8_1x128" for FP8 blocks, the MoE methods' default quantization) or "bf16" (W4A16
+    for MXFP4 weights: the reference's humming experts, scripts/run_ep.sh:4, README.md:25;
+    W8A16 for FP8 blocks)."""
     fp8 = FP8_ACT[weights.fmt]
     if act_format not in (None, fp8, "bf16"):
         raise ValueError(f"activation format {act_format!r} for {weights.fmt} weights "
                          f"(supported: {fp8!r}, 'bf16')")
-    if act_format == "bf16" and weights.fmt != "mxfp4":
-        raise NotImplementedError(f"bf16 activations with {weights.fmt} weights")
     act_fmt = _lib.AFD_A_BF16 if act_format == "bf16" else _lib.AFD_A_FP8
     if activation not in ACTIVATIONS:
         raise NotImplementedError(f"activation {activation!r} (supported: {sorted(ACTIVATIONS)})")
@@ -351,8 +350,8 @@ class AfdExperts(torch.nn.Module):
     waits (the FFN scheduler's setting). Results are identical bit for bit.
 
     ``act_format``: the activation precision of the GEMMs (``moe_cfg``): by default the
-    weight format's fp8 form, which the call quantizes x and h to; "bf16" (MXFP4 weights)
-    keeps x as it is and rounds h to bf16 (W4A16).
+    weight format's fp8 form, which the call quantizes x and h to; "bf16" keeps x as it is
+    and rounds h to bf16 (W4A16 for MXFP4 weights, W8A16 for FP8 blocks).
     """
 
     def __init__(

@@ -76,10 +76,13 @@ def test_workspace_layout_bf16_activations():
 def test_activation_format_checks():
     out = _lib.AfdWsLayout()
     L = _lib.lib()
-    bf16_fp8w = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_FP8_BLOCK, 0, 0.0, 0.0, 0, _lib.AFD_A_BF16)
     unknown = _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, _lib.AFD_W_MXFP4, 0, 0.0, 0.0, 0, 2)
-    for cfg in (bf16_fp8w, unknown):
-        assert L.afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) == _lib.AFD_ERR_UNSUPPORTED
+    assert L.afd_workspace_layout(ctypes.byref(unknown), 16, ctypes.byref(out)) == _lib.AFD_ERR_UNSUPPORTED
+    # W8A16: FP8 blocks with bf16 activations, the same bf16 h bytes as W4A16, no h scales
+    w8 = workspace_layout(_lib.AfdMoeCfg(4096, 1536, 8, 0, 64, _lib.AFD_W_FP8_BLOCK, 0, 0.0, 0.0, 0,
+                                         _lib.AFD_A_BF16), 16384)
+    assert w8["xs"] - w8["xq"] == 16384 * 4096 * 2 and w8["counts"] == w8["xs"]
+    assert w8["hs"] - w8["hq"] == w8["max_tiles"] * (1536 // 64) * 128 * 64 * 2 and w8["y"] == w8["hs"]
     # bf16 activations are not quantized: afd_quant_act refuses before touching any pointer
     a16 = _lib.AfdMoeCfg(256, 128, 2, 0, 8, _lib.AFD_W_MXFP4, 0, 0.0, 0.0, 0, _lib.AFD_A_BF16)
     assert L.afd_quant_act(ctypes.byref(a16), None, 0, None, None, None) == _lib.AFD_ERR_UNSUPPORTED
@@ -94,10 +97,11 @@ def test_python_activation_formats():
     assert moe_cfg(mx, 2, 0, act_format="mxfp8").act_fmt == _lib.AFD_A_FP8
     assert moe_cfg(mx, 2, 0, act_format="bf16").act_fmt == _lib.AFD_A_BF16
     assert moe_cfg(fp8, 2, 0, act_format="fp8_1x128").act_fmt == _lib.AFD_A_FP8
+    assert moe_cfg(fp8, 2, 0, act_format="bf16").act_fmt == _lib.AFD_A_BF16
     with pytest.raises(ValueError):
         moe_cfg(mx, 2, 0, act_format="fp8_1x128")
-    with pytest.raises(NotImplementedError):
-        moe_cfg(fp8, 2, 0, act_format="bf16")
+    with pytest.raises(ValueError):
+        moe_cfg(fp8, 2, 0, act_format="mxfp8")
 
 
 def test_bad_configs_rejected_on_host():

@@ -1,14 +1,16 @@
-"""GPU parity of the expert call with bf16 activations (W4A16: MXFP4 weights, the activations
-kept bf16, h rounded to bf16) against the fp32 CPU oracle run with ``act="bf16"``.
+"""GPU parity of the expert call with bf16 activations (W4A16: MXFP4 weights; W8A16: FP8
+128x128-block weights; the activations kept bf16, h rounded to bf16) against the fp32 CPU
+oracle run with ``act="bf16"`` on the dequantized weights.
 
 Bars: routing bit-exact (the same router as the fp8 path); the output within rel-L2 <= 1e-2 of
 the oracle (the weight expansion is exact, so the remaining difference is fp32 summation order
 and the bf16 rounding of h and y at different sums); tokens with no local expert exactly 0;
 the h images decoded from the workspace within the same bar of the oracle's h. At the
-DeepSeek-V4 F-rank size (16384 tokens): the tokens of 4 experts against the oracle, and the
-size-independent properties of the fp8 path's full-size test (subset and permutation rows,
-doubling the weights, the descriptor call, the static and dynamic walks bit-identical).
-Batched, answering and descriptor calls are bit-identical to the plain call.
+DeepSeek-V4 F-rank size (16384 tokens, MXFP4) and the ERNIE-style FP8-block size (16384
+tokens, Zipf(1.1)): tokens of a few experts against the oracle, and the size-independent
+properties of the fp8 path's full-size test (subset and permutation rows, doubling the
+weights, the descriptor call, the static and dynamic walks bit-identical). Batched,
+answering and descriptor calls are bit-identical to the plain call.
 """
 
 import ctypes
@@ -22,12 +24,16 @@ from gpu_util import bits16, dev, rel_l2, say
 from oracle import experts as OX
 from oracle import formats as F
 from sgl_asap_amd import workloads as W
-from sgl_asap_amd.moe.experts import AfdExperts, new_job_desc, pack_mxfp4_experts, release_workspaces, set_job
+from sgl_asap_amd.moe.experts import (AfdExperts, new_job_desc, pack_fp8_block_experts, pack_mxfp4_experts,
+                                      release_workspaces, set_job)
 from sgl_asap_amd.moe.topk import StandardTopKOutput
 
 pytestmark = pytest.mark.gpu
 
 REL_L2_TOL = 1e-2
+
+
+PACK = {"mxfp4": pack_mxfp4_experts, "fp8_block": pack_fp8_block_experts}
 
 
 def mx_deq(w13, w2):
@@ -36,9 +42,18 @@ def mx_deq(w13, w2):
     return F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1")
 
 
+def fp8_deq(w13, w2):
+    c13, s13 = F.fp8_block_quantize_2d(w13.numpy())
+    c2, s2 = F.fp8_block_quantize_2d(w2.numpy())
+    return F.fp8_block_dequantize_2d(c13, s13), F.fp8_block_dequantize_2d(c2, s2)
+
+
+DEQ = {"mxfp4": mx_deq, "fp8_block": fp8_deq}
+
+
 def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed, zipf=None, situ=None,
-             swiglu_limit=None, tile_walk="static"):
-    say(f"a16 H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} "
+             swiglu_limit=None, tile_walk="static", fmt="mxfp4"):
+    say(f"a16 fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} "
         f"seed={seed} zipf={zipf} situ={situ} swiglu_limit={swiglu_limit} walk={tile_walk}")
     gen = W.generator("cpu", seed)
     x = W.tokens(n, hidden, gen, "cpu")
@@ -47,7 +62,7 @@ def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed, zipf=None,
     else:
         ids, w = W.route_zipf(n, num_experts, k, zipf, gen, "cpu")
     w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
-    weights = pack_mxfp4_experts(w13, w2, device=dev())
+    weights = PACK[fmt](w13, w2, device=dev())
     act_kw, oact = {}, {}
     if situ is not None:
         act_kw = dict(activation="situ", gemm1_alpha=situ[0], gemm1_clamp_limit=situ[1])
@@ -60,7 +75,7 @@ def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed, zipf=None,
     assert experts.act_format == "bf16"
     out = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
-    w13d, w2d = mx_deq(w13, w2)
+    w13d, w2d = DEQ[fmt](w13, w2)
     ref, parts = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13d, w2d, e_lo, act="bf16", return_parts=True, **oact)
     return experts, out, ref, parts, (x, ids, w)
 
@@ -78,26 +93,30 @@ def assert_close(out, ref, ids, local):
 
 def h_from_images(experts, n, rows):
     """The gate_up GEMM's h rows in padded expert order, decoded from the workspace's bf16 A
-    images: one 32 KiB image per (row tile, 128-wide K stage), row r at r * 256 B, logical
-    16-byte chunk c at physical chunk c ^ (r % 16)."""
+    images. MXFP4: one 32 KiB image per (row tile, 128-wide K stage), row r at r * 256 B,
+    logical 16-byte chunk c at physical chunk c ^ (r % 16). FP8 block: one 16 KiB image per
+    (row tile, 64-wide K stage), row r at r * 128 B, chunk c at c ^ ((r ^ (r >> 3)) % 8)."""
     inter = experts.intermediate_size
-    stages = inter // 128
+    stage_k = 128 if experts.weights.fmt == "mxfp4" else 64
+    stages, chunks = inter // stage_k, stage_k // 8
     tiles = (rows + 127) // 128
-    raw = experts.ws_view("hq", torch.uint8, tiles * stages * 32768, n).cpu().numpy()
-    img = raw.reshape(tiles, stages, 128, 16, 16)  # [tile][stage][row][physical chunk][byte]
+    raw = experts.ws_view("hq", torch.uint8, tiles * stages * 128 * stage_k * 2, n).cpu().numpy()
+    img = raw.reshape(tiles, stages, 128, chunks, 16)  # [tile][stage][row][physical chunk][byte]
     r = np.arange(128)
-    logical = np.arange(16)[None, :] ^ (r[:, None] & 15)  # physical chunk of logical chunk c
-    ordered = img[:, :, r[:, None], logical, :]  # [tile][stage][row][logical chunk][byte]
-    h = ordered.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, stages * 256).view(np.uint16)
+    swz = (r & 15) if stage_k == 128 else ((r ^ (r >> 3)) & 7)
+    physical = np.arange(chunks)[None, :] ^ swz[:, None]  # physical chunk of logical chunk c
+    ordered = img[:, :, r[:, None], physical, :]  # [tile][stage][row][logical chunk][byte]
+    h = ordered.transpose(0, 2, 1, 3, 4).reshape(tiles * 128, stages * stage_k * 2).view(np.uint16)
     return F.bf16_to_f32(h[:rows])
 
 
-def test_tiny_layer_a16():
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_tiny_layer_a16(fmt):
     """The tiny CPU-runnable layer (H256 I128, 8 experts, top-2, 64 tokens) with bf16
     activations: output and h against the oracle, routing bit-exact."""
     s = W.SHAPES["tiny"]
     experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k,
-                                                     s.tokens, seed=0)
+                                                     s.tokens, seed=0, fmt=fmt)
     assert_close(out, ref, ids.numpy(), s.local)
     n, k = ids.shape
     pos = experts.ws_view("pair_pos", torch.int32, n * k, n).cpu().numpy()
@@ -110,12 +129,13 @@ def test_tiny_layer_a16():
     assert err <= REL_L2_TOL
 
 
-def test_a16_differs_from_fp8_activations():
-    """The bf16 path is not the fp8 path under another name: the same layer with MXFP8
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_a16_differs_from_fp8_activations(fmt):
+    """The bf16 path is not the fp8 path under another name: the same layer with fp8
     activations gives different bits, and lies farther from the bf16 oracle."""
     s = W.SHAPES["tiny"]
     experts, out, ref, parts, (x, ids, w) = run_case(s.hidden, s.inter, s.num_experts, 0, s.num_local, s.top_k,
-                                                     s.tokens, seed=1)
+                                                     s.tokens, seed=1, fmt=fmt)
     fp8 = AfdExperts(s.num_experts, s.top_k, 0, s.local, experts.weights, n_max=s.tokens)
     out8 = fp8(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
@@ -140,6 +160,24 @@ def test_a16_layers(hidden, inter, num_experts, e_lo, num_local, k, n, seed):
     assert_close(out, ref, ids.numpy(), range(e_lo, e_lo + num_local))
 
 
+@pytest.mark.parametrize(
+    "hidden,inter,num_experts,e_lo,num_local,k,n,seed,zipf",
+    [
+        (512, 256, 32, 8, 16, 4, 300, 51, None),     # 512-column tiles in both GEMMs
+        (256, 128, 16, 0, 16, 8, 1, 52, None),       # one token; 256-column tiles
+        (1024, 384, 16, 0, 16, 8, 700, 53, 1.1),     # K blocks 8 / 3, down N = 1024
+        (768, 640, 8, 0, 8, 2, 129, 54, None),       # down N = 768: 256-column tiles; 10 K stages
+        (4096, 1536, 64, 0, 4, 8, 96, 55, None),     # the ERNIE-style shape on 4 experts
+    ],
+)
+def test_w8a16_layers(hidden, inter, num_experts, e_lo, num_local, k, n, seed, zipf):
+    """FP8 128x128-block weights with bf16 activations (W8A16): the block scales change every
+    two 64-wide K stages, applied to the fp32 sums."""
+    experts, out, ref, parts, (x, ids, w) = run_case(hidden, inter, num_experts, e_lo, num_local, k, n, seed,
+                                                     zipf=zipf, fmt="fp8_block")
+    assert_close(out, ref, ids.numpy(), range(e_lo, e_lo + num_local))
+
+
 def draw(case: int) -> dict:
     rng = random.Random(5100 + case)
     num_experts = rng.choice([8, 16, 32, 64])
@@ -154,6 +192,7 @@ def draw(case: int) -> dict:
         n=rng.choice([1, 2, 31, 64, 127, 128, 129, 255, 300, 777]),
         zipf=rng.choice([None, 1.2]),
         tile_walk=rng.choice(["static", "dynamic"]),
+        fmt=rng.choice(["mxfp4", "fp8_block"]),
     )
     act = rng.choice(["silu", "situ", "limit"])
     if act == "situ":
@@ -163,23 +202,24 @@ def draw(case: int) -> dict:
     return spec
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(24))
 def test_a16_random_layer(case):
-    """Seeded random shapes: hidden 256-1536, inter 128-768 (both tile widths, 1-12 K stages),
-    token counts around the 128-row tile edge, partial local ranges, top-1 to top-8, uniform
-    and Zipf routing, the three activations, both tile walks."""
+    """Seeded random shapes: both weight formats, hidden 256-1536, inter 128-768 (both tile
+    widths, 1-12 K stages), token counts around the 128-row tile edge, partial local ranges,
+    top-1 to top-8, uniform and Zipf routing, the three activations, both tile walks."""
     s = draw(case)
     extra = {k: s[k] for k in ("situ", "swiglu_limit") if k in s}
     experts, out, ref, parts, (x, ids, w) = run_case(
         s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], 9100 + case,
-        zipf=s["zipf"], tile_walk=s["tile_walk"], **extra)
+        zipf=s["zipf"], tile_walk=s["tile_walk"], fmt=s["fmt"], **extra)
     assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
 
 
-def test_a16_walks_batch_answer_descriptor_identical():
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_a16_walks_batch_answer_descriptor_identical(fmt):
     """Static and dynamic walks, a batched call (with an empty first job), the answering call
     and the descriptor call all give the plain call's bits."""
-    experts, out, ref, parts, (x, ids, w) = run_case(1024, 512, 32, 0, 16, 8, 700, seed=41, zipf=1.2)
+    experts, out, ref, parts, (x, ids, w) = run_case(1024, 512, 32, 0, 16, 8, 700, seed=41, zipf=1.2, fmt=fmt)
     xd, idsd, wd = x.to(dev()), ids.to(torch.int32).to(dev()), w.to(dev())
     base = bits16(out)
     experts.tile_walk = "dynamic"
@@ -225,13 +265,13 @@ def test_a16_has_no_quantized_form():
     assert st == _lib.AFD_ERR_UNSUPPORTED
 
 
-@pytest.fixture(scope="module")
-def dsv4_a16():
-    shape = W.SHAPES["dsv4_rank"]
-    say(f"full-size W4A16 layer {shape.name}: packing weights")
+@pytest.fixture(scope="module", params=["dsv4_rank", "ernie_fp8"])
+def dsv4_a16(request):
+    shape = W.SHAPES[request.param]
+    say(f"full-size bf16-activation layer {shape.name}: packing weights")
     gen = W.generator("cpu", 1)
     w13, w2 = W.expert_weights(shape.num_local, shape.hidden, shape.inter, gen, "cpu")
-    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, pack_mxfp4_experts(w13, w2, device=dev()),
+    experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, PACK[shape.fmt](w13, w2, device=dev()),
                          n_max=shape.tokens, act_format="bf16")
     x, ids, w = W.job(shape, seed=0, device="cpu")
     job = (x.to(dev()), ids.to(torch.int32).to(dev()), w.to(torch.float32).to(dev()))
@@ -271,9 +311,13 @@ def test_dsv4_a16_properties(dsv4_a16):
 
 
 def test_dsv4_a16_subset_against_oracle(dsv4_a16):
-    """Tokens whose local experts all lie in [0, 4) (plus tokens with no local expert) against
-    the oracle run with those 4 experts only."""
+    """MXFP4: tokens whose local experts all lie in [0, 4) (plus tokens with no local expert)
+    against the oracle run with those 4 experts only. FP8 blocks (every expert local, 8 per
+    token): the tokens whose 8 experts are all among the 16 most used, those experts renumbered
+    for the oracle (a token's result does not depend on the numbering)."""
     shape, experts, (w13, w2), (xc, idsc, wc), _, out = dsv4_a16
+    if shape.fmt != "mxfp4":
+        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
     say(f"{shape.name} W4A16: tokens of 4 experts against the oracle")
     lo, keep = shape.local.start, 4
     ids = idsc.numpy()
@@ -291,3 +335,22 @@ def test_dsv4_a16_subset_against_oracle(dsv4_a16):
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
     assert err <= REL_L2_TOL
     assert not got[~has_kept[sub]].any()
+
+
+def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
+    w13, w2 = weights
+    xc, idsc, wc = job
+    rel = idsc.numpy() - shape.local.start
+    counts = np.bincount(rel.ravel(), minlength=len(shape.local))
+    chosen = np.argsort(-counts, kind="stable")[:keep]
+    table = np.full(len(shape.local), -1, dtype=np.int64)
+    table[chosen] = np.arange(keep)
+    sub = np.nonzero((table[rel] >= 0).all(axis=1))[0][:256]
+    say(f"{shape.name} W8A16: {len(sub)} tokens of the {keep} most used experts against the oracle")
+    assert len(sub) >= 128
+    w13d, w2d = fp8_deq(w13[chosen], w2[chosen])
+    ids = table[rel[sub]].astype(np.int32)
+    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="bf16")
+    err = rel_l2(F.bf16_to_f32(bits16(out)[sub]), F.bf16_to_f32(ref))
+    say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
+    assert err <= REL_L2_TOL

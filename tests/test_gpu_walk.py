@@ -1,7 +1,7 @@
 """GPU: the two tile walks of the persistent GEMMs give identical results. "dynamic" hands
 the tiles out from per-XCD counters, "static" gives each workgroup a fixed share; both run
-over the same dense tile order, so every output bit must agree, for both weight formats and
-both MXFP4 activation formats, for jobs from one token (8 row tiles, fewer than the 32 needed
+over the same dense tile order, so every output bit must agree, for both weight formats with
+fp8 or bf16 activations, for jobs from one token (8 row tiles, fewer than the 32 needed
 to split the rows over the XCDs) to thousands, for skewed routing, and while another stream
 holds a parked wait (a CU held by a wait kernel: the dynamic walk must still cover every
 tile).
@@ -31,10 +31,10 @@ PACK = {"mxfp4": pack_mxfp4_experts, "fp8_block": pack_fp8_block_experts}
 
 
 def layer(fmt, hidden, inter, num_local, n_max, seed=0):
-    """fmt: a weight format, or "mxfp4_a16" for MXFP4 weights with bf16 activations."""
+    """fmt: a weight format, with "_a16" for bf16 activations."""
     gen = W.generator("cpu", seed)
     w13, w2 = W.expert_weights(num_local, hidden, inter, gen, "cpu")
-    act = "bf16" if fmt == "mxfp4_a16" else None
+    act = "bf16" if fmt.endswith("_a16") else None
     pack = PACK[fmt.replace("_a16", "")]
     return AfdExperts(num_local, 8, 0, range(0, num_local), pack(w13, w2, device=dev()), n_max=n_max,
                       act_format=act)
@@ -76,7 +76,7 @@ def both(experts, x, topk):
     return outs["static"], outs["dynamic"]
 
 
-@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block", "mxfp4_a16"])
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block", "mxfp4_a16", "fp8_block_a16"])
 def test_walks_agree(fmt):
     experts = layer(fmt, 1024, 512, 32, 4096)
     for n, seed, zipf in ((1, 1, None), (7, 2, None), (300, 3, None), (4096, 4, None), (3000, 5, 1.2)):
