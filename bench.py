@@ -491,7 +491,8 @@ def bench_vendor(args) -> dict:
     """The vendor library's dense e4m3 x e4m3 GEMM (torch._scaled_mm on hipBLASLt, bf16 out,
     per-tensor scales) at the config's two GEMM shapes with the expert call's padded row count
     (every local expert's rows rounded up to 128): the same MFMA rate as the grouped W4A8 and
-    FP8 GEMMs, without their gather, routing and epilogues."""
+    FP8 GEMMs, without their gather, routing and epilogues. With ``--act bf16`` the dense bf16 x
+    bf16 GEMM (torch.mm on hipBLASLt), the MFMA rate of the bf16-activation GEMMs."""
     import torch
 
     from sgl_asap_amd import workloads as W
@@ -506,13 +507,17 @@ def bench_vendor(args) -> dict:
     counts = torch.bincount(local.flatten().long(), minlength=hi - lo)
     padded = int(((counts + 127) // 128 * 128).sum())
     out = {}
+    bf16 = args.act == "bf16"
     for name, (m, nn, k) in (("gate_up", (padded, 2 * shape.inter, shape.hidden)),
                              ("down", (padded, shape.hidden, shape.inter))):
-        a = torch.randn(m, k, device=dev).to(torch.float8_e4m3fn)
-        b = torch.randn(nn, k, device=dev).to(torch.float8_e4m3fn)
+        dt = torch.bfloat16 if bf16 else torch.float8_e4m3fn
+        a = torch.randn(m, k, device=dev).to(dt)
+        b = torch.randn(nn, k, device=dev).to(dt)
         one = torch.ones((), device=dev)
 
         def mm():
+            if bf16:
+                return torch.mm(a, b.t())
             return torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
 
         for _ in range(args.warmup):
@@ -528,16 +533,17 @@ def bench_vendor(args) -> dict:
         out[name] = {"m": m, "n": nn, "k": k, "us": round(us, 1), "tflops": round(2 * m * nn * k / us / 1e6, 1)}
         del a, b
     return {
-        "metric": "dense fp8 GEMM throughput of the vendor library at the expert call's GEMM shapes",
+        "metric": f"dense {'bf16' if bf16 else 'fp8'} GEMM throughput of the vendor library at the expert call's GEMM shapes",
         "value": out["gate_up"]["tflops"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "higher_is_better": True,
-        "dtype": "e4m3 x e4m3 -> bf16",
+        "dtype": "bf16 x bf16 -> bf16" if bf16 else "e4m3 x e4m3 -> bf16",
         "data": "synthetic (N(0,1) operands)",
-        "config": {"workload": f"{args.config}: {padded} padded rows (torch._scaled_mm, hipBLASLt)"},
+        "config": {"workload": f"{args.config}: {padded} padded rows "
+                               f"({'torch.mm' if bf16 else 'torch._scaled_mm'}, hipBLASLt)"},
         "gemms": out,
     }
 
