@@ -60,7 +60,7 @@
 extern "C" {
 #endif
 
-#define AFD_ABI_VERSION 4
+#define AFD_ABI_VERSION 5
 
 typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
 
@@ -147,9 +147,12 @@ typedef struct afd_moe_cfg {
  *    n*64 + 16*(c ^ (((n >> 1) ^ (n >> 2)) & 3)); scale j of row n at 16384 + 4n + (2(j & 1) | (j >> 1)). w13 rows
  *    interleave gate and up in groups of 32 (physical row 64j+q is gate row 32j+q for
  *    q < 32, else up row 32j+q-32). s13 and s2 are not used (NULL).
- *  FP8_BLOCK: w13 u8 [E][2I][H], s13 f32 [E][2I/128][H/128], w2 u8 [E][H][I],
- *    s2 f32 [E][H/128][I/128]; w13 rows interleave gate and up in groups of 32 as above,
- *    while s13 keeps logical block order (gate blocks, then up blocks). */
+ *  FP8_BLOCK: w13 / w2 are FP8 images, the e4m3 bytes of one 64-wide K stage of one 256-row
+ *    tile: [E][N/256][K/64][256 x 64 B] (16384 bytes each), 16-byte chunk c (16 e4m3 values)
+ *    of row n at byte n*64 + 16*(c ^ (((n >> 1) ^ (n >> 2)) & 3)) as in an MXFP4 tile;
+ *    s13 f32 [E][2I/128][H/128], s2 f32 [E][H/128][I/128]. w13 rows interleave gate and up
+ *    in groups of 32 as above, while s13 keeps logical block order (gate blocks, then up
+ *    blocks). */
 typedef struct afd_expert_weights {
   const void* w13;
   const void* s13;
@@ -173,8 +176,10 @@ typedef struct afd_ws_layout {
   uint64_t num_tiles;      /* i32 [1] row tiles in use */
   uint64_t hist;           /* i32 router scratch */
   uint64_t hq, hs;         /* intermediate activations and their scales (MXFP4: down A tile
-                              images, scales inside, hs empty; bf16 activations: bf16 images
-                              of 128 rows x 128 K (MXFP4) or 64 K (FP8 block), hs empty) */
+                              images, scales inside, hs empty; FP8 block: FP8 images of 256
+                              rows x 64 K [row tiles][I/64], hs f32 [row tiles][I/128][256];
+                              bf16 activations: bf16 images of 128 rows x 128 K (MXFP4) or
+                              64 K (FP8 block), hs empty) */
   uint64_t y;              /* bf16 [np_max][H] per-pair down outputs */
   int64_t np_max;          /* padded rows reserved: n*k + E*(block_m-1), rounded up */
   int32_t block_m;         /* row tile of the grouped GEMMs */
@@ -189,8 +194,10 @@ int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_layout* out);
 
 /* ---- weight packing (load time) -------------------------------------------------------
  * w: fp32 [mats][rows][cols] logical weights (for gate_up = 1: rows = 2I = [gate; up]).
- * afd_pack_mxfp4 writes mats * rows * (cols/2 + cols/32) bytes of tile images to `out`
- * (rows a multiple of 256, cols of 128). */
+ * afd_pack_mxfp4 writes mats * rows * (cols/2 + cols/32) bytes of tile images to `out`;
+ * afd_pack_fp8_block writes mats * rows * cols bytes of FP8 images to q and the fp32
+ * 128x128 block scales [mats][rows/128][cols/128] (logical block order) to s. Rows a
+ * multiple of 256, cols of 128. */
 int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_t cols, int32_t gate_up,
                    uint8_t* out, afd_stream_t stream);
 int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
@@ -200,9 +207,9 @@ int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
  * afd_repack_mxfp4: codes u8 [mats][rows][cols/2] int8-packed e2m1 (element 2i in the low
  * nibble) + scales u8 [mats][rows][cols/32] E8M0, the checkpoint layout -> the tile images
  * afd_pack_mxfp4 writes (same size, same limits), holding the checkpoint's codes and scales
- * exactly. afd_repack_fp8_block: codes e4m3 [mats][rows][cols] -> the kernel's row order
- * (with gate_up = 1 the 32-row gate/up interleave, else a copy; rows a multiple of 128, of
- * 256 with gate_up; cols of 128); the fp32 128x128 block scales keep their logical order and
+ * exactly. afd_repack_fp8_block: codes e4m3 [mats][rows][cols] -> the FP8 images
+ * afd_pack_fp8_block writes (with gate_up = 1 through the 32-row gate/up interleave; rows a
+ * multiple of 256, cols of 128); the fp32 128x128 block scales keep their logical order and
  * are used as they are. Pointers 16-byte aligned. */
 int afd_repack_mxfp4(const uint8_t* codes, const uint8_t* scales, int64_t mats, int32_t rows,
                      int32_t cols, int32_t gate_up, uint8_t* out, afd_stream_t stream);

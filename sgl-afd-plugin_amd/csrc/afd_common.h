@@ -275,6 +275,12 @@ constexpr int kImgK = 128;                        // K values per image
 // The W4A16 GEMMs' bf16 A block of one K stage (128 rows x 128 bf16, rows XOR-swizzled by
 // 16-byte chunk; afd_gemm_a16.hip): 32 KiB, no scales.
 constexpr int kImgA16 = kImgARows * kImgK * 2;
+// FP8 images (FP8 128x128-block weights, and the W8A8 down GEMM's e4m3 A operand): 64 K values
+// of e4m3 per row, laid out as a B image's data (img_b_off), no scales: 256 weight rows = 16
+// KiB, 128 activation rows = 8 KiB. The fp32 block scales stay in tables of their own.
+constexpr int kF8K = 64;
+constexpr int kImgF8B = kImgBRows * kF8K;  // 16384
+constexpr int kImgF8A = kImgARows * kF8K;  // 8192
 // The MX GEMM copies an A image's 512 B of scales as a 1 KiB piece, reading the 512 B that
 // follow; buffers of A images keep that much readable memory after their last image.
 constexpr int kImgReadSlack = 512;
@@ -291,6 +297,13 @@ __host__ __device__ __forceinline__ int img_a_off(int r, int c) {
 // byte offset of logical 16-byte chunk c (0..3) of row n in a B image
 __host__ __device__ __forceinline__ int img_b_off(int n, int c) {
   return n * 64 + ((c ^ (((n >> 1) ^ (n >> 2)) & 3)) << 4);
+}
+// FP8 weights [mats][rows][cols] as images [mats][rows / 256][cols / 64]: byte offset of the
+// image that holds physical row `row`, columns [col - col % 64, + 64)
+__host__ __device__ __forceinline__ int64_t fp8_image_offset(int64_t mat, int64_t row, int64_t col,
+                                                             int rows, int cols) {
+  return ((mat * (rows / kImgBRows) + row / kImgBRows) * (cols / kF8K) + col / kF8K) *
+         int64_t(kImgF8B);
 }
 
 // ---------------------------------------------------------------- direct global -> LDS copies

@@ -2,7 +2,8 @@
 // nothing is quantized on the activation side), for both weight formats:
 //   W4A16: MXFP4 weights (the tile images afd_pack_mxfp4 writes: 256 rows x 128 K of e2m1
 //          codes + UE8M0 scales per image),
-//   W8A16: FP8 128x128-block weights (e4m3 rows [E][N][K] + fp32 block scales).
+//   W8A16: FP8 128x128-block weights (the FP8 images afd_pack_fp8_block writes: 256 rows x
+//          64 K of e4m3 per image, + fp32 block scales).
 //
 //   gate_up: h[p, :] = bf16(act(x_t . Wg_e^T, x_t . Wu_e^T)) for every padded row p of expert
 //            e (t = token of the pair at row p), written as the down GEMM's bf16 A images.
@@ -25,8 +26,8 @@
 //   W4A16: 128 K per stage: the bf16 A block (128 rows x 256 B = 32 KiB, "A16 image") and the
 //          tile's WN/2 B images (17 KiB each), in a ring of 2 stages (WN = 4, 132 KiB) or 3;
 //   W8A16: 64 K per stage: the bf16 A block (128 rows x 128 B = 16 KiB, "A8 image") and the
-//          tile's weight rows gathered from [E][N][K] (16 KiB per 256 rows, laid out as an
-//          e2m1 B image's data), in a ring of 3 stages (WN = 4: 144 KiB).
+//          tile's WN/2 FP8 images (16 KiB each, laid out as an e2m1 B image's data), in a ring
+//          of 3 stages (WN = 4: 144 KiB).
 // The two wavefronts of a SIMD ping-pong in phases of 64 K (32 MFMAs of 32 clk per wavefront,
 // the W4A8 kernel's phase length), so one of them always feeds the matrix pipe while the
 // other reads its fragments.
@@ -61,7 +62,7 @@ struct A16GemmArgs {
   const afd_job* rows_desc;     // gate_up: if set, a_rows is its x (read when the kernel runs)
   int topk;                     // gate_up: pairs per token (token of pair p = p / topk)
   uint32_t topk_magic;          // div_magic(topk)
-  const uint8_t* b_img;         // MXFP4: B images [E][N/256][K/128]; FP8: e4m3 rows [E][N][K]
+  const uint8_t* b_img;         // MXFP4: B images [E][N/256][K/128]; FP8: images [E][N/256][K/64]
   const float* b_scale;         // FP8: block scales [E][N/128][K/128] (gate blocks, then up)
   const int32_t* sorted_pairs;  // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;   // [row tiles]
@@ -98,7 +99,7 @@ template <>
 struct A16Fmt<kWFp8> {
   static constexpr int kStageK = 64;
   static constexpr int kLdsA = kImgData;  // 128 rows x 128 B (the W4A8 A image's swizzle)
-  static constexpr int kLdsB = kImgData;  // 256 rows x 64 B (the e2m1 B image's swizzle)
+  static constexpr int kLdsB = kImgF8B;  // an FP8 image: 256 rows x 64 B (the e2m1 B image's swizzle)
   static constexpr int kBData = 16;
   __host__ __device__ static int a_off(int r, int c) { return img_a_off(r, c); }
 };
@@ -185,13 +186,6 @@ __global__ __launch_bounds__((A16Tile<WF, WN>::kThreads)) void a16_gemm_kernel(A
   const int b_lane = T::kLdsA + bimg * F::kLdsB + img_b_off(brow + lr, kFp8 ? 2 * lk : lk);
   const int sb_lane = T::kLdsA + bimg * F::kLdsB + kImgData + 4 * (brow + lr) + 2 * lk;
 
-  // FP8 weights: lane l copies, for its piece q' (16 rows) of a 256-row block, physical chunk
-  // l % 4 of row 16 q' + l / 4 of the block, i.e. logical chunk (l % 4) ^ swizzle(row), from
-  // that weight row of [E][N][K]. The swizzle only reads row bits below 4, which are l / 4, so
-  // the lane's offset is the same for every piece (the piece's rows go into its base address).
-  const uint32_t b_voff =
-      static_cast<uint32_t>((lane >> 2) * p.K + (((lane & 3) ^ (((lane >> 3) ^ (lane >> 4)) & 3)) << 4));
-
   // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A block from the
   // token rows: lane l copies, for its piece q, physical chunk l % C of row R (w kAQ + q) +
   // l / C of the block (C = 16-byte chunks per row, R = rows per piece), i.e. logical chunk
@@ -232,10 +226,8 @@ __global__ __launch_bounds__((A16Tile<WF, WN>::kThreads)) void a16_gemm_kernel(A
   auto copy_tile = [&](int mt, int nt, int64_t e) {
     a_tile = MODE == kDown ? p.a_img + int64_t(mt) * KT * T::kLdsA
                            : reinterpret_cast<const uint8_t*>(a_rows);
-    if constexpr (kFp8)
-      b_tile = p.b_img + (e * p.N + int64_t(nt) * kBN) * p.K;
-    else
-      b_tile = p.b_img + (e * (p.N / kImgBRows) + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
+    constexpr int64_t kImgBytes = kFp8 ? kImgF8B : kImgB;
+    b_tile = p.b_img + (e * (p.N / kImgBRows) + int64_t(nt) * T::kBImgs) * KT * kImgBytes;
   };
   // this wavefront's copies of stage kt into ring slot kt % kStages: its A pieces, its data
   // pieces of every 256-row weight block, and (MXFP4) for w < kBImgs the scale piece of image w
@@ -253,12 +245,7 @@ __global__ __launch_bounds__((A16Tile<WF, WN>::kThreads)) void a16_gemm_kernel(A
       constexpr int q = decltype(qc)::value;
       constexpr int img = q / T::kQP;
       const int off = (w_u * T::kQP + q % T::kQP) * 1024;
-      if constexpr (kFp8)
-        lds_dma16(st + T::kLdsA + img * F::kLdsB + off,
-                  b_tile + (int64_t(256 * img + 16 * (w_u * T::kQP + q % T::kQP)) * p.K + int64_t(kt) * kStageK),
-                  b_voff);
-      else
-        lds_dma16(st + T::kLdsA + img * kImgB + off, b_tile + (int64_t(img) * KT + kt) * kImgB + off, voff);
+      lds_dma16(st + T::kLdsA + img * F::kLdsB + off, b_tile + (int64_t(img) * KT + kt) * F::kLdsB + off, voff);
     });
     if constexpr (!kFp8) {
       if (w_u < T::kBImgs)

@@ -1,33 +1,39 @@
 // Grouped FP8-e4m3 GEMMs with 128x128-block fp32 weight scales and 1x128 fp32 activation
-// scales (the block-FP8 expert format) on gfx950 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4 with
-// unit scales, e4m3 x e4m3).
+// scales (W8A8, the block-FP8 expert format) on gfx950 MFMA (v_mfma_scale_f32_32x32x64_f8f6f4
+// with unit scales, e4m3 x e4m3).
 //
-//   gate_up: h[p, :] = silu(x_t . Wg_e^T) * (x_t . Wu_e^T) for every padded row p of expert e
+//   gate_up: h[p, :] = act(x_t . Wg_e^T, x_t . Wu_e^T) for every padded row p of expert e
 //            (t = token of the pair at row p), quantized to e4m3 with one fp32 scale per 1x128
-//            group (the down GEMM's A operand and its scales).
+//            group: the down GEMM's A operand (FP8 images of 128 rows x 64 K) and its scales.
 //   down:    y[p, :] = bf16(h_p . W2_e^T).
 //
-// Block scales: a 128-wide K stage kb is exactly one scale block of both operands, with the
-// product s_kb = s_x[row, kb] * s_w[block, kb]; the result is sum_kb s_kb * P_kb, P_kb the
-// stage's unscaled MFMA sum. The accumulators hold R_kb = (sum_{k <= kb} s_k P_k) / s_kb: before
-// stage kb's MFMAs they are multiplied by s_{kb-1} / s_kb, the MFMAs then add P_kb, and the
-// epilogue multiplies by the last s. This costs no second set of registers for the partial
-// sums and one multiply per accumulator and stage; it rounds differently from folding each
-// stage separately by about one fp32 rounding per stage (relative 2^-24 each). The MFMA
-// operands are swapped (weights first, activations second), so a lane's accumulators all
-// belong to one activation row and s_kb is one value per 32x32 tile.
+// Block scales: the 64-K stages 2 kb and 2 kb + 1 make up scale block kb of both operands,
+// with s_kb = s_x[row, kb] * s_w[block, kb]; the result is sum_kb s_kb * P_kb, P_kb the
+// block's unscaled MFMA sum. The accumulators hold R_kb = (sum_{k <= kb} s_k P_k) / s_kb: at
+// the first stage of block kb > 0 they are multiplied by s_{kb-1} / s_kb (in the wavefront's
+// LDS-read phase, beside the other wavefront's MFMAs), the MFMAs then add P_kb, and the
+// epilogue multiplies by the last s. No second set of registers holds partial sums; the
+// result rounds differently from folding each block separately by about one fp32 rounding
+// per block (relative 2^-24 each). The MFMA operands are swapped (weights first, activations
+// second), so a lane's accumulators all belong to one activation row and s_kb is one value
+// per 32x32 tile and lane.
 //
-// Tiling: a workgroup of 8 wavefronts owns a 128 x 256 output tile; wavefront (g, c) owns rows
-// [64 g, 64 g + 64) and columns [64 c, 64 c + 64): 2 x 2 MFMA tiles, 64 accumulators per lane. Both operands move HBM -> LDS with gfx950's direct global_load_lds in
-// 1 KiB pieces of 8 rows x 128 B, each lane fetching one 16-byte chunk of a row at its own
-// offset, so the activation rows are gathered (gate_up: the token rows through sorted_pairs;
-// down: the tile's rows of h) and the weight rows come straight from the [E][N][K] layout. LDS
-// holds every operand in the swizzled 128-byte-row layout of the MX kernel's A images (no bank
-// conflicts for the MFMA operand reads), in a ring of 3 stages. As in the MX kernel, the two
-// wavefronts of a SIMD (group 0: rows 0-63, group 1: rows 64-127) ping-pong between reading a
-// stage from LDS and running its 8 MFMAs (and rescaling its accumulators), half a stage
-// apart. The persistent workgroups walk the tiles XCD by XCD in blocks of 8 x 4 tiles
-// (TileWalk).
+// Tiling: a workgroup of 8 wavefronts owns a 256 x 256 output tile (the router pads this
+// format's expert segments to 256 rows, so a row tile is one expert's); wavefront (wm, wn)
+// owns 64 x 128 = 2 x 4 MFMA tiles of 32x32 (128 fp32 accumulators per lane), so per MFMA a
+// lane reads 1.5 fragments of 32 bytes from LDS. The square tile needs the fewest operand
+// bytes per MAC that 8 x 128 accumulators allow (a stage moves 33 KiB for 4 M MACs, against
+// 40.5 KiB for a 128 x 512 tile): the copies into LDS, not the matrix pipe, bound these
+// GEMMs. K advances 64 per stage (one MFMA k-step). A stage is the A block (256 rows x 64 B
+// of e4m3: gate_up gathers the token rows through sorted_pairs, down copies one FP8 image of
+// h), the tile's FP8 weight image (16 KiB, contiguous in HBM: afd_pack_fp8_block's layout)
+// and the 256 activation rows' scales of the stage's K block; everything moves HBM -> LDS
+// with gfx950's direct global_load_lds (1 KiB pieces, the scales as 4-byte words), into a
+// ring of 3 stages. Both operands keep the e2m1 B image's swizzled 64-byte rows (img_b_off)
+// in LDS: the 16-byte chunks an MFMA operand read takes from 16 consecutive rows fall on 16
+// distinct 16-byte bank groups. The two wavefronts of a SIMD ping-pong between reading a
+// stage's fragments and running its 8 MFMAs (as the W4A8 and W4A16 kernels), and the
+// persistent workgroups walk the tiles XCD by XCD (TileWalk), statically or by claims.
 #include <type_traits>
 
 #include "afd_common.h"
@@ -37,55 +43,20 @@ namespace afd {
 namespace fp8 {
 
 // gate_up with SwiGLU, gate_up with an activation that takes constants (SiTU, or SwiGLU with
-// a limit: SiTU's longer epilogue would raise the register pressure of the SwiGLU kernel),
-// down
+// a limit), down
 enum { kGateUp = 0, kDown = 1, kGateUpParam = 2 };
 
-// Tile walk blocks of 8 row tiles x 4 column tiles: a 1 MiB weight slice is shared 8 ways
-// (column-tile-fastest walks fetch ~3x more from beyond L2).
+// Tile walk blocks of 8 row tiles: a weight slice is shared by 8 row tiles of its expert in L2.
 constexpr int kWalkRows = 8;
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = kBlockM;  // 128 activation rows
-constexpr int kBN = 256;      // weight rows (output columns)
-constexpr int kBK = 128;      // K per stage = one scale block
-// LDS stage: activations (128 rows x 128 B), their 128 fp32 scales, weights (256 rows x 128 B)
-constexpr int kXScales = kBM * kBK;         // 16384
-constexpr int kWOff = kXScales + kBM * 4;   // 16896
-constexpr int kStage = kWOff + kBN * kBK;   // 49664
-constexpr int kStages = 3;
-// after the ring: the tile's weight block scales for every K stage, two blocks x 32 stages
-// per 256 B group (written by one wavefront's dword copies)
-constexpr int kWScales = kStages * kStage;
-constexpr int kMaxKT = 128;
-// then the gate_up epilogue's per-row amax of each column wavefront, [128 rows][4]
-constexpr int kAmax = kWScales + 2 * kMaxKT * 4;
-constexpr int kLds = kAmax + kBM * 4 * 4;
-// copies per wavefront and stage: 2 activation pieces, 4 weight pieces and one piece of
-// activation scales (a wavefront past the two halves repeats its first weight piece: the same
-// bytes to the same place), so every wavefront counts the same number of copies
-constexpr int kQX = kBM / 8 / kWaves;  // 2
-constexpr int kQW = kBN / 8 / kWaves;  // 4
-constexpr int kPieces = kQX + kQW + 1;
-// the down epilogue's bf16 tile: kBM rows of kBN / 8 16-byte chunks, chunk c of row r at
-// physical chunk c ^ (r % 16), so the 16 rows a 16-lane pass of a write covers (one logical
-// chunk each) and the 16 consecutive chunks a pass of a read covers (one row) fall on 16
-// distinct 16-byte bank groups
-constexpr int kYChunks = kBN / 8;
-static_assert(kQX * kWaves * 8 == kBM && kQW * kWaves * 8 == kBN, "pieces cover the tile");
-static_assert(kBM * kBN * 2 <= kStages * kStage, "down epilogue tile must fit the stages");
-static_assert(kLds <= 160 * 1024, "LDS of one CU");
-static_assert(2 * kPieces < 64, "vmcnt is a 6-bit counter");
-
 struct Fp8GemmArgs {
-  const uint8_t* a;   // gate_up: token rows xq [n][K]; down: hq [np][K]
-  const float* as;    // their scales: xs [n][K/128]; hs [np][K/128]
-  const afd_job* rows_desc;  // gate_up: if set, a / as are its xq / xs
+  const uint8_t* a;          // gate_up: token rows xq [n][K]; down: h images [row tiles][K/64]
+  const float* as;           // gate_up: xs [n][K/128]; down: hs [row tiles][K/128][128]
+  const afd_job* rows_desc;  // gate_up: if set, a / as are its xq / xs (read when the kernel runs)
   int topk;
   uint32_t topk_magic;  // div_magic(topk)
-  const uint8_t* b;     // e4m3 [E][N][K] (gate_up rows interleaved gate/up by 32)
-  const float* bs;      // [E][N/128][K/128] in logical block order
+  const uint8_t* b;     // FP8 images [E][N/256][K/64] (gate_up rows interleaved gate/up by 32)
+  const float* bs;      // [E][N/128][K/128] in logical block order (gate blocks, then up)
   const int32_t* sorted_pairs;    // [np] flat pair index per padded row, -1 = pad
   const int32_t* tile_expert;     // [row tiles]
   const int32_t* num_tiles;       // [1]
@@ -94,138 +65,172 @@ struct Fp8GemmArgs {
   uint32_t* walk_ctr;             // [8] zeroed tile counters (one per XCD); nullptr: static walk
   int K, N;
   ActParams act;  // gate_up: the activation
-  uint8_t* hq;  // gate_up out: e4m3 [np][N/2]
-  float* hs;    // gate_up out: fp32 [np][N/256]
-  uint16_t* y;  // down out: bf16 [np][N]
+  uint8_t* hq;    // gate_up out: h images [row tiles][N/2/64]
+  float* hs;      // gate_up out: h scales [row tiles][N/2/128][128]
+  uint16_t* y;    // down out: bf16 [np][N]
 };
 
+// The tile: 256 activation rows (two 128-row blocks of one expert: the router pads this
+// format's expert segments to 256 rows) x 256 weight rows. Eight wavefronts, (wm, wn) =
+// (w / 2, w % 2), own 64 x 128 each; wavefronts w and w + 4 share a SIMD, so the ping-pong
+// groups are w < 4 (rows 0-127) and w >= 4 (rows 128-255).
+struct Tile {
+  static constexpr int kWaves = 8;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kBM = kFp8BlockM;
+  static constexpr int kBN = 256;
+  // LDS stage: A block (256 rows x 64 B), the weight image (256 rows x 64 B), the 256
+  // activation rows' fp32 scales of the stage's K block
+  static constexpr int kBOff = kImgF8B;
+  static constexpr int kAScale = 2 * kImgF8B;
+  static constexpr int kStage = kAScale + kBM * 4;
+  static constexpr int kStages = 3;
+  static constexpr int kRing = kStages * kStage;
+  // down: its epilogue's bf16 tile over the ring. gate_up: after the ring, the epilogue's
+  // per-row amax of each column wavefront, [2][256 rows], then the tile's activation-row
+  // scales for every K block (the scale table, filled once per tile; see the kernel)
+  static constexpr int kYBytes = kBM * kBN * 2;
+  static constexpr int kDownLds = kRing > kYBytes ? kRing : kYBytes;
+  static constexpr int kAmax = kRing;
+  static constexpr int kTab = kAmax + 2 * kBM * 4;
+  static constexpr int kTabMaxQ = 7;  // table pieces per wavefront: K up to 7168
+  static constexpr int kGateUpLds = kTab + kWaves * kTabMaxQ * 1024;
+  static constexpr int kLds = kDownLds > kGateUpLds ? kDownLds : kGateUpLds;
+  // per wavefront and stage: 2 pieces of the A block and 2 of the weight image; wavefronts
+  // 0-3 also copy the scale words of rows [64 w, 64 w + 64)
+  static constexpr int kAQ = (kImgF8B / 1024) / kWaves;
+  static constexpr int kQP = (kImgF8B / 1024) / kWaves;
+  static constexpr int kPiecesMin = kAQ + kQP;  // pieces of a wavefront without scales
+  static constexpr int kYChunks = kBN / 8;
+  static_assert(kBM == 256 && kAQ * kWaves * 1024 == kImgF8B, "pieces cover a stage");
+  static_assert((kStage & 255) == 0, "slot offsets leave the fragment addresses' low 8 bits alone");
+  static_assert(kLds + 256 <= 160 * 1024, "LDS of one CU");
+  template <int MODE>
+  static constexpr int lds_bytes() { return MODE == 1 ? kDownLds : kGateUpLds; }
+  static_assert(kStages * (kPiecesMin + 1) < 64, "vmcnt is a 6-bit counter");
+};
+
+// A uniform read of data the kernel never writes (the weight block scales), through the
+// scalar cache: a vector load's wait would drain the copies in flight.
+__device__ __forceinline__ float load_uniform(const float* p) {
+  return *(const __attribute__((address_space(4))) float*)p;
+}
+
 template <int MODE>
-__global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
+__global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
+  using T = Tile;
+  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[T::lds_bytes<MODE>()];
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
-  const int wm = w_u / 4, wn = w_u % 4, lr = lane & 31, lk = lane >> 5;
+  const int wm = w_u >> 1, wn = w_u & 1, lr = lane & 31, lk = lane >> 5;
   const TileWalk<kWalkRows> walk(p.num_tiles[0], p.N / kBN, blockIdx.x, gridDim.x, p.walk_ctr);
   __shared__ int claimed[2];  // the claimed walk positions lane 0 publishes (as in the MX kernel)
-  const int KT = p.K / kBK;
-  const int nblk = p.N / kBK;  // weight scale blocks along N
+  const int KT = p.K / kF8K;
+  const int kb_n = p.K / 128;  // scale blocks along K
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
-
-  // Copy offsets. Piece q of a wavefront covers 8 rows: image row r = 8 (w Q + q) + lane / 8,
-  // physical chunk lane % 8, i.e. logical chunk (lane % 8) ^ swizzle(r) of the source row.
-  // Weight rows and down's h rows are fixed per lane (the tile is a scalar base); gate_up's
-  // rows are token rows, looked up per tile. Wavefronts 0 and 1 also copy the activation
-  // scales of rows [64 w, 64 w + 64).
-  auto chunk = [&](int r) { return (lane & 7) ^ ((r ^ (r >> 3)) & 7); };
-  uint32_t w_voff[kQW];
-#pragma unroll
-  for (int q = 0; q < kQW; ++q) {
-    const int r = 8 * (w_u * kQW + q) + (lane >> 3);
-    w_voff[q] = static_cast<uint32_t>(r * p.K + chunk(r) * 16);
-  }
-  const bool copies_scales = w_u < 2;
-  const int s_row = 64 * (w_u & 1) + lane;
-
-  // A tile's metadata is loaded one tile ahead and decoded after the previous tile's K loop,
-  // whose last wait leaves no copy in flight, so no tile starts by waiting for a load.
-  int sp_next[kQX + 1], e_next = 0;
-  auto load_next = [&](int ii) {
-    int m, nn;
-    walk.at_dense(ii, m, nn);
-    e_next = p.tile_expert[m];
-    if constexpr (MODE != kDown) {
-#pragma unroll
-      for (int q = 0; q < kQX; ++q)
-        sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * kQX + q) + (lane >> 3)];
-      sp_next[kQX] = p.sorted_pairs[m * kBM + s_row];
-    }
-  };
-  int e_cur = 0;
-  uint32_t x_voff[kQX], s_voff;
-  // down: rows of the tile, relative to the tile's first row
-#pragma unroll
-  for (int q = 0; q < kQX; ++q) {
-    const int r = 8 * (w_u * kQX + q) + (lane >> 3);
-    x_voff[q] = static_cast<uint32_t>(r * p.K + chunk(r) * 16);
-  }
-  s_voff = static_cast<uint32_t>(s_row * KT * 4);
-  auto decode_next = [&]() {
-    e_cur = __builtin_amdgcn_readfirstlane(e_next);
-    if constexpr (MODE != kDown) {
-      // padding rows (-1) read token 0; their results are never used
-      auto token = [&](int sp) {
-        return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
-      };
-#pragma unroll
-      for (int q = 0; q < kQX; ++q) {
-        const int r = 8 * (w_u * kQX + q) + (lane >> 3);
-        x_voff[q] = token(sp_next[q]) * static_cast<uint32_t>(p.K) + chunk(r) * 16;
-      }
-      s_voff = token(sp_next[kQX]) * static_cast<uint32_t>(KT * 4);
-    }
-  };
-  // The tile whose stages the copies below fetch. gate_up starts the next tile's copies
-  // (weight scales and the first two stages) right after its own K loop: its epilogue works
-  // from registers and a small LDS area outside the ring, so the copies land while it runs.
-  // down's epilogue stages its output through the ring, so it starts them at the tile start.
-  constexpr bool kEarlyStart = MODE != kDown;
-  const uint8_t* x_tile = nullptr;
-  const float* s_tile = nullptr;
-  const uint8_t* w_tile = nullptr;
-  int blk0 = 0, blk1 = 0;
-  int64_t e_copy = 0;
+  const uint32_t voff = static_cast<uint32_t>(lane) * 16;
   const uint8_t* a_rows = p.a;
   const float* a_scales = p.as;
   if (MODE != kDown && p.rows_desc != nullptr) {
     a_rows = p.rows_desc->xq;
     a_scales = static_cast<const float*>(p.rows_desc->xs);
   }
-  auto copy_tile = [&](int mt, int nt, int64_t e) {
-    x_tile = MODE != kDown ? a_rows : a_rows + int64_t(mt) * kBM * p.K;
-    s_tile = MODE != kDown ? a_scales : a_scales + int64_t(mt) * kBM * KT;
-    w_tile = p.b + (e * p.N + int64_t(nt) * kBN) * int64_t(p.K);
-    // the two weight scale blocks of the tile: gate_up (gate, up) of its 128 h columns;
-    // down the two 128-row blocks (wavefront columns 64 c use block c / 2)
-    blk0 = MODE != kDown ? nt * kBN / 256 : nt * kBN / 128;
-    blk1 = MODE != kDown ? nblk / 2 + nt * kBN / 256 : nt * kBN / 128 + 1;
-    e_copy = e;
-  };
-  auto issue_piece = [&](int kt, auto qc) {
-    constexpr int q = decltype(qc)::value;
-    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
-    if constexpr (q < kQX) {
-      lds_dma16(st + (w_u * kQX + q) * 1024, x_tile + kt * kBK, x_voff[q]);
-    } else if constexpr (q < kQX + kQW) {
-      constexpr int qw = q - kQX;
-      lds_dma16(st + kWOff + (w_u * kQW + qw) * 1024, w_tile + kt * kBK, w_voff[qw]);
-    } else {
-      if (copies_scales)
-        lds_dma4(st + kXScales + (w_u & 1) * 256, s_tile + kt, s_voff);
-      else
-        lds_dma16(st + kWOff + w_u * kQW * 1024, w_tile + kt * kBK, w_voff[0]);
-    }
-  };
-  auto issue = [&](int kt) { static_for<kPieces>([&](auto q) { issue_piece(kt, q); }); };
-  const int last = KT - 1;
-  // Wavefront 0 first copies the tile's weight block scales (lane x: block x < 32 ? blk0 :
-  // blk1, stage 32 g + x % 32, clamped in bounds); those copies are older than every piece of
-  // stage 0, so the wait for stage 0 covers them. Then the first two stages.
-  auto start_copies = [&]() {
-    if (w_u == 0) {
-      const float* bs_e = p.bs + e_copy * nblk * KT;
-      const int b = lk == 0 ? blk0 : blk1;
-      for (int g = 0; g * 32 < KT; ++g) {
-        const int kb = min(lr + 32 * g, KT - 1);
-        lds_dma4(lds_base + kWScales + g * 256, bs_e, static_cast<uint32_t>((b * KT + kb) * 4));
-      }
-    }
-    issue(0);
-    issue(min(1, last));
+  // fragment bases of the lane in a stage: A row 64 wm + lr and weight row 128 wn + lr, each
+  // at logical chunk lk (the operand's first 16 bytes; its second 16 are logical chunk lk + 2,
+  // i.e. the address with bit 5 flipped). Rows + 32 i keep the swizzle.
+  const int a_lane = img_b_off(wm * 64 + lr, lk);
+  const int b_lane = T::kBOff + img_b_off(wn * 128 + lr, lk);
+  // gate_up's activation-row scales: with K a multiple of 512 up to 7168, every row's K-block
+  // scales (K / 128 words, contiguous in xs) are copied once per tile into the scale table;
+  // otherwise wavefronts 0-3 copy the 256 rows' words of each stage's K block into its slot.
+  // The table: wavefront w's pieces q hold rows [32 w, 32 w + 32), lane l = 2 (row % 32) + h
+  // taking 16-byte chunk 2 q + h of row 32 w + l / 2 (the last piece of an odd chunk count
+  // repeats the last chunk).
+  const int tab_chunks = kb_n / 4, tab_q = (tab_chunks + 1) / 2;
+  const bool table = MODE != kDown && kb_n % 4 == 0 && tab_q <= T::kTabMaxQ;
+  const bool copies_scales = w_u < 4 && !table;
+  auto tab_off = [&](int r, int kb) {  // byte offset of row r's scale of K block kb
+    const int c = kb >> 2;
+    return T::kTab + (((r >> 5) * tab_q + (c >> 1)) * 64 + (r & 31) * 2 + (c & 1)) * 16 + (kb & 3) * 4;
   };
 
-  // The walk's dense positions: static, or with p.walk_ctr claimed one tile ahead by lane 0
-  // (the first two here, each later one during the last K stage of the tile before the one
-  // that needs it); see the MX kernel.
+  // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A block from the
+  // token rows: lane l copies, for its piece q (16 rows), physical chunk l % 4 of row
+  // 16 (w kAQ + q) + l / 4 of the block, i.e. logical chunk (l % 4) ^ swizzle(row), from the
+  // row's token; the scale-copying wavefront w < 4 copies the word of row 64 w + l. Padding
+  // rows (-1) read token 0; their results are never stored.
+  int sp_next[T::kAQ + 2], e_next = 0, own_next = -1;
+  auto load_next = [&](int ii) {
+    int m, nn;
+    walk.at_dense(ii, m, nn);
+    e_next = p.tile_expert[m];
+    own_next = p.sorted_pairs[m * kBM + 64 * wm + lane];
+    if constexpr (MODE != kDown) {
+#pragma unroll
+      for (int q = 0; q < T::kAQ; ++q)
+        sp_next[q] = p.sorted_pairs[m * kBM + 16 * (w_u * T::kAQ + q) + (lane >> 2)];
+      sp_next[T::kAQ] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
+      sp_next[T::kAQ + 1] = p.sorted_pairs[m * kBM + 32 * w_u + (lane >> 1)];
+    }
+  };
+  int e_cur = 0, live_cur = 0;
+  uint32_t a_voff[T::kAQ] = {}, s_voff = 0, t_voff = 0;
+  auto decode_next = [&]() {
+    e_cur = __builtin_amdgcn_readfirstlane(e_next);
+    live_cur = __popcll(__ballot(own_next >= 0));  // real rows of this group, a scalar
+    if constexpr (MODE != kDown) {
+      auto token = [&](int sp) {
+        return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
+      };
+#pragma unroll
+      for (int q = 0; q < T::kAQ; ++q) {
+        const int r = 16 * (w_u * T::kAQ + q) + (lane >> 2);
+        const int c = (img_b_off(r, lane & 3) - r * kF8K) >> 4;  // the swizzle is an involution
+        a_voff[q] = token(sp_next[q]) * static_cast<uint32_t>(p.K) + c * 16;
+      }
+      s_voff = token(sp_next[T::kAQ]) * static_cast<uint32_t>(kb_n * 4);
+      t_voff = token(sp_next[T::kAQ + 1]) * static_cast<uint32_t>(kb_n * 4);
+    }
+  };
+  // gate_up starts the next tile's copies right after its own K loop: its epilogue works from
+  // registers and an LDS area past the ring. down's epilogue stages its output through the
+  // ring, so it starts them at the tile start.
+  constexpr bool kEarlyStart = MODE != kDown;
+  const uint8_t* a_tile = nullptr;
+  const float* s_tile = nullptr;
+  const uint8_t* b_tile = nullptr;
+  auto copy_tile = [&](int mt, int nt, int64_t e) {
+    a_tile = MODE != kDown ? a_rows : a_rows + int64_t(mt) * KT * kImgF8B;
+    s_tile = MODE != kDown ? a_scales : a_scales + int64_t(mt) * kb_n * kBM;
+    b_tile = p.b + (e * (p.N / kImgBRows) + nt) * KT * int64_t(kImgF8B);
+  };
+  // this wavefront's copies of stage kt into ring slot kt % kStages: its A pieces, its
+  // weight pieces, and (wavefronts 0-3) scale words
+  auto issue = [&](int kt) {
+    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+    static_for<T::kAQ>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int off = (w_u * T::kAQ + q) * 1024;
+      if constexpr (MODE != kDown)
+        lds_dma16(st + off, a_tile + int64_t(kt) * kF8K, a_voff[q]);
+      else
+        lds_dma16(st + off, a_tile + int64_t(kt) * kImgF8B + off, voff);
+    });
+    static_for<T::kQP>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int off = (w_u * T::kQP + q) * 1024;
+      lds_dma16(st + T::kBOff + off, b_tile + int64_t(kt) * kImgF8B + off, voff);
+    });
+    if (copies_scales) {
+      if constexpr (MODE != kDown)
+        lds_dma4(st + T::kAScale + w_u * 256, s_tile + (kt >> 1), s_voff);
+      else
+        lds_dma4(st + T::kAScale + w_u * 256, s_tile + (kt >> 1) * kBM + 64 * w_u, lane * 4u);
+    }
+  };
+  const int last = KT - 1;
+
   const bool dynamic = p.walk_ctr != nullptr;
   int i = walk.first, i_next = walk.first + walk.stride;
   if (dynamic) {
@@ -241,6 +246,21 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   i = min(i, walk.tiles);
   i_next = min(i_next, walk.tiles);
   uint32_t ticket = 0;  // lives across the tile loop (no write to its register waits for it)
+  // A tile's K loop starts with every ring slot filled: stages 0 .. kStages - 1 (clamped to
+  // the last stage) are issued before it, during the previous tile's epilogue (gate_up) or at
+  // the start of the tile (down).
+  // (gate_up with the scale table: the tile's table pieces first, so the wait for stage 0
+  // covers them; the previous tile's K loop, the table's only reader, has ended by then)
+  auto issue_first = [&]() {
+    if (MODE != kDown && table) {
+      for (int q = 0; q < tab_q; ++q) {
+        const int c = min(2 * q + (lane & 1), tab_chunks - 1);
+        lds_dma16(lds_base + static_cast<uint32_t>(T::kTab + (w_u * tab_q + q) * 1024), s_tile,
+                  t_voff + static_cast<uint32_t>(c * 16));
+      }
+    }
+    static_for<kStages>([&](auto sc) { issue(min(static_cast<int>(decltype(sc)::value), last)); });
+  };
   if (i < walk.tiles) {
     load_next(i);
     decode_next();
@@ -248,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
       int mt, nt;
       walk.at_dense(i, mt, nt);
       copy_tile(mt, nt, e_cur);
-      start_copies();
+      issue_first();
     }
   }
 
@@ -262,140 +282,181 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
     // down: the expert's pairs fill its first rows; rows below row_end are real
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
+    // 32-row blocks of this group with a real row (padding rows come last in a segment)
+    const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
     if (has_next) load_next(i_next);
     if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
 
-    v16f acc[2][2];
+    // The weight block scales of this wavefront's 128 weight rows (uniform): gate_up a gate
+    // block (tiles j even) and an up block (j odd), down one block for both; s_blk[x] points
+    // at the block's row of K-block scales. sw0, sw1: those of the K block being accumulated,
+    // swn0, swn1: of the next one, read a block ahead. The activation rows' scales of the
+    // K block (sx0, sx1: lane rows 64 wm + lr and + 32), read from the stage's scale words.
+    const float* s_blk[2];
+    {
+      const int row0 = n0 + 128 * wn;
+      const float* se = p.bs + e * (p.N / 128) * kb_n;
+      if constexpr (MODE != kDown) {
+        s_blk[0] = se + (row0 / 256) * kb_n;
+        s_blk[1] = se + (p.N / 256 + row0 / 256) * kb_n;
+      } else {
+        s_blk[0] = s_blk[1] = se + (row0 / 128) * kb_n;
+      }
+    }
+    // (named scalars, not arrays: arrays written in the branches below end up in scratch)
+    float sw0 = load_uniform(s_blk[0]), sw1 = load_uniform(s_blk[1]);
+    float swn0 = sw0, swn1 = sw1;
+    float sx0 = 1.0f, sx1 = 1.0f;
+
+    v16f acc[2][4];
 #pragma unroll
     for (int i2 = 0; i2 < 2; ++i2)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
 
-    // Operand fragments of both k-steps of one stage and the stage's scales. An 8-bit operand
-    // lane half h holds K [16h, 16h+16) in bytes 0-15 and K [32+16h, 32+16h+16) in bytes 16-31
-    // of the k-step. x: activation rows 64 g + 32 i + lane % 32; w: weight rows
-    // 64 c + 32 j + lane % 32.
-    struct Frag {
-      v8i x[2][2], w[2][2];  // [ks][i], [ks][j]
-      float sx[2], sw[2];
-    };
-    Frag f;
-    float sx_prev[2] = {1.0f, 1.0f}, sw_prev[2] = {1.0f, 1.0f};
-    const float* wsc = reinterpret_cast<const float*>(lds + kWScales);
+    // The fragments of one stage: an 8-bit operand's lane half h holds K [16 h, 16 h + 16) in
+    // bytes 0-15 and K [32 + 16 h, + 16) in bytes 16-31, i.e. logical chunks h and h + 2 of
+    // the row's 64 bytes.
+    v8i fa[2], fb[4];
     auto read_stage = [&](int kt) {
-      const uint8_t* xb = lds + (kt % kStages) * kStage;
-      const uint8_t* wb = xb + kWOff;
-      // row r + 32 has the swizzle of row r with chunk bit 2 flipped: its chunk c sits 4096 B
-      // after row r's chunk c ^ 4, so four lane addresses serve both row blocks
-      const int rx = wm * 64 + lr, rw = wn * 64 + lr;
+      const int a0 = (kt % kStages) * kStage + a_lane, b0 = (kt % kStages) * kStage + b_lane;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2) {
-          const int kc = (ks ^ i2) * 4 + lk;
-          v4i lo = *reinterpret_cast<const v4i*>(xb + img_a_off(rx, kc) + i2 * 4096);
-          v4i hi = *reinterpret_cast<const v4i*>(xb + img_a_off(rx, kc + 2) + i2 * 4096);
-          f.x[ks][i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          lo = *reinterpret_cast<const v4i*>(wb + img_a_off(rw, kc) + i2 * 4096);
-          hi = *reinterpret_cast<const v4i*>(wb + img_a_off(rw, kc + 2) + i2 * 4096);
-          f.w[ks][i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+      for (int i2 = 0; i2 < 2; ++i2) {
+        const v4i lo = *reinterpret_cast<const v4i*>(lds + a0 + 2048 * i2);
+        const v4i hi = *reinterpret_cast<const v4i*>(lds + (a0 ^ 32) + 2048 * i2);
+        fa[i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
-      const float* sx = reinterpret_cast<const float*>(xb + kXScales);
-      f.sx[0] = sx[wm * 64 + lr];
-      f.sx[1] = sx[wm * 64 + 32 + lr];
-      // block b of stage kt at group kt / 32, half b, word kt % 32
-      const float* sw = wsc + (kt >> 5) * 64 + (kt & 31);
-      if constexpr (MODE != kDown) {
-        f.sw[0] = sw[0];
-        f.sw[1] = sw[32];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const v4i lo = *reinterpret_cast<const v4i*>(lds + b0 + 2048 * j);
+        const v4i hi = *reinterpret_cast<const v4i*>(lds + (b0 ^ 32) + 2048 * j);
+        fb[j] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    };
+    // At the first stage of K block kb (even kt), in the read phase: the block's activation
+    // scales from the slot, the factors s_{kb-1} / s_kb of the accumulators, and the next
+    // block's weight scales read ahead. The multiplies themselves run in the MFMA phase, each
+    // tile's 16 right before its MFMA: the tile's previous MFMA finished a phase ago, and the
+    // next tile's multiplies issue beside this tile's MFMA.
+    float r00 = 1.0f, r01 = 1.0f, r10 = 1.0f, r11 = 1.0f;
+    int kb_next = 0;  // the K block whose weight scales swn0, swn1 hold
+    auto block_scales = [&](int kt) {
+      float x0, x1;
+      if (MODE != kDown && table) {
+        x0 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + lr, kt >> 1));
+        x1 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + 32 + lr, kt >> 1));
       } else {
-        f.sw[0] = f.sw[1] = sw[(wn >> 1) * 32];
+        const float* sxs = reinterpret_cast<const float*>(lds + (kt % kStages) * kStage + T::kAScale);
+        x0 = sxs[wm * 64 + lr];
+        x1 = sxs[wm * 64 + 32 + lr];
       }
+      r00 = (sx0 * sw0) * __builtin_amdgcn_rcpf(x0 * swn0);
+      r01 = (sx0 * sw1) * __builtin_amdgcn_rcpf(x0 * swn1);
+      r10 = (sx1 * sw0) * __builtin_amdgcn_rcpf(x1 * swn0);
+      r11 = (sx1 * sw1) * __builtin_amdgcn_rcpf(x1 * swn1);
+      sw0 = swn0;
+      sw1 = swn1;
+      sx0 = x0;
+      sx1 = x1;
+      kb_next = min(kb_next + 1, kb_n - 1);
+      swn0 = load_uniform(s_blk[0] + kb_next);
+      swn1 = load_uniform(s_blk[1] + kb_next);
     };
-    // The stage's 8 MFMAs. Before its first k-step, a tile's accumulators go from R_{kb-1} to
-    // R_{kb-1} * s_{kb-1} / s_kb (stage kb's scales are in f); those 16 multiplies overlap the
-    // previous tiles' MFMAs. On the first stage the accumulators are 0 and the ratio is unused.
-    auto mma_stage = [&]() {
-      float ratio[2][2];
-#pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          ratio[i2][j] = (sx_prev[i2] * sw_prev[j]) * __builtin_amdgcn_rcpf(f.sx[i2] * f.sw[j]);
-      static_for<2>([&](auto ksc) {
-        constexpr int ks = decltype(ksc)::value;
-        static_for<2>([&](auto i2c) {
-          constexpr int i2 = decltype(i2c)::value;
-          static_for<2>([&](auto jc) {
+    // the stage's 8 MFMAs (D[weight row][activation row]), 32-row blocks of padding skipped;
+    // with `moved`, each tile's accumulators take their factor first
+    auto mma_stage = [&](bool moved) {
+      static_for<2>([&](auto i2c) {
+        constexpr int i2 = decltype(i2c)::value;
+        if (i2 == 0 ? live_i0 : live_i1) {
+          static_for<4>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            if constexpr (ks == 0) {
+            if (moved) {
+              const float r = i2 == 0 ? ((j & 1) ? r01 : r00) : ((j & 1) ? r11 : r10);
 #pragma unroll
-              for (int q = 0; q < 16; ++q) acc[i2][j][q] *= ratio[i2][j];
+              for (int q = 0; q < 16; ++q) acc[i2][j][q] *= r;
             }
-            // D[weight row][activation row]: lane x holds activation row x % 32
             acc[i2][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                f.w[ks][j], f.x[ks][i2], acc[i2][j], 0 /*e4m3*/, 0 /*e4m3*/, 0, 127 /*x1*/, 0,
-                127 /*x1*/);
+                fb[j], fa[i2], acc[i2][j], 0 /*e4m3*/, 0 /*e4m3*/, 0, 127 /*x1*/, 0, 127 /*x1*/);
+            // keeps each tile's multiplies after the previous MFMA (hoisted, they would need
+            // registers for all 128 products at once)
+            if (moved) __builtin_amdgcn_sched_barrier(0);
           });
-        });
+        }
       });
-      sx_prev[0] = f.sx[0];
-      sx_prev[1] = f.sx[1];
-      sw_prev[0] = f.sw[0];
-      sw_prev[1] = f.sw[1];
     };
-
-    // Ping-pong as in the MX kernel: each group copies its pieces of stage kt+2 when it starts
-    // reading stage kt; copies are clamped to the last stage (a clamped copy rewrites a slot
-    // with its own bytes). Epilogue stores of the previous tile still in flight only make the
-    // counted waits stricter (loads complete in order among themselves).
-    if constexpr (!kEarlyStart) start_copies();
-    wait_vmcnt<kPieces>();  // own pieces of stage 0 (and the weight scales) landed
+    // Ping-pong over stages: group 0 reads stage kt + 1 while group 1 multiplies stage kt, and
+    // the other way round; every wavefront meets the others at a barrier every half stage. At
+    // stage kt >= 1 each group copies its pieces of stage kt + 2 into the slot of stage
+    // kt - 1, which both groups finished reading before the barrier that started this read
+    // phase (clamped to the last stage: a clamped copy rewrites a slot with its own bytes, and
+    // keeps every wavefront's count of copies in flight the same at each wait). Before the
+    // barrier after which group 0 reads stage kt + 1, both groups have waited for their pieces
+    // of it: group 0 after its MFMAs of stage kt, group 1 after its reads of stage kt. The
+    // counted waits allow one later stage in flight (a wavefront that also copies scale words
+    // waits for one piece more than it needs).
+    if constexpr (!kEarlyStart) issue_first();
+    wait_vmcnt<(kStages - 1) * T::kPiecesMin>();  // own pieces of stage 0 landed
     __syncthreads();
-    if (wm == 0) {
-      for (int kt = 0; kt < KT; ++kt) {
+    // The loops take two stages per iteration (KT is even), the K block's first with the
+    // accumulators' factor and its second without, so neither MFMA phase branches on it (the
+    // factor of block 0 multiplies zeros).
+    if (w_u < 4) {
+      auto phase = [&](int kt, auto first_c) {
+        constexpr bool kFirst = decltype(first_c)::value;
         // the claim rides on the last stage, whose end waits for every copy anyway
-        if (claims && kt == last) ticket = walk.claim_ticket();
-        issue(min(kt + 2, last));
+        if (!kFirst && claims && kt == last) ticket = walk.claim_ticket();
+        if (kt >= 1) issue(min(kt + kStages - 1, last));
         read_stage(kt);
-        wait_vmcnt_lds<2 * kPieces>();  // own reads done (copies may be in flight)
+        if constexpr (kFirst) block_scales(kt);
+        wait_lds();  // own reads done (copies may be in flight)
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage();
+        mma_stage(kFirst);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<kPieces>();  // own pieces of stage kt+1 landed
+        wait_vmcnt<(kStages - 2) * T::kPiecesMin>();  // own pieces of stage kt + 1
         __syncthreads();
+      };
+      for (int kt = 0; kt < KT; kt += 2) {
+        phase(kt, std::true_type{});
+        phase(kt + 1, std::false_type{});
       }
       __syncthreads();
     } else {
       __syncthreads();
-      for (int kt = 0; kt < KT; ++kt) {
-        issue(min(kt + 2, last));
+      auto phase = [&](int kt, auto first_c) {
+        constexpr bool kFirst = decltype(first_c)::value;
+        if (kt >= 1) issue(min(kt + kStages - 1, last));
         read_stage(kt);
-        wait_vmcnt_lds<kPieces>();  // own reads done, own pieces of stage kt+1 landed
+        if constexpr (kFirst) block_scales(kt);
+        wait_vmcnt_lds<(kStages - 2) * T::kPiecesMin>();  // own reads, own pieces of stage kt + 1
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
-        mma_stage();
+        mma_stage(kFirst);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
+      };
+      for (int kt = 0; kt < KT; kt += 2) {
+        phase(kt, std::true_type{});
+        phase(kt + 1, std::false_type{});
       }
     }
     // R_last * s_last
+    {
+      const float l00 = sx0 * sw0, l01 = sx0 * sw1, l10 = sx1 * sw0, l11 = sx1 * sw1;
 #pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const float sl = sx_prev[i2] * sw_prev[j];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) acc[i2][j][q] *= sl;
-      }
+        for (int q = 0; q < 16; ++q) {
+          acc[0][j][q] *= (j & 1) ? l01 : l00;
+          acc[1][j][q] *= (j & 1) ? l11 : l10;
+        }
+    }
     wait_vmcnt<0>();  // every copy of this tile landed
     if (claims) claimed[0] = walk.resolve(ticket);
     __syncthreads();  // and every wavefront is done reading the stages
@@ -407,58 +468,65 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
         int mt2, nt2;
         walk.at_dense(i_next, mt2, nt2);
         copy_tile(mt2, nt2, e_cur);
-        start_copies();
+        issue_first();
       }
     }
 
-    // accumulator q of tile (i, j): activation row 64 g + 32 i + lane % 32, output column
-    // 64 c + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4
+    // Accumulator q of tile (i2, j): activation row 64 wm + 32 i2 + lane % 32, output column
+    // 128 wn + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4.
     if constexpr (MODE != kDown) {
-      // SwiGLU (or SiTU) in registers: column tiles j = 0, 1 are the gate and up halves of one
-      // 64-row group of interleaved W13, i.e. the same 32 intermediate columns; the lane holds
-      // h columns 32 c + 8 q4 + 4 lk + (0..3) of its two rows. The tile's 128 h columns are
-      // one 1x128 group per row: the row's amax over its 4 column wavefronts goes through a
-      // 2 KiB LDS area; then each lane half assembles 16 contiguous codes with one exchange
-      // and stores them.
+      // Column tiles j = 2 jj and 2 jj + 1 are the gate and up halves of one 64-row group of
+      // interleaved W13: h columns n0 / 2 + 64 wn + 32 jj + [0, 32), 16 values of each row in
+      // this lane and 16 in lane ^ 32. The tile's 128 h columns are one 1x128 group per row:
+      // the row's amax over both column wavefronts goes through an LDS area past the ring. Each
+      // lane half then assembles 16 contiguous codes with one exchange and stores them into
+      // the down GEMM's A image (row tile mt, K stage column / 64); the group's scale goes
+      // to the scale table.
       const int inter = p.N / 2;
-      float* amax_l = reinterpret_cast<float*>(lds + kAmax);
+      float* amax_l = reinterpret_cast<float*>(lds + T::kAmax);
       auto quant_store = [&](auto fn) {
-        float h[2][16];
+        float h[2][2][16];
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2) {
           float m = 0.0f;
 #pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            h[i2][q] = fn(acc[i2][0][q], acc[i2][1][q]);
-            m = fmaxf(m, fabsf(h[i2][q]));
-          }
+          for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              h[i2][jj][q] = fn(acc[i2][2 * jj][q], acc[i2][2 * jj + 1][q]);
+              m = fmaxf(m, fabsf(h[i2][jj][q]));
+            }
           m = fmaxf(m, xor32(m, lk));
-          if (lk == 0) amax_l[(wm * 64 + i2 * 32 + lr) * 4 + wn] = m;
+          if (lk == 0) amax_l[wn * kBM + wm * 64 + i2 * 32 + lr] = m;
         }
         __syncthreads();
 #pragma unroll
         for (int i2 = 0; i2 < 2; ++i2) {
           const int row = wm * 64 + i2 * 32 + lr;
-          const v4f a4 = *reinterpret_cast<const v4f*>(amax_l + row * 4);
-          const float amax = fmaxf(fmaxf(a4[0], a4[1]), fmaxf(a4[2], a4[3]));
+          const float amax = fmaxf(amax_l[row], amax_l[kBM + row]);
           const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
-          uint32_t d[4];
 #pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            d[q4] = pk4_e4m3(h[i2][4 * q4] / sc, h[i2][4 * q4 + 1] / sc, h[i2][4 * q4 + 2] / sc,
-                             h[i2][4 * q4 + 3] / sc);
-          // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
-          // 16-31 (the partner's d2, d3 and its own)
-          const uint32_t p0 = swap_halves(d[2], d[0], lk);
-          const uint32_t p1 = swap_halves(d[3], d[1], lk);
-          v4i chunk;
-          chunk[0] = static_cast<int>(lk ? p0 : d[0]);
-          chunk[1] = static_cast<int>(lk ? d[2] : p0);
-          chunk[2] = static_cast<int>(lk ? p1 : d[1]);
-          chunk[3] = static_cast<int>(lk ? d[3] : p1);
-          *reinterpret_cast<v4i*>(p.hq + int64_t(m0 + row) * inter + n0 / 2 + wn * 32 + lk * 16) =
-              chunk;
-          if (wn == 0 && lk == 0) p.hs[int64_t(m0 + row) * (inter / kBK) + n0 / 256] = sc;
+          for (int jj = 0; jj < 2; ++jj) {
+            uint32_t d[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4)
+              d[q4] = pk4_e4m3(h[i2][jj][4 * q4] / sc, h[i2][jj][4 * q4 + 1] / sc,
+                               h[i2][jj][4 * q4 + 2] / sc, h[i2][jj][4 * q4 + 3] / sc);
+            // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
+            // 16-31 (the partner's d2, d3 and its own)
+            const uint32_t p0 = swap_halves(d[2], d[0], lk);
+            const uint32_t p1 = swap_halves(d[3], d[1], lk);
+            v4i chunk;
+            chunk[0] = static_cast<int>(lk ? p0 : d[0]);
+            chunk[1] = static_cast<int>(lk ? d[2] : p0);
+            chunk[2] = static_cast<int>(lk ? p1 : d[1]);
+            chunk[3] = static_cast<int>(lk ? d[3] : p1);
+            const int col0 = n0 / 2 + 64 * wn + 32 * jj;  // multiple of 32
+            uint8_t* img = p.hq + (int64_t(mt) * (inter / kF8K) + col0 / kF8K) * kImgF8B;
+            *reinterpret_cast<v4i*>(img + img_b_off(row, (col0 % kF8K) / 16 + lk)) = chunk;
+            if (jj == 0 && wn == 0 && lk == 0)
+              p.hs[(int64_t(mt) * (inter / 128) + col0 / 128) * kBM + row] = sc;
+          }
         }
       };
       if constexpr (MODE == kGateUpParam) {
@@ -471,24 +539,26 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
       } else {
         quant_store([](float g, float u) { return act_swiglu(g, u); });
       }
+      // the amax area is read before the next tile's epilogue writes it again: every
+      // wavefront passes the next K loop's barriers in between
     } else {
-      // Lane half lk holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile; trading halves
-      // with v_permlane32_swap (first operand of lanes 32-63 for the second of lanes 0-31)
-      // leaves lane half lk with whole 16-byte chunks 2 pr + lk, in column order, written to
-      // LDS with one 16-byte write each.
-      const int nvalid = min(kBM, row_end - m0);  // rows [0, nvalid) of this tile are real
-      auto y_chunk = [](int r, int c) { return (r * kYChunks + (c ^ (r & 15))) * 16; };
-#pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int row = wm * 64 + i2 * 32 + lr;
-          const v16f& a = acc[i2][j];
+      // bf16 y rows through LDS (chunk c of row r at physical chunk c ^ (r % 16)), so the
+      // stores write whole rows. Lane half lk holds columns 8 q4 + 4 lk .. + 3 of each
+      // 32-column tile; trading halves with v_permlane32_swap leaves lane half lk with whole
+      // 16-byte chunks 2 pr + lk, in column order. Rows [0, nvalid) of this tile are real;
+      // the stores are non-temporal (y is read once, by the finalize).
+      const int nvalid = min(kBM, row_end - m0);
+      auto y_chunk = [](int r, int c) { return (r * T::kYChunks + (c ^ (r & 15))) * 16; };
+      static_for<2>([&](auto ic) {
+        constexpr int i2 = decltype(ic)::value;
+        const int row = wm * 64 + i2 * 32 + lr;
+        static_for<4>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
           uint32_t h[4][2];
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            h[q4][0] = pk_bf16(a[q4 * 4], a[q4 * 4 + 1]);
-            h[q4][1] = pk_bf16(a[q4 * 4 + 2], a[q4 * 4 + 3]);
+            h[q4][0] = pk_bf16(acc[i2][j][4 * q4], acc[i2][j][4 * q4 + 1]);
+            h[q4][1] = pk_bf16(acc[i2][j][4 * q4 + 2], acc[i2][j][4 * q4 + 3]);
           }
 #pragma unroll
           for (int pr = 0; pr < 2; ++pr) {
@@ -496,14 +566,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
             const auto d1 = __builtin_amdgcn_permlane32_swap(h[2 * pr][1], h[2 * pr + 1][1], false, false);
             const v4i chunk = {static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
                                static_cast<int>(d1[1])};
-            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 64 + j * 32) / 8 + 2 * pr + lk)) = chunk;
+            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 128 + j * 32) / 8 + 2 * pr + lk)) = chunk;
           }
-        }
+        });
+      });
       __syncthreads();
 #pragma unroll 4
-      for (int q = 0; q < kBM * kYChunks / kThreads; ++q) {
-        const int idx = q * kThreads + t;
-        const int row = idx / kYChunks, c = idx % kYChunks;
+      for (int q = 0; q < kBM * T::kYChunks / T::kThreads; ++q) {
+        const int idx = q * T::kThreads + t;
+        const int row = idx / T::kYChunks, c = idx % T::kYChunks;
         if (row < nvalid)
           __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
                                       reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
@@ -514,27 +585,27 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
 }
 
 template <int MODE>
-static int launch(Fp8GemmArgs p, int max_row_tiles, hipStream_t stream) {
-  if (p.K % kBK || p.N % kBN || p.K / kBK > kMaxKT) return AFD_ERR_SHAPE;
+static int launch(const Fp8GemmArgs& p, int max_row_tiles, hipStream_t stream) {
+  if (p.K % 128 || p.N % Tile::kBN) return AFD_ERR_SHAPE;
   // resident workgroups per CU (registers and LDS decide); initialized once, thread-safely
   static const int per_cu = [] {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fp8_gemm_kernel<MODE>, kThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fp8_gemm_kernel<MODE>, Tile::kThreads, 0) !=
             hipSuccess ||
         b < 1)
       b = 1;
     return b;
   }();
-  const int max_tiles = max_row_tiles * (p.N / kBN);
+  const int max_tiles = max_row_tiles * (p.N / Tile::kBN);
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
-  hipLaunchKernelGGL(fp8_gemm_kernel<MODE>, dim3(grid), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL(fp8_gemm_kernel<MODE>, dim3(grid), dim3(Tile::kThreads), 0, stream, p);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }
 
 static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws_layout& L) {
-  Fp8GemmArgs p;
+  Fp8GemmArgs p = {};
   p.topk = cfg.topk;
   p.topk_magic = div_magic(cfg.topk);
   p.act = act_params(cfg);
@@ -543,9 +614,6 @@ static Fp8GemmArgs common_args(const afd_moe_cfg& cfg, uint8_t* ws, const afd_ws
   p.num_tiles = reinterpret_cast<const int32_t*>(ws + L.num_tiles);
   p.padded_offsets = reinterpret_cast<const int32_t*>(ws + L.padded_offsets);
   p.counts = reinterpret_cast<const int32_t*>(ws + L.counts);
-  p.hq = nullptr;
-  p.hs = nullptr;
-  p.y = nullptr;
   return p;
 }
 
@@ -575,7 +643,6 @@ int launch_fp8_down(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_
   fp8::Fp8GemmArgs p = fp8::common_args(cfg, ws, L);
   p.a = ws + L.hq;
   p.as = reinterpret_cast<const float*>(ws + L.hs);
-  p.rows_desc = nullptr;
   p.b = static_cast<const uint8_t*>(wt.w2);
   p.bs = static_cast<const float*>(wt.s2);
   p.walk_ctr = cfg.tile_walk == AFD_WALK_DYNAMIC ? call_counters(ws, L) + kDownWalkWord : nullptr;

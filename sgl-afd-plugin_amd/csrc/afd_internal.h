@@ -11,6 +11,11 @@ namespace afd {
 constexpr int kMaxLocalExperts = 256;
 constexpr int kMaxTopk = 32;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
+constexpr int kFp8BlockM = 256;  // the same for FP8 block weights with fp8 activations (W8A8)
+// the row tile (segment padding) of a configuration's GEMMs
+inline int block_m_of(const afd_moe_cfg& cfg) {
+  return cfg.weight_fmt == AFD_W_FP8_BLOCK && cfg.act_fmt == AFD_A_FP8 ? kFp8BlockM : kBlockM;
+}
 constexpr int kMaxBatch = AFD_MAX_BATCH;  // jobs of one batched call
 
 

@@ -271,7 +271,8 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   const int64_t pairs = int64_t(n) * cfg->topk;
   const bool mx = cfg->weight_fmt == AFD_W_MXFP4;
   const bool a16 = bf16_act(*cfg);
-  const int64_t np_max = (pairs + E * (kBlockM - 1) + kBlockM - 1) / kBlockM * kBlockM;
+  const int64_t bm = block_m_of(*cfg);
+  const int64_t np_max = (pairs + E * (bm - 1) + bm - 1) / bm * bm;
   uint64_t o = 0;
   auto take = [&](uint64_t bytes) {
     uint64_t at = o;
@@ -279,11 +280,11 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
     return at;
   };
   afd_ws_layout L;
-  const uint64_t max_tiles = uint64_t(np_max / kBlockM);
+  const uint64_t max_tiles = uint64_t(np_max / bm);
   // xq / xs: the per-token e4m3 rows and their scales (MXFP4: UE8M0 per 32, in stage order;
   // FP8 block: fp32 per 1x128). MXFP4: hq holds the down GEMM's A images (the h rows in
-  // expert order, scales inside, hs empty); FP8 block: hq / hs the padded-row intermediate
-  // and its scales. bf16 activations: xq holds a batched call's bf16 rows (a single job's
+  // expert order, scales inside, hs empty); FP8 block: hq the down GEMM's FP8 A images (256
+  // rows x 64 K) and hs their fp32 1x128 scales [row tiles][I/128][256]. bf16 activations: xq holds a batched call's bf16 rows (a single job's
   // are read in place), hq the down GEMM's bf16 A images (MXFP4: 32 KiB per 128 K, FP8 block:
   // 16 KiB per 64 K; the same bytes), xs and hs are empty.
   L.xq = take(a16 ? uint64_t(n) * H * 2 : uint64_t(n) * H);
@@ -293,7 +294,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.padded_offsets = take((E + 1) * 4);
   L.sorted_pairs = take(uint64_t(np_max) * 4);
   L.pair_pos = take(uint64_t(pairs) * 4);
-  L.tile_expert = take(uint64_t(np_max / kBlockM) * 4);
+  L.tile_expert = take(max_tiles * 4);
   L.num_tiles = take(4);
   L.hist = take(uint64_t(128) * E * 4);
   L.hq = take(a16  ? max_tiles * (I / kImgK) * kImgA16
@@ -303,8 +304,8 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.y = take(uint64_t(np_max) * H * 2);
   L.total = o;
   L.np_max = np_max;
-  L.block_m = kBlockM;
-  L.max_tiles = static_cast<int32_t>(np_max / kBlockM);
+  L.block_m = static_cast<int32_t>(bm);
+  L.max_tiles = static_cast<int32_t>(max_tiles);
   *out = L;
   return AFD_OK;
 }

@@ -92,8 +92,8 @@ __device__ __forceinline__ int64_t gate_up_dest_row(int64_t lr, int64_t rows, in
 
 // ---------------------------------------------------------------- FP8 128x128 weight packer
 // One workgroup per logical 128x128 block: amax over the block, then each lane quantizes 64
-// values. Scales stay in logical block order; with gate_up the codes land on the physical
-// rows of the 32-row gate/up interleave.
+// values, one row of an FP8 image (fp8_image_offset). Scales stay in logical block order;
+// with gate_up the codes land on the physical rows of the 32-row gate/up interleave.
 __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
     const float* __restrict__ w, int rows, int cols, int gate_up, uint8_t* __restrict__ q,
     float* __restrict__ s) {
@@ -126,7 +126,9 @@ __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
-  uint8_t* dst = q + (mat * rows + prow) * cols + int64_t(cb) * kFp8Block + bc;
+  // the lane's 64 columns are one image row: K stage 2 cb + t % 2 of physical row prow
+  uint8_t* img = q + fp8_image_offset(mat, prow, int64_t(cb) * kFp8Block + bc, rows, cols);
+  const int rr = static_cast<int>(prow % kImgBRows);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     v4i out;
@@ -138,7 +140,7 @@ __global__ __launch_bounds__(kQuantThreads) void pack_fp8_block_kernel(
         packed |= f32_to_e4m3(clamp_e4m3(v[i * 16 + j * 4 + b] / sc)) << (8 * b);
       out[j] = static_cast<int>(packed);
     }
-    reinterpret_cast<v4i*>(dst)[i] = out;
+    *reinterpret_cast<v4i*>(img + img_b_off(rr, i)) = out;
   }
   if (t == 0) s[(mat * rbs + rb) * cbs + cb] = sc;
 }
@@ -170,7 +172,9 @@ __global__ __launch_bounds__(kQuantThreads) void repack_mxfp4_kernel(
   }
 }
 
-// Checkpoint FP8 block experts: e4m3 rows moved into the kernel's row order, 16 bytes a lane.
+// Checkpoint FP8 block experts: e4m3 rows [mats][rows][cols] moved into the FP8 images, one
+// 16-byte chunk a lane (chunk c of physical row r: logical row r's chunk, through the gate/up
+// interleave with gate_up).
 __global__ __launch_bounds__(kQuantThreads) void repack_fp8_rows_kernel(
     const uint8_t* __restrict__ q, int64_t chunks, int rows, int cols, int gate_up,
     uint8_t* __restrict__ out) {
@@ -182,7 +186,8 @@ __global__ __launch_bounds__(kQuantThreads) void repack_fp8_rows_kernel(
     int64_t mat = prow / rows;
     int r = static_cast<int>(prow % rows);
     int64_t src = mat * rows + (gate_up ? gate_up_source_row(r, rows, 32) : r);
-    *reinterpret_cast<v4i*>(out + prow * cols + j * 16) =
+    uint8_t* img = out + fp8_image_offset(mat, r, int64_t(j) * 16, rows, cols);
+    *reinterpret_cast<v4i*>(img + img_b_off(r % kImgBRows, j % 4)) =
         *reinterpret_cast<const v4i*>(q + src * cols + j * 16);
   }
 }
@@ -245,8 +250,7 @@ extern "C" int afd_pack_mxfp4(const float* w, int64_t mats, int32_t rows, int32_
 extern "C" int afd_pack_fp8_block(const float* w, int64_t mats, int32_t rows, int32_t cols,
                                   int32_t gate_up, uint8_t* q, float* s, afd_stream_t stream) {
   if (!w || !q || !s || mats < 0) return AFD_ERR_ARG;
-  if (rows <= 0 || cols <= 0 || rows % kFp8Block || cols % kFp8Block) return AFD_ERR_SHAPE;
-  if (gate_up && rows % 256) return AFD_ERR_SHAPE;
+  if (rows <= 0 || cols <= 0 || rows % kImgBRows || cols % kFp8Block) return AFD_ERR_SHAPE;
   if (mats == 0) return AFD_OK;
   int64_t blocks = mats * (rows / kFp8Block) * (cols / kFp8Block);
   if (blocks > 0x7fffffff) return AFD_ERR_SHAPE;
@@ -278,8 +282,7 @@ extern "C" int afd_repack_fp8_block(const uint8_t* q, int64_t mats, int32_t rows
                                     int32_t gate_up, uint8_t* out, afd_stream_t stream) {
   if (!q || !out || mats < 0) return AFD_ERR_ARG;
   if (!aligned16(q) || !aligned16(out)) return AFD_ERR_ARG;
-  if (rows <= 0 || cols <= 0 || rows % kFp8Block || cols % kFp8Block) return AFD_ERR_SHAPE;
-  if (gate_up && rows % 256) return AFD_ERR_SHAPE;
+  if (rows <= 0 || cols <= 0 || rows % kImgBRows || cols % kFp8Block) return AFD_ERR_SHAPE;
   if (mats == 0) return AFD_OK;
   int64_t chunks = mats * rows * (cols / 16);
   hipLaunchKernelGGL(repack_fp8_rows_kernel, dim3(grid_for(chunks)), dim3(kQuantThreads), 0,

@@ -36,7 +36,7 @@ AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 AFD_WALK_STATIC, AFD_WALK_DYNAMIC = 0, 1
 
 # afd_abi_version() of the library these structures match
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # Every entry point include/afd.h declares; tests check the library exports all of them.
 EXPORTED = (

@@ -1,5 +1,6 @@
-"""numpy statement of the MX GEMM operand tile images (the layout include/afd.h documents),
-used by the tests to compare the GPU's packed bytes with the oracle's codes and scales."""
+"""numpy statement of the GEMM operand tile images (the layouts include/afd.h documents):
+MXFP4 B images, MXFP8 A images and FP8 images, used by the tests to compare the GPU's packed
+bytes with the oracle's codes and scales."""
 
 import numpy as np
 
@@ -26,6 +27,24 @@ def b_images(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     img[..., :IMG_DATA] = body.reshape(e, nt, kt, IMG_DATA)
     img[..., IMG_DATA:] = sc.reshape(e, nt, kt, 256 * 4)
     return img
+
+
+def _swizzle_rows(data: np.ndarray) -> np.ndarray:
+    """[..., 256, 4, 16] logical chunks -> the same rows with chunk c at physical chunk
+    c ^ ((row >> 1 ^ row >> 2) & 3) (the B image's data layout)."""
+    body = np.zeros_like(data)
+    rows = np.arange(data.shape[-3])
+    for c in range(4):
+        phys = c ^ (((rows >> 1) ^ (rows >> 2)) & 3)
+        body[..., rows, phys, :] = data[..., rows, c, :]
+    return body
+
+
+def fp8_images(codes: np.ndarray) -> np.ndarray:
+    """e4m3 codes [E, N, K] (physical row order) -> FP8 images [E, N/256, K/64, 16384]."""
+    e, n, k = codes.shape
+    data = codes.reshape(e, n // 256, 256, k // 64, 4, 16).transpose(0, 1, 3, 2, 4, 5)
+    return _swizzle_rows(data).reshape(e, n // 256, k // 64, 256 * 64)
 
 
 def a_rows(images: np.ndarray, k: int):

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_functions():
         assert hasattr(L, name), name
-    assert L.afd_abi_version() == _lib.ABI_VERSION == 4
+    assert L.afd_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_status_strings():
@@ -55,6 +55,23 @@ def test_workspace_layout_dsv4_rank():
     offs = [L[k] for k in ("xq", "xs", "counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos",
                            "tile_expert", "num_tiles", "hist", "hq", "hs", "y")]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert L["total"] >= L["y"] + L["np_max"] * 4096 * 2
+
+
+def test_workspace_layout_fp8_block():
+    """W8A8 (FP8 block weights, fp8 activations): expert segments pad to 256 rows; hq holds one
+    16 KiB FP8 image per 256-row tile and 64-wide K stage of h, hs their fp32 1x128 scales."""
+    cfg = _lib.AfdMoeCfg(4096, 1536, 8, 0, 64, _lib.AFD_W_FP8_BLOCK)
+    L = workspace_layout(cfg, 16384)
+    assert L["block_m"] == 256
+    assert L["np_max"] == (16384 * 8 + 64 * 255 + 255) // 256 * 256
+    tiles = L["np_max"] // 256
+    assert L["max_tiles"] == tiles
+    assert L["xq"] == 0 and L["xs"] == 16384 * 4096
+    assert L["counts"] - L["xs"] == 16384 * (4096 // 128) * 4
+    assert L["hs"] - L["hq"] == tiles * (1536 // 64) * 256 * 64
+    assert L["y"] - L["hs"] == tiles * (1536 // 128) * 256 * 4
+    assert L["tile_expert"] + tiles * 4 <= L["num_tiles"]
     assert L["total"] >= L["y"] + L["np_max"] * 4096 * 2
 
 

@@ -63,7 +63,8 @@ def test_repack_fp8_block_bitexact(gate_up):
     out = torch.empty_like(qd)
     _lib.call("afd_repack_fp8_block", qd.data_ptr(), mats, rows, cols, gate_up, out.data_ptr(), _stream())
     torch.cuda.synchronize()
-    assert np.array_equal(u8(out), codes[:, _gate_up_rows(rows)] if gate_up else codes)
+    rows_in_order = codes[:, _gate_up_rows(rows)] if gate_up else codes
+    assert np.array_equal(u8(out).reshape(-1), L.fp8_images(rows_in_order).reshape(-1))
 
 
 def test_repack_rejects_bad_shapes_and_alignment():

@@ -18,9 +18,11 @@ def _i32(ws, off, count):
     return ws[off : off + 4 * count].view(torch.int32).cpu().numpy()
 
 
-def run_route(ids: np.ndarray, e_lo: int, num_local: int):
+def run_route(ids: np.ndarray, e_lo: int, num_local: int, fmt=_lib.AFD_W_MXFP4):
+    """fmt: the weight format, which sets the segment padding (MXFP4: 128 rows, FP8 blocks with
+    fp8 activations: 256)."""
     n, k = ids.shape
-    cfg = _lib.AfdMoeCfg(256, 128, k, e_lo, num_local, _lib.AFD_W_MXFP4)
+    cfg = _lib.AfdMoeCfg(256, 128, k, e_lo, num_local, fmt)
     L = workspace_layout(cfg, n)
     ws = torch.full((L["total"],), 0xAB, dtype=torch.uint8, device=dev())
     ids_d = torch.from_numpy(np.ascontiguousarray(ids, dtype=np.int32)).to(dev())
@@ -42,8 +44,8 @@ def run_route(ids: np.ndarray, e_lo: int, num_local: int):
     }
 
 
-def check(ids, e_lo, num_local):
-    got = run_route(ids, e_lo, num_local)
+def check(ids, e_lo, num_local, fmt=_lib.AFD_W_MXFP4):
+    got = run_route(ids, e_lo, num_local, fmt)
     ref = R.route(ids, e_lo, num_local, got["block_m"])
     for key in ("counts", "offsets", "padded_offsets", "sorted_pairs", "pair_pos"):
         assert np.array_equal(got[key], ref[key]), key
@@ -95,3 +97,16 @@ def test_route_edge_cases():
     # n = 0
     got = run_route(np.zeros((0, 8), dtype=np.int32), 0, 64)
     assert got["num_tiles"] == 0 and not got["counts"].any()
+
+
+@pytest.mark.parametrize("n,k,num_experts,e_lo,num_local,seed", [CASES[i] for i in (1, 3, 5, 7, 8, 9, 13, 14)])
+def test_route_256_row_segments(n, k, num_experts, e_lo, num_local, seed):
+    """The FP8-block layout (W8A8) pads every expert segment to 256 rows: the same permutation,
+    its own padded offsets and tile table, bit-exact against the oracle with block_m 256."""
+    say(f"route256 n={n} k={k} experts={num_experts} local=[{e_lo},{e_lo + num_local}) seed={seed}")
+    g = torch.Generator().manual_seed(seed)
+    scores = torch.rand(n, num_experts, generator=g)
+    ids = torch.topk(scores, k, dim=1).indices.to(torch.int32).numpy()
+    got = run_route(ids, e_lo, num_local, _lib.AFD_W_FP8_BLOCK)
+    assert got["block_m"] == 256
+    check(ids, e_lo, num_local, _lib.AFD_W_FP8_BLOCK)
