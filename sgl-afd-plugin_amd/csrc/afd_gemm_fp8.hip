@@ -29,7 +29,7 @@
 // h), the tile's FP8 weight image (16 KiB, contiguous in HBM: afd_pack_fp8_block's layout)
 // and the 256 activation rows' scales of the stage's K block; everything moves HBM -> LDS
 // with gfx950's direct global_load_lds (1 KiB pieces, the scales as 4-byte words), into a
-// ring of 3 stages. Both operands keep the e2m1 B image's swizzled 64-byte rows (img_b_off)
+// ring of 3 stages (down: 4). Both operands keep the e2m1 B image's swizzled 64-byte rows (img_b_off)
 // in LDS: the 16-byte chunks an MFMA operand read takes from 16 consecutive rows fall on 16
 // distinct 16-byte bank groups. The two wavefronts of a SIMD ping-pong between reading a
 // stage's fragments and running its 8 MFMAs (as the W4A8 and W4A16 kernels), and the
@@ -84,13 +84,16 @@ struct Tile {
   static constexpr int kBOff = kImgF8B;
   static constexpr int kAScale = 2 * kImgF8B;
   static constexpr int kStage = kAScale + kBM * 4;
-  static constexpr int kStages = 3;
-  static constexpr int kRing = kStages * kStage;
+  // ring slots: gate_up 3 (its scale table takes the rest of the LDS), down 4 (its epilogue
+  // tile covers the ring; one more stage in flight measured 3% faster)
+  template <int MODE>
+  static constexpr int stages() { return MODE == 1 ? 4 : 3; }
+  static constexpr int kRing = 3 * kStage;
   // down: its epilogue's bf16 tile over the ring. gate_up: after the ring, the epilogue's
   // per-row amax of each column wavefront, [2][256 rows], then the tile's activation-row
   // scales for every K block (the scale table, filled once per tile; see the kernel)
   static constexpr int kYBytes = kBM * kBN * 2;
-  static constexpr int kDownLds = kRing > kYBytes ? kRing : kYBytes;
+  static constexpr int kDownLds = 4 * kStage > kYBytes ? 4 * kStage : kYBytes;
   static constexpr int kAmax = kRing;
   static constexpr int kTab = kAmax + 2 * kBM * 4;
   static constexpr int kTabMaxQ = 7;  // table pieces per wavefront: K up to 7168
@@ -107,7 +110,7 @@ struct Tile {
   static_assert(kLds + 256 <= 160 * 1024, "LDS of one CU");
   template <int MODE>
   static constexpr int lds_bytes() { return MODE == 1 ? kDownLds : kGateUpLds; }
-  static_assert(kStages * (kPiecesMin + 1) < 64, "vmcnt is a 6-bit counter");
+  static_assert(4 * (kPiecesMin + 1) < 64, "vmcnt is a 6-bit counter");
 };
 
 // A uniform read of data the kernel never writes (the weight block scales), through the
@@ -119,7 +122,7 @@ __device__ __forceinline__ float load_uniform(const float* p) {
 template <int MODE>
 __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   using T = Tile;
-  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
+  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::stages<MODE>(), kStage = T::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t lds[T::lds_bytes<MODE>()];
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
