@@ -97,7 +97,7 @@ struct Tile {
   static constexpr int kAmax = kRing;
   static constexpr int kTab = kAmax + 2 * kBM * 4;
   static constexpr int kTabMaxQ = 7;  // table pieces per wavefront: K up to 7168
-  static constexpr int kGateUpLds = kTab + kWaves * kTabMaxQ * 1024;
+  static constexpr int kGateUpLds = kTab + kWaves * kTabMaxQ * 1024;  // 256 rows x 14 chunks
   static constexpr int kLds = kDownLds > kGateUpLds ? kDownLds : kGateUpLds;
   // per wavefront and stage: 2 pieces of the A block and 2 of the weight image; wavefronts
   // 0-3 also copy the scale words of rows [64 w, 64 w + 64)
@@ -147,16 +147,13 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
   // gate_up's activation-row scales: with K a multiple of 512 up to 7168, every row's K-block
   // scales (K / 128 words, contiguous in xs) are copied once per tile into the scale table;
   // otherwise wavefronts 0-3 copy the 256 rows' words of each stage's K block into its slot.
-  // The table: wavefront w's pieces q hold rows [32 w, 32 w + 32), lane l = 2 (row % 32) + h
-  // taking 16-byte chunk 2 q + h of row 32 w + l / 2 (the last piece of an odd chunk count
-  // repeats the last chunk).
-  const int tab_chunks = kb_n / 4, tab_q = (tab_chunks + 1) / 2;
-  const bool table = MODE != kDown && kb_n % 4 == 0 && tab_q <= T::kTabMaxQ;
+  // The table holds 16-byte chunk c (the scales of K blocks 4 c .. 4 c + 3) of row r at
+  // (256 c + r) * 16, so the 32 rows an operand read takes fill consecutive 16-byte units (no
+  // bank conflicts); wavefront w copies chunks c = 2 q + w / 4 of rows 64 (w % 4) + lane.
+  const int tab_chunks = kb_n / 4;
+  const bool table = MODE != kDown && kb_n % 4 == 0 && (tab_chunks + 1) / 2 <= T::kTabMaxQ;
   const bool copies_scales = w_u < 4 && !table;
-  auto tab_off = [&](int r, int kb) {  // byte offset of row r's scale of K block kb
-    const int c = kb >> 2;
-    return T::kTab + (((r >> 5) * tab_q + (c >> 1)) * 64 + (r & 31) * 2 + (c & 1)) * 16 + (kb & 3) * 4;
-  };
+  auto tab_off = [&](int r, int c) { return T::kTab + (c * kBM + r) * 16; };
 
   // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A block from the
   // token rows: lane l copies, for its piece q (16 rows), physical chunk l % 4 of row
@@ -174,7 +171,7 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
       for (int q = 0; q < T::kAQ; ++q)
         sp_next[q] = p.sorted_pairs[m * kBM + 16 * (w_u * T::kAQ + q) + (lane >> 2)];
       sp_next[T::kAQ] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
-      sp_next[T::kAQ + 1] = p.sorted_pairs[m * kBM + 32 * w_u + (lane >> 1)];
+      sp_next[T::kAQ + 1] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
     }
   };
   int e_cur = 0, live_cur = 0;
@@ -256,11 +253,9 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
   // covers them; the previous tile's K loop, the table's only reader, has ended by then)
   auto issue_first = [&]() {
     if (MODE != kDown && table) {
-      for (int q = 0; q < tab_q; ++q) {
-        const int c = min(2 * q + (lane & 1), tab_chunks - 1);
-        lds_dma16(lds_base + static_cast<uint32_t>(T::kTab + (w_u * tab_q + q) * 1024), s_tile,
+      for (int c = w_u >> 2; c < tab_chunks; c += 2)
+        lds_dma16(lds_base + static_cast<uint32_t>(tab_off(64 * (w_u & 3), c)), s_tile,
                   t_voff + static_cast<uint32_t>(c * 16));
-      }
     }
     static_for<kStages>([&](auto sc) { issue(min(static_cast<int>(decltype(sc)::value), last)); });
   };
@@ -344,12 +339,21 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     // tile's 16 right before its MFMA: the tile's previous MFMA finished a phase ago, and the
     // next tile's multiplies issue beside this tile's MFMA.
     float r00 = 1.0f, r01 = 1.0f, r10 = 1.0f, r11 = 1.0f;
+    v4f xc0 = {}, xc1 = {};  // scale-table chunks of the lane's two rows (see block_scales)
     int kb_next = 0;  // the K block whose weight scales swn0, swn1 hold
     auto block_scales = [&](int kt) {
       float x0, x1;
       if (MODE != kDown && table) {
-        x0 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + lr, kt >> 1));
-        x1 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + 32 + lr, kt >> 1));
+        // one 16-byte read per row brings the scales of 4 K blocks; they shift down a lane of
+        // the vector per block
+        if (((kt >> 1) & 3) == 0) {
+          xc0 = *reinterpret_cast<const v4f*>(lds + tab_off(wm * 64 + lr, kt >> 3));
+          xc1 = *reinterpret_cast<const v4f*>(lds + tab_off(wm * 64 + 32 + lr, kt >> 3));
+        }
+        x0 = xc0[0];
+        x1 = xc1[0];
+        xc0 = v4f{xc0[1], xc0[2], xc0[3], xc0[3]};
+        xc1 = v4f{xc1[1], xc1[2], xc1[3], xc1[3]};
       } else {
         const float* sxs = reinterpret_cast<const float*>(lds + (kt % kStages) * kStage + T::kAScale);
         x0 = sxs[wm * 64 + lr];
