@@ -84,33 +84,39 @@ struct Tile {
   static constexpr int kBOff = kImgF8B;
   static constexpr int kAScale = 2 * kImgF8B;
   static constexpr int kStage = kAScale + kBM * 4;
-  // ring slots: gate_up 3 (its scale table takes the rest of the LDS), down 4 (its epilogue
-  // tile covers the ring; one more stage in flight measured 3% faster)
-  template <int MODE>
-  static constexpr int stages() { return MODE == 1 ? 4 : 3; }
-  static constexpr int kRing = 3 * kStage;
-  // down: its epilogue's bf16 tile over the ring. gate_up: after the ring, the epilogue's
-  // per-row amax of each column wavefront, [2][256 rows], then the tile's activation-row
-  // scales for every K block (the scale table, filled once per tile; see the kernel)
+  // down: a ring of 4 such stages (one more stage in flight than 3 measured 3% faster), its
+  // epilogue's bf16 tile over the ring
+  static constexpr int kStages = 4;
   static constexpr int kYBytes = kBM * kBN * 2;
-  static constexpr int kDownLds = 4 * kStage > kYBytes ? 4 * kStage : kYBytes;
-  static constexpr int kAmax = kRing;
-  static constexpr int kTab = kAmax + 2 * kBM * 4;
-  static constexpr int kTabMaxQ = 7;  // table pieces per wavefront: K up to 7168
-  static constexpr int kGateUpLds = kTab + kWaves * kTabMaxQ * 1024;  // 256 rows x 14 chunks
-  static constexpr int kLds = kDownLds > kGateUpLds ? kDownLds : kGateUpLds;
+  static constexpr int kDownLds = kStages * kStage > kYBytes ? kStages * kStage : kYBytes;
   // per wavefront and stage: 2 pieces of the A block and 2 of the weight image; wavefronts
   // 0-3 also copy the scale words of rows [64 w, 64 w + 64)
   static constexpr int kAQ = (kImgF8B / 1024) / kWaves;
   static constexpr int kQP = (kImgF8B / 1024) / kWaves;
   static constexpr int kPiecesMin = kAQ + kQP;  // pieces of a wavefront without scales
   static constexpr int kYChunks = kBN / 8;
-  static_assert(kBM == 256 && kAQ * kWaves * 1024 == kImgF8B, "pieces cover a stage");
-  static_assert((kStage & 255) == 0, "slot offsets leave the fragment addresses' low 8 bits alone");
-  static_assert(kLds + 256 <= 160 * 1024, "LDS of one CU");
+  // gate_up gathers its A rows from the token rows, whose 64-byte halves a 64-K stage would
+  // take as two requests of the same 128-byte line; it copies them per 128-K superstage
+  // instead: an A ring of 2 superstages (256 rows x 128 B, in the MXFP8 A image's layout,
+  // img_a_off), a ring of 3 weight images, the per-stage scale slots of the fallback (see the
+  // kernel), the epilogue's per-row amax of each column wavefront [2][256 rows], and the
+  // scale table (K up to 4096)
+  static constexpr int kGASlot = kBM * 128;
+  static constexpr int kGB = 2 * kGASlot;
+  static constexpr int kGS = kGB + 3 * kImgF8B;
+  static constexpr int kGAmax = kGS + 3 * kBM * 4;
+  static constexpr int kGTab = kGAmax + 2 * kBM * 4;
+  static constexpr int kTabMaxChunks = 8;  // 16-byte chunks (4 K blocks) per row: K <= 4096
+  static constexpr int kGateUpLds = kGTab + kTabMaxChunks * kBM * 16;
+  static constexpr int kGAQ = (kGASlot / 1024) / kWaves;  // A pieces of a wavefront and superstage
+  static_assert(kBM == 256 && kAQ * kWaves * 1024 == kImgF8B && kGAQ * kWaves * 1024 == kGASlot,
+                "pieces cover a stage");
+  static_assert((kStage & 255) == 0 && (kGB & 255) == 0,
+                "slot offsets leave the fragment addresses' low 8 bits alone");
+  static_assert(kDownLds + 256 <= 160 * 1024 && kGateUpLds + 256 <= 160 * 1024, "LDS of one CU");
   template <int MODE>
   static constexpr int lds_bytes() { return MODE == 1 ? kDownLds : kGateUpLds; }
-  static_assert(4 * (kPiecesMin + 1) < 64, "vmcnt is a 6-bit counter");
+  static_assert(4 * (kPiecesMin + 1) < 64 && kQP + 2 * (kGAQ + kQP) + 1 < 64, "vmcnt is a 6-bit counter");
 };
 
 // A uniform read of data the kernel never writes (the weight block scales), through the
@@ -122,7 +128,9 @@ __device__ __forceinline__ float load_uniform(const float* p) {
 template <int MODE>
 __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p) {
   using T = Tile;
-  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::stages<MODE>(), kStage = T::kStage;
+  constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
+  constexpr bool kGU = MODE != kDown;
+  constexpr int kNA = kGU ? T::kGAQ : T::kAQ;  // A pieces of a wavefront per (super)stage
   __shared__ __attribute__((aligned(16))) uint8_t lds[T::lds_bytes<MODE>()];
   const int t = threadIdx.x, lane = t & 63;
   const int w_u = __builtin_amdgcn_readfirstlane(t >> 6);  // wavefront index, scalar
@@ -139,28 +147,35 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     a_rows = p.rows_desc->xq;
     a_scales = static_cast<const float*>(p.rows_desc->xs);
   }
-  // fragment bases of the lane in a stage: A row 64 wm + lr and weight row 128 wn + lr, each
-  // at logical chunk lk (the operand's first 16 bytes; its second 16 are logical chunk lk + 2,
-  // i.e. the address with bit 5 flipped). Rows + 32 i keep the swizzle.
-  const int a_lane = img_b_off(wm * 64 + lr, lk);
-  const int b_lane = T::kBOff + img_b_off(wn * 128 + lr, lk);
-  // gate_up's activation-row scales: with K a multiple of 512 up to 7168, every row's K-block
+  // fragment bases of the lane: weight row 128 wn + lr at logical chunk lk (the operand's
+  // first 16 bytes; its second 16 are logical chunk lk + 2, i.e. the address with bit 5
+  // flipped), A row 64 wm + lr the same way (down) or (gate_up, 128-byte rows) the row's
+  // swizzled base, XORed with the chunk per read. Rows + 32 i keep the 64-byte rows' swizzle
+  // and flip chunk bit 2 of the 128-byte rows'.
+  const int a_lane = kGU ? 0 : img_b_off(wm * 64 + lr, lk);
+  int a_ch[4] = {};  // gate_up: chunks lk, lk + 2, lk + 4, lk + 6 of the lane's A row
+  if constexpr (kGU) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a_ch[j] = img_a_off(wm * 64 + lr, lk + 2 * j);
+  }
+  const int b_lane = (kGU ? T::kGB : T::kBOff) + img_b_off(wn * 128 + lr, lk);
+  // gate_up's activation-row scales: with K a multiple of 512 up to 4096, every row's K-block
   // scales (K / 128 words, contiguous in xs) are copied once per tile into the scale table;
   // otherwise wavefronts 0-3 copy the 256 rows' words of each stage's K block into its slot.
   // The table holds 16-byte chunk c (the scales of K blocks 4 c .. 4 c + 3) of row r at
-  // (256 c + r) * 16, so the 32 rows an operand read takes fill consecutive 16-byte units (no
-  // bank conflicts); wavefront w copies chunks c = 2 q + w / 4 of rows 64 (w % 4) + lane.
+  // (256 c + r) * 16 (a read of one block's scale of 32 rows: two-way bank conflicts, once
+  // per 128 K); wavefront w copies chunks c = 2 q + w / 4 of rows 64 (w % 4) + lane.
   const int tab_chunks = kb_n / 4;
-  const bool table = MODE != kDown && kb_n % 4 == 0 && (tab_chunks + 1) / 2 <= T::kTabMaxQ;
+  const bool table = kGU && kb_n % 4 == 0 && tab_chunks <= T::kTabMaxChunks;
   const bool copies_scales = w_u < 4 && !table;
-  auto tab_off = [&](int r, int c) { return T::kTab + (c * kBM + r) * 16; };
+  auto tab_off = [&](int r, int c) { return T::kGTab + (c * kBM + r) * 16; };
 
-  // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A block from the
-  // token rows: lane l copies, for its piece q (16 rows), physical chunk l % 4 of row
-  // 16 (w kAQ + q) + l / 4 of the block, i.e. logical chunk (l % 4) ^ swizzle(row), from the
-  // row's token; the scale-copying wavefront w < 4 copies the word of row 64 w + l. Padding
-  // rows (-1) read token 0; their results are never stored.
-  int sp_next[T::kAQ + 2], e_next = 0, own_next = -1;
+  // Tile metadata one tile ahead (as the W4A8 kernel). gate_up gathers its A superstages from
+  // the token rows: lane l copies, for its piece q (8 rows of 128 B), physical chunk l % 8 of
+  // row 8 (w kGAQ + q) + l / 8, i.e. logical chunk (l % 8) ^ swizzle(row), from the row's
+  // token; the scale words (fallback) and the table chunks of wavefront w are those of row
+  // 64 (w % 4) + l. Padding rows (-1) read token 0; their results are never stored.
+  int sp_next[kNA + 1], e_next = 0, own_next = -1;
   auto load_next = [&](int ii) {
     int m, nn;
     walk.at_dense(ii, m, nn);
@@ -168,14 +183,13 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     own_next = p.sorted_pairs[m * kBM + 64 * wm + lane];
     if constexpr (MODE != kDown) {
 #pragma unroll
-      for (int q = 0; q < T::kAQ; ++q)
-        sp_next[q] = p.sorted_pairs[m * kBM + 16 * (w_u * T::kAQ + q) + (lane >> 2)];
-      sp_next[T::kAQ] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
-      sp_next[T::kAQ + 1] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
+      for (int q = 0; q < kNA; ++q)
+        sp_next[q] = p.sorted_pairs[m * kBM + 8 * (w_u * kNA + q) + (lane >> 3)];
+      sp_next[kNA] = p.sorted_pairs[m * kBM + 64 * (w_u & 3) + lane];
     }
   };
   int e_cur = 0, live_cur = 0;
-  uint32_t a_voff[T::kAQ] = {}, s_voff = 0, t_voff = 0;
+  uint32_t a_voff[kNA] = {}, s_voff = 0;
   auto decode_next = [&]() {
     e_cur = __builtin_amdgcn_readfirstlane(e_next);
     live_cur = __popcll(__ballot(own_next >= 0));  // real rows of this group, a scalar
@@ -184,13 +198,12 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
         return sp >= 0 ? div_by_magic(static_cast<uint32_t>(sp), p.topk_magic) : 0u;
       };
 #pragma unroll
-      for (int q = 0; q < T::kAQ; ++q) {
-        const int r = 16 * (w_u * T::kAQ + q) + (lane >> 2);
-        const int c = (img_b_off(r, lane & 3) - r * kF8K) >> 4;  // the swizzle is an involution
+      for (int q = 0; q < kNA; ++q) {
+        const int r = 8 * (w_u * kNA + q) + (lane >> 3);
+        const int c = (img_a_off(r, lane & 7) - r * 128) >> 4;  // the swizzle is an involution
         a_voff[q] = token(sp_next[q]) * static_cast<uint32_t>(p.K) + c * 16;
       }
-      s_voff = token(sp_next[T::kAQ]) * static_cast<uint32_t>(kb_n * 4);
-      t_voff = token(sp_next[T::kAQ + 1]) * static_cast<uint32_t>(kb_n * 4);
+      s_voff = token(sp_next[kNA]) * static_cast<uint32_t>(kb_n * 4);
     }
   };
   // gate_up starts the next tile's copies right after its own K loop: its epilogue works from
@@ -205,29 +218,42 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     s_tile = MODE != kDown ? a_scales : a_scales + int64_t(mt) * kb_n * kBM;
     b_tile = p.b + (e * (p.N / kImgBRows) + nt) * KT * int64_t(kImgF8B);
   };
-  // this wavefront's copies of stage kt into ring slot kt % kStages: its A pieces, its
-  // weight pieces, and (wavefronts 0-3) scale words
-  auto issue = [&](int kt) {
+  // down: this wavefront's copies of stage kt into ring slot kt % 4: its A pieces, its weight
+  // pieces, and (wavefronts 0-3) scale words
+  auto issue_down = [&](int kt) {
     const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
     static_for<T::kAQ>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       const int off = (w_u * T::kAQ + q) * 1024;
-      if constexpr (MODE != kDown)
-        lds_dma16(st + off, a_tile + int64_t(kt) * kF8K, a_voff[q]);
-      else
-        lds_dma16(st + off, a_tile + int64_t(kt) * kImgF8B + off, voff);
+      lds_dma16(st + off, a_tile + int64_t(kt) * kImgF8B + off, voff);
     });
     static_for<T::kQP>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       const int off = (w_u * T::kQP + q) * 1024;
       lds_dma16(st + T::kBOff + off, b_tile + int64_t(kt) * kImgF8B + off, voff);
     });
-    if (copies_scales) {
-      if constexpr (MODE != kDown)
-        lds_dma4(st + T::kAScale + w_u * 256, s_tile + (kt >> 1), s_voff);
-      else
-        lds_dma4(st + T::kAScale + w_u * 256, s_tile + (kt >> 1) * kBM + 64 * w_u, lane * 4u);
-    }
+    if (copies_scales)
+      lds_dma4(st + T::kAScale + w_u * 256, s_tile + (kt >> 1) * kBM + 64 * w_u, lane * 4u);
+  };
+  // gate_up: its A pieces of superstage sk (K [128 sk, + 128)) into A slot sk % 2; its weight
+  // pieces of stage kt into B slot kt % 3, with (fallback, wavefronts 0-3) the scale words
+  auto issue_a = [&](int sk) {
+    const uint32_t st = lds_base + static_cast<uint32_t>((sk & 1) * T::kGASlot);
+    static_for<kNA>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      lds_dma16(st + (w_u * kNA + q) * 1024, a_tile + int64_t(sk) * 128, a_voff[q]);
+    });
+  };
+  auto issue_b = [&](int kt) {
+    const int slot = kt % 3;
+    const uint32_t st = lds_base + static_cast<uint32_t>(T::kGB + slot * kImgF8B);
+    static_for<T::kQP>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      const int off = (w_u * T::kQP + q) * 1024;
+      lds_dma16(st + off, b_tile + int64_t(kt) * kImgF8B + off, voff);
+    });
+    if (copies_scales)
+      lds_dma4(lds_base + static_cast<uint32_t>(T::kGS + slot * kBM * 4 + w_u * 256), s_tile + (kt >> 1), s_voff);
   };
   const int last = KT - 1;
 
@@ -246,19 +272,50 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
   i = min(i, walk.tiles);
   i_next = min(i_next, walk.tiles);
   uint32_t ticket = 0;  // lives across the tile loop (no write to its register waits for it)
-  // A tile's K loop starts with every ring slot filled: stages 0 .. kStages - 1 (clamped to
-  // the last stage) are issued before it, during the previous tile's epilogue (gate_up) or at
-  // the start of the tile (down).
-  // (gate_up with the scale table: the tile's table pieces first, so the wait for stage 0
-  // covers them; the previous tile's K loop, the table's only reader, has ended by then)
+  const int last_sk = KT / 2 - 1;  // the last superstage (KT is even)
+  // A tile's K loop starts with every ring slot filled, issued during the previous tile's
+  // epilogue (gate_up) or at the start of the tile (down). down: stages 0-3. gate_up: the
+  // tile's table pieces (so the wait for stage 0 covers them; the previous tile's K loop, the
+  // table's only reader, has ended by then), then A superstage 0, weights of stages 0 and 1,
+  // then what the loop itself would have issued at stage 0: A superstage 1 and weights of
+  // stage 2 (all clamped to the last (super)stage: a clamped copy rewrites a slot with its
+  // own bytes, and keeps every wavefront's count of copies in flight the same at each wait).
   auto issue_first = [&]() {
-    if (MODE != kDown && table) {
-      for (int c = w_u >> 2; c < tab_chunks; c += 2)
-        lds_dma16(lds_base + static_cast<uint32_t>(tab_off(64 * (w_u & 3), c)), s_tile,
-                  t_voff + static_cast<uint32_t>(c * 16));
+    if constexpr (kGU) {
+      if (table) {
+        for (int c = w_u >> 2; c < tab_chunks; c += 2)
+          lds_dma16(lds_base + static_cast<uint32_t>(tab_off(64 * (w_u & 3), c)), s_tile,
+                    s_voff + static_cast<uint32_t>(c * 16));
+      }
+      issue_a(0);
+      issue_b(0);
+      issue_b(min(1, last));
+      issue_a(min(1, last_sk));
+      issue_b(min(2, last));
+    } else {
+      static_for<kStages>([&](auto sc) { issue_down(min(static_cast<int>(decltype(sc)::value), last)); });
     }
-    static_for<kStages>([&](auto sc) { issue(min(static_cast<int>(decltype(sc)::value), last)); });
   };
+  // the copies issued at stage kt >= 1 of the K loop: gate_up A superstage kt / 2 + 1 (at even
+  // kt) and weights of stage kt + 2; down stage kt + 3
+  auto issue = [&](int kt) {
+    if constexpr (kGU) {
+      if ((kt & 1) == 0) issue_a(min(kt / 2 + 1, last_sk));
+      issue_b(min(kt + 2, last));
+    } else {
+      issue_down(min(kt + kStages - 1, last));
+    }
+  };
+  // Copies complete in issue order, so each wait leaves in flight exactly what was issued
+  // after the last piece the next stage needs (a wavefront that also copies scale words waits
+  // for a piece or two more than it needs): down, one stage of copies; gate_up, at the end of
+  // an even stage (the next stage needs only its weights) the copies issued at this stage, at
+  // the end of an odd stage (the next needs A superstage and weights issued at the stage
+  // before) the weights issued at this stage. Before stage 0: everything after stage 0's
+  // weights.
+  constexpr int kWaitFirst = kGU ? T::kQP + kNA + T::kQP : (kStages - 1) * T::kPiecesMin;
+  constexpr int kWaitEven = kGU ? kNA + T::kQP : (kStages - 2) * T::kPiecesMin;
+  constexpr int kWaitOdd = kGU ? T::kQP : (kStages - 2) * T::kPiecesMin;
   if (i < walk.tiles) {
     load_next(i);
     decode_next();
@@ -318,13 +375,29 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     // bytes 0-15 and K [32 + 16 h, + 16) in bytes 16-31, i.e. logical chunks h and h + 2 of
     // the row's 64 bytes.
     v8i fa[2], fb[4];
-    auto read_stage = [&](int kt) {
-      const int a0 = (kt % kStages) * kStage + a_lane, b0 = (kt % kStages) * kStage + b_lane;
+    // ks: the stage's k-step within its gate_up superstage (kt & 1)
+    auto read_stage = [&](int kt, auto ks_c) {
+      constexpr int ks = decltype(ks_c)::value;
+      const int b0 = (kGU ? (kt % 3) * kImgF8B : (kt % kStages) * kStage) + b_lane;
+      if constexpr (kGU) {
+        // row r0 + 32 i2's chunk c sits 4096 B after row r0's chunk c ^ 4, so the four lane
+        // addresses of chunks lk + 2 j serve both row blocks of both k-steps
+        const uint8_t* as = lds + ((kt >> 1) & 1) * T::kGASlot;
 #pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2) {
-        const v4i lo = *reinterpret_cast<const v4i*>(lds + a0 + 2048 * i2);
-        const v4i hi = *reinterpret_cast<const v4i*>(lds + (a0 ^ 32) + 2048 * i2);
-        fa[i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const int j = 2 * (ks ^ i2);  // chunk lk + 2 j: the k-step's first 16 bytes
+          const v4i lo = *reinterpret_cast<const v4i*>(as + a_ch[j] + 4096 * i2);
+          const v4i hi = *reinterpret_cast<const v4i*>(as + a_ch[j + 1] + 4096 * i2);
+          fa[i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      } else {
+        const int a0 = (kt % kStages) * kStage + a_lane;
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2) {
+          const v4i lo = *reinterpret_cast<const v4i*>(lds + a0 + 2048 * i2);
+          const v4i hi = *reinterpret_cast<const v4i*>(lds + (a0 ^ 32) + 2048 * i2);
+          fa[i2] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -339,23 +412,16 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     // tile's 16 right before its MFMA: the tile's previous MFMA finished a phase ago, and the
     // next tile's multiplies issue beside this tile's MFMA.
     float r00 = 1.0f, r01 = 1.0f, r10 = 1.0f, r11 = 1.0f;
-    v4f xc0 = {}, xc1 = {};  // scale-table chunks of the lane's two rows (see block_scales)
     int kb_next = 0;  // the K block whose weight scales swn0, swn1 hold
     auto block_scales = [&](int kt) {
       float x0, x1;
       if (MODE != kDown && table) {
-        // one 16-byte read per row brings the scales of 4 K blocks; they shift down a lane of
-        // the vector per block
-        if (((kt >> 1) & 3) == 0) {
-          xc0 = *reinterpret_cast<const v4f*>(lds + tab_off(wm * 64 + lr, kt >> 3));
-          xc1 = *reinterpret_cast<const v4f*>(lds + tab_off(wm * 64 + 32 + lr, kt >> 3));
-        }
-        x0 = xc0[0];
-        x1 = xc1[0];
-        xc0 = v4f{xc0[1], xc0[2], xc0[3], xc0[3]};
-        xc1 = v4f{xc1[1], xc1[2], xc1[3], xc1[3]};
+        const int kb = kt >> 1;
+        x0 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + lr, kb >> 2) + (kb & 3) * 4);
+        x1 = *reinterpret_cast<const float*>(lds + tab_off(wm * 64 + 32 + lr, kb >> 2) + (kb & 3) * 4);
       } else {
-        const float* sxs = reinterpret_cast<const float*>(lds + (kt % kStages) * kStage + T::kAScale);
+        const float* sxs = reinterpret_cast<const float*>(
+            lds + (kGU ? T::kGS + (kt % 3) * kBM * 4 : (kt % kStages) * kStage + T::kAScale));
         x0 = sxs[wm * 64 + lr];
         x1 = sxs[wm * 64 + 32 + lr];
       }
@@ -404,7 +470,7 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
     // counted waits allow one later stage in flight (a wavefront that also copies scale words
     // waits for one piece more than it needs).
     if constexpr (!kEarlyStart) issue_first();
-    wait_vmcnt<(kStages - 1) * T::kPiecesMin>();  // own pieces of stage 0 landed
+    wait_vmcnt<kWaitFirst>();  // own pieces of stage 0 landed
     __syncthreads();
     // The loops take two stages per iteration (KT is even), the K block's first with the
     // accumulators' factor and its second without, so neither MFMA phase branches on it (the
@@ -414,8 +480,8 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
         constexpr bool kFirst = decltype(first_c)::value;
         // the claim rides on the last stage, whose end waits for every copy anyway
         if (!kFirst && claims && kt == last) ticket = walk.claim_ticket();
-        if (kt >= 1) issue(min(kt + kStages - 1, last));
-        read_stage(kt);
+        if (kt >= 1) issue(kt);
+        read_stage(kt, std::integral_constant<int, kFirst ? 0 : 1>{});
         if constexpr (kFirst) block_scales(kt);
         wait_lds();  // own reads done (copies may be in flight)
         __syncthreads();
@@ -424,7 +490,7 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
         mma_stage(kFirst);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<(kStages - 2) * T::kPiecesMin>();  // own pieces of stage kt + 1
+        wait_vmcnt<kFirst ? kWaitEven : kWaitOdd>();  // own pieces of stage kt + 1
         __syncthreads();
       };
       for (int kt = 0; kt < KT; kt += 2) {
@@ -436,10 +502,10 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
       __syncthreads();
       auto phase = [&](int kt, auto first_c) {
         constexpr bool kFirst = decltype(first_c)::value;
-        if (kt >= 1) issue(min(kt + kStages - 1, last));
-        read_stage(kt);
+        if (kt >= 1) issue(kt);
+        read_stage(kt, std::integral_constant<int, kFirst ? 0 : 1>{});
         if constexpr (kFirst) block_scales(kt);
-        wait_vmcnt_lds<(kStages - 2) * T::kPiecesMin>();  // own reads, own pieces of stage kt + 1
+        wait_vmcnt_lds<kFirst ? kWaitEven : kWaitOdd>();  // own reads, own pieces of stage kt + 1
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_setprio(1);
@@ -490,7 +556,7 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
       // the down GEMM's A image (row tile mt, K stage column / 64); the group's scale goes
       // to the scale table.
       const int inter = p.N / 2;
-      float* amax_l = reinterpret_cast<float*>(lds + T::kAmax);
+      float* amax_l = reinterpret_cast<float*>(lds + T::kGAmax);
       auto quant_store = [&](auto fn) {
         float h[2][2][16];
 #pragma unroll
