@@ -108,6 +108,13 @@ __device__ __forceinline__ uint32_t pk_e4m3(float lo, float hi) {
 // Exchange between the lane halves of a wavefront: lane l < 32 receives hi_sends of lane
 // l + 32, lane l >= 32 receives lo_sends of lane l - 32 (lk = l / 32). One
 // v_permlane32_swap (VALU) instead of a ds_bpermute through the LDS crossbar.
+// The value x, opaque to the optimizer: what is computed from the result inside a loop stays
+// there instead of being hoisted out and kept live in a register across the whole loop.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ uint32_t swap_halves(uint32_t lo_sends, uint32_t hi_sends, int lk) {
   const auto r = __builtin_amdgcn_permlane32_swap(hi_sends, lo_sends, false, false);
   return lk ? r[0] : r[1];
@@ -335,6 +342,18 @@ __device__ __forceinline__ void lds_dma4(uint32_t m0, const void* base, uint32_t
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(m0), "v"(voff),
                "s"(uniform_ptr(base))
                : "memory");
+}
+
+// Global stores through inline assembly: the compiler neither moves, merges nor splits them,
+// so a caller that counts its vector-memory instructions for s_waitcnt knows their number.
+// A store of more than 8 bytes reads its data registers one cycle late, and the compiler
+// does not see that hazard in inline assembly, so the s_nop keeps the next instruction from
+// overwriting them first.
+__device__ __forceinline__ void store16(void* p, v4i v) {
+  asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store8(void* p, uint32_t v) {
+  asm volatile("global_store_byte %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
 
 // s_waitcnt vmcnt(N) leaving the other counters alone.

@@ -97,8 +97,16 @@ extern "C" __device__ v16f mfma_scale_f4_f8(v4i a, v8i b, v16f c, int cbsz, int 
                                             int opsel_a, int scale_a, int opsel_b, int scale_b)
     __asm("llvm.amdgcn.mfma.scale.f32.32x32x64.f8f6f4.v4i32.v8i32");
 
-template <int MODE, int WN>
+// kCont false: each tile fills the ring, runs its K loop, drains the ring and runs its
+// epilogue. kCont (gate_up with at least 3 K stages, static walk): the copy ring runs on across
+// tiles (the next tile's first stages are copied during the current tile's last two, like any
+// other stage) and each group's epilogue runs in its next read phase, beside the other group's
+// MFMAs. The dynamic walk keeps the first form: its claim's result would be a counted load
+// that the compiler waits for (draining the ring) wherever that register is copied or reused,
+// while the first form claims during a last stage whose end waits for every copy anyway.
+template <int MODE, int WN, bool kCont>
 __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArgs p) {
+  static_assert(!kCont || MODE != kDown, "the continuous ring is gate_up's (down stages y in LDS)");
   using T = MxTile<WN>;
   constexpr int kBM = T::kBM, kBN = T::kBN, kStages = T::kStages, kStage = T::kStage;
   __shared__ __attribute__((aligned(16))) uint8_t lds[T::kLds];
@@ -110,6 +118,11 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   // lane 0 claims the walk's dense positions (the tile after next, one tile ahead) and
   // publishes them here; every wavefront reads them after a barrier
   __shared__ int claimed[2];
+  // continuous ring: the next row tile's 128 pair indices, then its expert (64 copies)
+  __shared__ __attribute__((aligned(16))) int32_t meta[kCont ? kBM + 64 : 1];
+  // vector-memory instructions of one wavefront's gate_up epilogue: a 16-byte h chunk and a
+  // scale byte per MX block (2 x 2 blocks)
+  constexpr int kEpiStores = 8;
   const int KT = p.K / kImgK;
   const uint32_t lds_base = __builtin_amdgcn_readfirstlane(lds_offset(lds));
   const uint32_t voff = static_cast<uint32_t>(lane) * 16;
@@ -190,9 +203,9 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     b_tile = p.b_img + (e * nt256 + int64_t(nt) * T::kBImgs) * KT * int64_t(kImgB);
     src16 = img16 == 0 ? a_tile + kImgData : b_tile + int64_t(img16 - 1) * KT * kImgB + kImgData;
   };
-  auto issue_piece = [&](int kt, auto qc) {
+  auto issue_piece = [&](int kt, uint32_t slot_off, auto qc) {
     constexpr int q = decltype(qc)::value;
-    const uint32_t st = lds_base + static_cast<uint32_t>((kt % kStages) * kStage);
+    const uint32_t st = lds_base + slot_off;
     if constexpr (q == T::kImgs * T::kQP) {
       if (MODE != kDown && img16 == 0)  // 64 rows' scale words, gathered
         lds_dma4(st + kImgData + s_half * 256, a_scales + int64_t(kt) * 4, s_voff);
@@ -210,15 +223,17 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
                   b_tile + (int64_t(img - 1) * KT + kt) * kImgB + off, voff);
     }
   };
-  auto issue = [&](int kt) {
-    static_for<T::kPieces>([&](auto q) { issue_piece(kt, q); });
+  // stage kt of the copy tile into the ring slot at byte offset slot_off
+  auto issue_at = [&](int kt, uint32_t slot_off) {
+    static_for<T::kPieces>([&](auto q) { issue_piece(kt, slot_off, q); });
   };
+  auto issue = [&](int kt) { issue_at(kt, static_cast<uint32_t>((kt % kStages) * kStage)); };
   const int last = KT - 1;
 
   // The walk's dense positions: static (this workgroup's first, first + stride, ...) or,
   // with p.walk_ctr, claimed one tile ahead by lane 0 from its XCD's counter (the first two
   // here, each later one during the last K stage of the tile before the one that needs it).
-  const bool dynamic = p.walk_ctr != nullptr;
+  const bool dynamic = !kCont && p.walk_ctr != nullptr;
   int i = walk.first, i_next = walk.first + walk.stride;
   if (dynamic) {
     if (t == 0) {
@@ -237,6 +252,241 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
   // increment; an increment, which the compiler's atomic combining leaves alone, so nothing
   // waits for its result before the use)
   uint32_t ticket = 0;
+
+  v16f acc[2][4];
+  auto zero_acc = [&]() {
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
+  };
+  // 32-row blocks i of this group with a real row, in the tile being multiplied
+  bool live_i0 = false, live_i1 = false;
+
+  // Operand fragments of both k-steps of one stage, with the stage's scale words.
+  // 8-bit operand of the f8f6f4 MFMA: lane half h holds K [16h, 16h+16) in bytes 0-15 and
+  // K [32+16h, 32+16h+16) in bytes 16-31 of the k-step; the e2m1 operand holds K [32h, 32h+32);
+  // the scale of lane x+32b covers K block b.
+  struct Frag {
+    v8i a[2][2];  // [ks][i]
+    v4i b[2][4];  // [ks][j]
+    uint32_t sa[2], sb[4];  // bytes 0, 1: the scales of k-steps 0, 1 for this lane half
+  };
+  Frag f;
+  auto read_stage = [&](int s) {
+    const uint8_t* abase = lds + s * kStage;
+    const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
+    const uint16_t* sa = reinterpret_cast<const uint16_t*>(abase + kImgData) + lk;
+    const uint16_t* sb = reinterpret_cast<const uint16_t*>(bbase + kImgData) + lk;
+    // Row r + 32 has the swizzle of row r with chunk bit 2 flipped, so its chunk c sits 4096 B
+    // after row r's chunk c ^ 4: four lane addresses serve both row blocks, the second through
+    // the instruction's offset field.
+    const int r0 = wm * 64 + lr;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int i2 = 0; i2 < 2; ++i2) {
+        const int kc = (ks ^ i2) * 4 + lk;
+        f.a[ks][i2].lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc) + i2 * 4096);
+        f.a[ks][i2].hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc + 2) + i2 * 4096);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        f.b[ks][j] = *reinterpret_cast<const v4i*>(bbase + img_b_off(brow + j * 32 + lr, ks * 2 + lk));
+    }
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) f.sa[i2] = sa[2 * (wm * 64 + i2 * 32 + lr)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f.sb[j] = sb[2 * (brow + j * 32 + lr)];
+  };
+  // the 16 MFMAs of a stage (blocks of padding rows skipped)
+  auto mma_stage = [&]() {
+    static_for<2>([&](auto ksc) {
+      constexpr int ks = decltype(ksc)::value;
+      static_for<2>([&](auto i2c) {
+        constexpr int i2 = decltype(i2c)::value;
+        static_for<4>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          // D[weight row][activation row]; op_sel ks: byte ks of the lane's scale half-word
+          if (i2 == 0 ? live_i0 : live_i1)
+            acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
+                                          0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
+                                          static_cast<int>(f.sa[i2]));
+        });
+      });
+    });
+  };
+
+  // gate_up epilogue of row tile mt, columns [n0, n0 + kBN), from the accumulators.
+  // Accumulator q of tile (i, j): activation row 64 wm + 32 i + lane % 32, output column
+  // 128 wn + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4. Column tiles j = 2 jj and 2 jj + 1 are
+  // the gate and up halves of one 64-row group of interleaved W13, i.e. the same 32
+  // intermediate columns: one MX block of h per (i, jj), 16 values in this lane and 16 in
+  // lane ^ 32. The block's scale needs one exchange; then lane half lk assembles 16-byte chunk
+  // lk of the block (h columns 16 lk .. 16 lk + 15) with a second, and stores it into the down
+  // GEMM's A image (stage n0 / 256 + block / 4 of row tile mt). Exactly kEpiStores
+  // vector-memory instructions per wavefront (inline assembly, so the count is fixed): the
+  // continuous ring's waits count them.
+  auto gate_up_epilogue = [&](int mt, int n0) __attribute__((always_inline)) {
+    const int kt_down = p.N / kImgBRows;  // K stages of the down GEMM (I / 128)
+    // lane-derived addresses are computed here, not kept live through the K loop
+    const int ln = opaque(lane), lr = ln & 31, lk = ln >> 5;
+    auto quant_store = [&](auto fn) {
+      static_for<2>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        static_for<2>([&](auto jjc) {
+          constexpr int jj = decltype(jjc)::value;
+          float h[16];
+          float amax = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            h[q] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
+            amax = fmaxf(amax, fabsf(h[q]));
+          }
+          amax = fmaxf(amax, xor32(amax, lk));
+          const uint32_t code = mx_scale_code(amax, 8);
+          const float inv = mx_inv_scale(code);
+          uint32_t d[4];  // h columns 8 q4 + 4 lk .. + 3
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            d[q4] = pk4_e4m3(h[4 * q4] * inv, h[4 * q4 + 1] * inv, h[4 * q4 + 2] * inv,
+                             h[4 * q4 + 3] * inv);
+          // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
+          // 16-31 (the partner's d2, d3 and its own)
+          const uint32_t p0 = swap_halves(d[2], d[0], lk);
+          const uint32_t p1 = swap_halves(d[3], d[1], lk);
+          v4i chunk;
+          chunk[0] = static_cast<int>(lk ? p0 : d[0]);
+          chunk[1] = static_cast<int>(lk ? d[2] : p0);
+          chunk[2] = static_cast<int>(lk ? p1 : d[1]);
+          chunk[3] = static_cast<int>(lk ? d[3] : p1);
+          const int row = wm * 64 + i * 32 + lr;
+          const int hblk = wn * 2 + jj;  // MX block among the tile's kBN / 64
+          uint8_t* img = p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + hblk / 4) * kImgA;
+          const int jb = hblk % 4;
+          store16(img + img_a_off(row, 2 * jb + lk), chunk);
+          // both lane halves hold the block's code (the amax was exchanged): the same byte to
+          // the same place
+          store8(img + kImgData + row * 4 + scale_byte(jb), code);
+        });
+      });
+    };
+    if constexpr (MODE == kGateUpParam) {
+      if (p.act.act == AFD_ACT_SITU)
+        quant_store([&](float g, float u) {
+          return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
+        });
+      else
+        quant_store([&](float g, float u) { return act_swiglu_limit(g, u, p.act.l); });
+    } else {
+      quant_store([](float g, float u) { return act_swiglu(g, u); });
+    }
+  };
+
+  if constexpr (kCont) {
+    // Continuous ring. Stages are numbered across tiles and take ring slots in turn; a tile's
+    // stage kt + 2 (past its last: the next tile's stage kt + 2 - KT, or a rewrite of the last
+    // stage into the free slot if there is no next tile) is copied when stage kt is read, so
+    // the copies never drain. The copies switch to the next tile two stages before the end: by
+    // then its 128 pair indices and its expert, copied into `meta` by direct-to-LDS copies of
+    // waves 0-2 at the tile's first stage (older than that stage's ring copies, so that
+    // stage's waits cover them), are decoded from LDS. A group's epilogue of the previous tile
+    // runs in its first read phase of the next tile, beside the other group's MFMAs; its
+    // kEpiStores stores are issued after that stage's copies, so the waits of that stage
+    // allow them in flight, and the next stage's waits take them in.
+    if (i >= walk.tiles) return;
+    load_next(i);
+    decode_next();
+    int mt, nt;
+    walk.at_dense(i, mt, nt);
+    copy_tile(mt, nt, e_cur);
+    issue_at(0, 0);
+    issue_at(1, kStage);
+    wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
+    __syncthreads();
+    if (wm != 0) __syncthreads();  // group 1 runs half a stage behind group 0
+    const uint32_t meta_lds = lds_offset(meta);
+    // the tile loop of one group (kG0: group 0), instantiated per group so that each loop body
+    // holds one form of the stage
+    auto run = [&](auto grp) __attribute__((always_inline)) {
+    constexpr bool kG0 = decltype(grp)::value;
+    int rs = 0;  // ring slot of the stage read next
+    int mt_prev = 0, n0_prev = 0;
+    for (bool first = true;; first = false) {
+      walk.at_dense(i, mt, nt);
+      const bool has_next = i_next < walk.tiles;
+      int mt1 = 0, nt1 = 0;
+      if (has_next) walk.at_dense(i_next, mt1, nt1);
+      live_i0 = live_cur > 0;
+      live_i1 = live_cur > 32;
+      auto stage = [&](int kt, auto epi) __attribute__((always_inline)) {
+        constexpr int kSt = decltype(epi)::value ? kEpiStores : 0;
+        if (kt == 0) {
+          if (has_next && w_u < 3) {
+            const int32_t* src = w_u == 2 ? p.tile_expert + mt1
+                                          : p.sorted_pairs + int64_t(mt1) * kBM + 64 * w_u;
+            lds_dma4(meta_lds + w_u * 256, src, w_u == 2 ? 0u : static_cast<uint32_t>(lane) * 4);
+          }
+        }
+        if (kt == last - 1 && has_next) {
+          const int ln = opaque(lane);
+          e_next = meta[kBM];
+          own_next = meta[64 * wm + ln];
+#pragma unroll
+          for (int q = 0; q < T::kQP; ++q) sp_next[q] = meta[8 * (w_u * T::kQP + q) + (ln >> 3)];
+          sp_next[T::kQP] = meta[64 * s_half + ln];
+          decode_next();
+          copy_tile(mt1, nt1, e_cur);
+        }
+        const int ck = kt + 2 <= last ? kt + 2 : has_next ? kt + 2 - KT : last;
+        issue_at(ck, static_cast<uint32_t>((rs == 0 ? 2 : rs - 1) * kStage));
+        if constexpr (decltype(epi)::value) gate_up_epilogue(mt_prev, n0_prev);
+        if (kt == 0) zero_acc();
+        read_stage(rs);
+        if constexpr (kG0) {
+          wait_vmcnt_lds<2 * T::kPieces + kSt>();  // own reads done (copies may be in flight)
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_setprio(1);
+          mma_stage();
+          __builtin_amdgcn_s_setprio(0);
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<T::kPieces + kSt>();  // own pieces of the next stage landed
+          __syncthreads();
+        } else {
+          wait_vmcnt_lds<T::kPieces + kSt>();  // own reads done, own next pieces landed
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_setprio(1);
+          mma_stage();
+          __builtin_amdgcn_s_setprio(0);
+          __builtin_amdgcn_sched_barrier(0);
+          __syncthreads();
+        }
+        rs = rs == 2 ? 0 : rs + 1;
+      };
+      if (first)
+        stage(0, std::false_type{});
+      else
+        stage(0, std::true_type{});
+      for (int kt = 1; kt < KT; ++kt) stage(kt, std::false_type{});
+      mt_prev = mt;
+      n0_prev = nt * kBN;
+      if (!has_next) break;
+      i = i_next;
+      i_next = min(i_next + walk.stride, walk.tiles);
+    }
+    // the last tile's epilogue: group 0's beside group 1's last MFMAs, then group 1's
+    gate_up_epilogue(mt_prev, n0_prev);
+    if constexpr (kG0) __syncthreads();
+    };
+    if (wm == 0)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
+  } else {
   if (i < walk.tiles) {
     load_next(i);
     decode_next();
@@ -259,72 +509,11 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     // real (loaded now, used by the epilogue)
     int row_end = 0;
     if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    // 32-row blocks i of this group with a real row
-    const bool live_i0 = live_cur > 0, live_i1 = live_cur > 32;
+    live_i0 = live_cur > 0;
+    live_i1 = live_cur > 32;
     if (has_next) load_next(i_next);
     if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
-
-    v16f acc[2][4];
-#pragma unroll
-    for (int i2 = 0; i2 < 2; ++i2)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 16; ++q) acc[i2][j][q] = 0.0f;
-
-    // Operand fragments of both k-steps of one stage, with the stage's scale words.
-    // 8-bit operand of the f8f6f4 MFMA: lane half h holds K [16h, 16h+16) in bytes 0-15 and
-    // K [32+16h, 32+16h+16) in bytes 16-31 of the k-step; the e2m1 operand holds K [32h, 32h+32);
-    // the scale of lane x+32b covers K block b.
-    struct Frag {
-      v8i a[2][2];  // [ks][i]
-      v4i b[2][4];  // [ks][j]
-      uint32_t sa[2], sb[4];  // bytes 0, 1: the scales of k-steps 0, 1 for this lane half
-    };
-    Frag f;
-    auto read_stage = [&](int s) {
-      const uint8_t* abase = lds + s * kStage;
-      const uint8_t* bbase = abase + T::kLdsA + bimg * kImgB;
-      const uint16_t* sa = reinterpret_cast<const uint16_t*>(abase + kImgData) + lk;
-      const uint16_t* sb = reinterpret_cast<const uint16_t*>(bbase + kImgData) + lk;
-      // Row r + 32 has the swizzle of row r with chunk bit 2 flipped, so its chunk c sits 4096 B
-      // after row r's chunk c ^ 4: four lane addresses serve both row blocks, the second through
-      // the instruction's offset field.
-      const int r0 = wm * 64 + lr;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-        for (int i2 = 0; i2 < 2; ++i2) {
-          const int kc = (ks ^ i2) * 4 + lk;
-          f.a[ks][i2].lo = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc) + i2 * 4096);
-          f.a[ks][i2].hi = *reinterpret_cast<const v4i*>(abase + img_a_off(r0, kc + 2) + i2 * 4096);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          f.b[ks][j] = *reinterpret_cast<const v4i*>(bbase + img_b_off(brow + j * 32 + lr, ks * 2 + lk));
-      }
-#pragma unroll
-      for (int i2 = 0; i2 < 2; ++i2) f.sa[i2] = sa[2 * (wm * 64 + i2 * 32 + lr)];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) f.sb[j] = sb[2 * (brow + j * 32 + lr)];
-    };
-    // the 16 MFMAs of a stage (blocks of padding rows skipped)
-    auto mma_stage = [&]() {
-      static_for<2>([&](auto ksc) {
-        constexpr int ks = decltype(ksc)::value;
-        static_for<2>([&](auto i2c) {
-          constexpr int i2 = decltype(i2c)::value;
-          static_for<4>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            // D[weight row][activation row]; op_sel ks: byte ks of the lane's scale half-word
-            if (i2 == 0 ? live_i0 : live_i1)
-              acc[i2][j] = mfma_scale_f4_f8(f.b[ks][j], f.a[ks][i2], acc[i2][j], 4 /*A e2m1*/,
-                                            0 /*B e4m3*/, ks, static_cast<int>(f.sb[j]), ks,
-                                            static_cast<int>(f.sa[i2]));
-          });
-        });
-      });
-    };
+    zero_acc();
 
     // Ping-pong: the two wavefronts of a SIMD (one per group) alternate between reading a
     // stage's operands from LDS and running its 16 MFMAs, half a stage apart, so one of them
@@ -396,65 +585,8 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       }
     }
 
-    // Accumulator q of tile (i, j): activation row 64 wm + 32 i + lane % 32, output column
-    // 128 wn + 32 j + 8 (q / 4) + 4 (lane / 32) + q % 4.
     if constexpr (MODE != kDown) {
-      // Column tiles j = 2 jj and 2 jj + 1 are the gate and up halves of one 64-row group of
-      // interleaved W13, i.e. the same 32 intermediate columns: one MX block of h per (i, jj),
-      // 16 values in this lane and 16 in lane ^ 32. The block's scale needs one exchange; then
-      // lane half lk assembles 16-byte chunk lk of the block (h columns 16 lk .. 16 lk + 15)
-      // with a second, and stores it into the down GEMM's A image (stage n0 / 256 + block / 4
-      // of row tile mt).
-      const int kt_down = p.N / kImgBRows;  // K stages of the down GEMM (I / 128)
-      auto quant_store = [&](auto fn) {
-        static_for<2>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          static_for<2>([&](auto jjc) {
-            constexpr int jj = decltype(jjc)::value;
-            float h[16];
-            float amax = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-              h[q] = fn(acc[i][2 * jj][q], acc[i][2 * jj + 1][q]);
-              amax = fmaxf(amax, fabsf(h[q]));
-            }
-            amax = fmaxf(amax, xor32(amax, lk));
-            const uint32_t code = mx_scale_code(amax, 8);
-            const float inv = mx_inv_scale(code);
-            uint32_t d[4];  // h columns 8 q4 + 4 lk .. + 3
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4)
-              d[q4] = pk4_e4m3(h[4 * q4] * inv, h[4 * q4 + 1] * inv, h[4 * q4 + 2] * inv,
-                               h[4 * q4 + 3] * inv);
-            // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
-            // 16-31 (the partner's d2, d3 and its own)
-            const uint32_t p0 = swap_halves(d[2], d[0], lk);
-            const uint32_t p1 = swap_halves(d[3], d[1], lk);
-            v4i chunk;
-            chunk[0] = static_cast<int>(lk ? p0 : d[0]);
-            chunk[1] = static_cast<int>(lk ? d[2] : p0);
-            chunk[2] = static_cast<int>(lk ? p1 : d[1]);
-            chunk[3] = static_cast<int>(lk ? d[3] : p1);
-            const int row = wm * 64 + i * 32 + lr;
-            const int hblk = wn * 2 + jj;  // MX block among the tile's kBN / 64
-            uint8_t* img =
-                p.h_img + (int64_t(mt) * kt_down + n0 / kImgBRows + hblk / 4) * kImgA;
-            const int jb = hblk % 4;
-            *reinterpret_cast<v4i*>(img + img_a_off(row, 2 * jb + lk)) = chunk;
-            if (lk == 0) img[kImgData + row * 4 + scale_byte(jb)] = static_cast<uint8_t>(code);
-          });
-        });
-      };
-      if constexpr (MODE == kGateUpParam) {
-        if (p.act.act == AFD_ACT_SITU)
-          quant_store([&](float g, float u) {
-            return act_situ(g, u, p.act.a, p.act.inv_a, p.act.l, p.act.inv_l);
-          });
-        else
-          quant_store([&](float g, float u) { return act_swiglu_limit(g, u, p.act.l); });
-      } else {
-        quant_store([](float g, float u) { return act_swiglu(g, u); });
-      }
+      gate_up_epilogue(mt, n0);
     } else {
       // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
       // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
@@ -502,15 +634,16 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
       __syncthreads();
     }
   }
+  }
 }
 
-template <int MODE, int WN>
+template <int MODE, int WN, bool kCont>
 static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream) {
   using T = MxTile<WN>;
   // resident workgroups per CU (registers and LDS decide); initialized once, thread-safely
   static const int per_cu = [] {
     int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE, WN>, T::kThreads,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, mx_gemm_kernel<MODE, WN, kCont>, T::kThreads,
                                                      0) != hipSuccess ||
         b < 1)
       b = 1;
@@ -520,15 +653,23 @@ static int launch_mx(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream)
   MxGemmArgs a = p;
   int grid = device_cu_count() * per_cu;
   if (max_tiles < grid) grid = max_tiles < 1 ? 1 : max_tiles;
-  hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN>), dim3(grid), dim3(T::kThreads), 0, stream, a);
+  hipLaunchKernelGGL((mx_gemm_kernel<MODE, WN, kCont>), dim3(grid), dim3(T::kThreads), 0, stream, a);
   AFD_CHECK_LAUNCH();
   return AFD_OK;
 }
 
 template <int MODE>
 static int launch_mx_any(const MxGemmArgs& p, int max_row_tiles, hipStream_t stream) {
-  if (p.N % MxTile<4>::kBN == 0) return launch_mx<MODE, 4>(p, max_row_tiles, stream);
-  return launch_mx<MODE, 2>(p, max_row_tiles, stream);
+  if constexpr (MODE != kDown) {
+    // the continuous ring (static walk) decodes the next tile two stages before the end and
+    // reads what was copied at the first stage: three stages at least
+    if (p.K / kImgK >= 3 && p.walk_ctr == nullptr) {
+      if (p.N % MxTile<4>::kBN == 0) return launch_mx<MODE, 4, true>(p, max_row_tiles, stream);
+      return launch_mx<MODE, 2, true>(p, max_row_tiles, stream);
+    }
+  }
+  if (p.N % MxTile<4>::kBN == 0) return launch_mx<MODE, 4, false>(p, max_row_tiles, stream);
+  return launch_mx<MODE, 2, false>(p, max_row_tiles, stream);
 }
 
 int launch_mx_gate_up(const afd_moe_cfg& cfg, const afd_expert_weights& wt, uint8_t* ws,

@@ -99,7 +99,9 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
   if constexpr (kWriteThrough) {
     // one 16-byte vector store per lane (a wavefront writes 1 KiB of whole lines), with the
     // system-scope cache bits; the caller waits for its acknowledgement
-    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(out_row + col), "v"(o)
+    // (the s_nop: a store of more than 8 bytes reads its data registers a cycle late, a
+    // hazard the compiler does not see in inline assembly)
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 0" ::"v"(out_row + col), "v"(o)
                  : "memory");
   } else {
     *reinterpret_cast<v4i*>(out_row + col) = o;
