@@ -11,7 +11,13 @@ every format the kernels write there (bf16 y and h, e4m3 h, UE8M0 and fp32 scale
 dynamic walk runs first: a tile that a walk skipped would leave NaN rows behind, which reach
 the output through the finalize, so each output is also checked to hold no NaN. (That every
 tile is taken exactly once is shown on the CPU for the walk code itself,
-tests/test_walk_model.py.)"""
+tests/test_walk_model.py.)
+
+The MXFP4 gate_up of the static walk with at least 3 K stages runs its copy ring on across
+tiles (the next tile decoded from LDS two stages before the end, the previous tile's epilogue
+inside the next tile's first stage); the dynamic walk runs tile by tile. Their equality pins
+that form, down to its smallest K (hidden 512: 4 stages) and its 256-column tiles (2I not a
+multiple of 512)."""
 
 import time
 
@@ -84,6 +90,16 @@ def test_walks_agree(fmt):
         x, topk = job(n, 1024, 32, seed, zipf)
         s, d = both(experts, x, topk)
         assert np.array_equal(s, d), (fmt, n, seed)
+
+
+@pytest.mark.parametrize("hidden,inter", [(512, 384), (256, 128), (768, 256), (1536, 640)])
+def test_walks_agree_across_shapes(hidden, inter):
+    experts = layer("mxfp4", hidden, inter, 16, 2048, seed=hidden)
+    for n, seed, zipf in ((5, 11, None), (700, 12, None), (2048, 13, 1.2)):
+        say(f"walks mxfp4 H={hidden} I={inter} n={n} zipf={zipf}")
+        x, topk = job(n, hidden, 16, seed, zipf)
+        s, d = both(experts, x, topk)
+        assert np.array_equal(s, d), (hidden, inter, n, seed)
 
 
 def test_dynamic_walk_with_a_parked_wait():
