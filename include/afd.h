@@ -30,6 +30,10 @@
  *                                (P/srt/layers/moe/token_dispatcher/asap.py:174-184) fused
  *                                with the shared-expert add (P/srt/batch_overlap/
  *                                operations_strategy.py:106-111)
+ *   afd_silu_mul ............... the activation of the attention rank's shared-expert MLP
+ *                                (computed at P/srt/batch_overlap/operations_strategy.py:94,
+ *                                255 by SGLang's DeepseekV2MLP: SiluAndMul between its
+ *                                gate_up and down projections)
  *   afd_pack_mxfp4 / _fp8_block  the quant methods' weight repack at load time
  *                                (FlashInfer layout, mxfp4_flashinfer_trtllm_moe.py:11-13)
  *   afd_repack_mxfp4 / ......... the checkpoint expert load (P/srt/model_loader/weight_utils.py
@@ -60,7 +64,7 @@
 extern "C" {
 #endif
 
-#define AFD_ABI_VERSION 5
+#define AFD_ABI_VERSION 6
 
 typedef void* afd_stream_t; /* a hipStream_t; NULL is the null stream */
 
@@ -370,6 +374,14 @@ int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const float* w, int
  * + fp32(shared)) : routed. `parts` is a host array of device pointers. */
 int afd_combine(const uint16_t* const* parts, int32_t num_parts, const uint16_t* shared,
                 uint16_t* out, int64_t numel, afd_stream_t stream);
+
+/* The shared-expert MLP's activation (replaces SGLang's SiluAndMul in the MLP the reference
+ * calls at P/srt/batch_overlap/operations_strategy.py:94, 255): gate_up bf16 [n][2 inter]
+ * (gate columns first, then up) -> out bf16 [n][inter], out = bf16(silu(g) * u) computed in
+ * float with one rounding, silu(g) = g / (1 + e^-g). inter a multiple of 8, both pointers
+ * 16-byte aligned, n * inter / 8 < 2^32. */
+int afd_silu_mul(const uint16_t* gate_up, int64_t n, int32_t inter, uint16_t* out,
+                 afd_stream_t stream);
 
 /* ---- transport (one GPU: producer and consumer streams) ---------------------------------
  * Done flags are 64-bit message counters that only grow (a message's counter is the count of

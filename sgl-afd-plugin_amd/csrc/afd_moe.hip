@@ -218,6 +218,29 @@ __global__ __launch_bounds__(256) void combine_kernel(PartList parts, int num_pa
   }
 }
 
+// ---------------------------------------------------------------- shared-expert activation
+// h = bf16(silu(g) * u) for the rows of [gate | up] (bf16 [n][2 inter]): a lane takes 8
+// columns, 16 bytes of g and 16 of u from one row, computes the routed experts' SwiGLU in
+// float and rounds once. HBM-bound: per element 4 B read, 2 B written.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                       uint32_t vecs, uint32_t vpr,
+                                                       uint16_t* __restrict__ out) {
+  for (uint32_t v = blockIdx.x * 256u + threadIdx.x; v < vecs; v += gridDim.x * 256u) {
+    const uint32_t r = v / vpr, c = v - r * vpr;
+    const v4i* row = reinterpret_cast<const v4i*>(gu + int64_t(r) * vpr * 16);
+    const v4i g = row[c], u = row[vpr + c];
+    v4i o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t a = static_cast<uint32_t>(g[i]), b = static_cast<uint32_t>(u[i]);
+      o[i] = static_cast<int>(
+          pk_bf16(act_swiglu(__uint_as_float(a << 16), __uint_as_float(b << 16)),
+                  act_swiglu(__uint_as_float(a & 0xffff0000u), __uint_as_float(b & 0xffff0000u))));
+    }
+    reinterpret_cast<v4i*>(out + int64_t(r) * vpr * 8)[c] = o;
+  }
+}
+
 // ---------------------------------------------------------------- configuration checks
 static int check_cfg(const afd_moe_cfg* cfg) {
   if (!cfg) return AFD_ERR_ARG;
@@ -592,6 +615,24 @@ extern "C" int afd_finalize(const uint16_t* y, const int32_t* pair_pos, const fl
   if (hidden <= 0 || hidden % kFinElems) return AFD_ERR_SHAPE;
   const JobIn job{nullptr, nullptr, nullptr, w, out, n};
   return launch_finalize(y, pair_pos, job, k, hidden, Reply{}, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int afd_silu_mul(const uint16_t* gate_up, int64_t n, int32_t inter, uint16_t* out,
+                            afd_stream_t stream) {
+  if (n < 0 || inter <= 0) return AFD_ERR_ARG;
+  if (n == 0) return AFD_OK;
+  if (!gate_up || !out) return AFD_ERR_ARG;
+  if (inter % 8 || reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+    return AFD_ERR_SHAPE;
+  const int64_t vecs = n * (inter / 8);
+  if (vecs > 0xffffffffll) return AFD_ERR_SHAPE;
+  int64_t grid = (vecs + 255) / 256;
+  if (grid > int64_t(8) * device_cu_count()) grid = int64_t(8) * device_cu_count();
+  hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), gate_up, static_cast<uint32_t>(vecs),
+                     static_cast<uint32_t>(inter / 8), out);
+  AFD_CHECK_LAUNCH();
+  return AFD_OK;
 }
 
 extern "C" int afd_combine(const uint16_t* const* parts, int32_t num_parts,

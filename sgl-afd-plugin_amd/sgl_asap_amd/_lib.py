@@ -36,7 +36,7 @@ AFD_WAIT_GEQ, AFD_WAIT_EQ, AFD_WAIT_AND, AFD_WAIT_NOR = 0, 1, 2, 3
 AFD_WALK_STATIC, AFD_WALK_DYNAMIC = 0, 1
 
 # afd_abi_version() of the library these structures match
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # Every entry point include/afd.h declares; tests check the library exports all of them.
 EXPORTED = (
@@ -62,6 +62,7 @@ EXPORTED = (
     "afd_moe_ffn_profiled",
     "afd_finalize",
     "afd_combine",
+    "afd_silu_mul",
     "afd_host_alloc",
     "afd_host_free",
     "afd_copy_async",
@@ -247,6 +248,7 @@ _SIGS = {
     ),
     "afd_finalize": ([_P, _P, _P, _I32, _I32, _I32, _P, _P], _I32),
     "afd_combine": ([ctypes.POINTER(ctypes.c_void_p), _I32, _P, _P, _I64, _P], _I32),
+    "afd_silu_mul": ([_P, _I64, _I32, _P, _P], _I32),
     "afd_host_alloc": ([ctypes.POINTER(ctypes.c_void_p), _U64], _I32),
     "afd_host_free": ([_P], _I32),
     "afd_copy_async": ([_P, _P, _U64, _P], _I32),

@@ -5,9 +5,11 @@ In the reference the shared experts stay on the attention rank and are the model
 the combine (``python/sgl_asap_plugin/srt/batch_overlap/operations_strategy.py:106-111``,
 ordering in ``srt/batch_overlap/single_batch_overlap.py:109-134``). This module is that MLP
 for the one-GPU loop and its benchmark: plain library GEMMs (hipBLASLt through torch) in
-bf16, with the gate and up projections in one matrix.
+bf16, with the gate and up projections in one matrix, and between them the activation as one
+HBM-bound kernel (``afd_silu_mul``, SGLang's fused SiluAndMul; silu and the product as two
+torch kernels on the strided gate half took 164 us of a loop layer).
 
-    out = W_down . (silu(W_gate . x) * (W_up . x))
+    out = W_down . bf16(silu(W_gate . x) * (W_up . x))
 
 The add itself is fused into the combine kernel (``afd_combine``'s ``shared`` argument).
 """
@@ -15,6 +17,8 @@ The add itself is fused into the combine kernel (``afd_combine``'s ``shared`` ar
 from __future__ import annotations
 
 import torch
+
+from .. import _lib
 
 
 class SharedExpertMLP(torch.nn.Module):
@@ -50,5 +54,18 @@ class SharedExpertMLP(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.hidden_size:
             raise TypeError(f"expected bf16 [n, {self.hidden_size}], got {x.dtype} {tuple(x.shape)}")
-        gate, up = torch.mm(x, self.w_gate_up.t()).split(self.intermediate_size, dim=1)
-        return torch.mm(torch.nn.functional.silu(gate) * up, self.w_down.t())
+        gate_up = torch.mm(x, self.w_gate_up.t())
+        return torch.mm(silu_mul(gate_up), self.w_down.t())
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """bf16(silu(gate) * up) of bf16 [n, 2I] rows [gate | up] on their device's current stream:
+    SGLang's SiluAndMul, as ``afd_silu_mul``."""
+    if gate_up.dtype != torch.bfloat16 or gate_up.dim() != 2 or gate_up.shape[1] % 2:
+        raise TypeError(f"expected bf16 [n, 2I], got {gate_up.dtype} {tuple(gate_up.shape)}")
+    gate_up = gate_up.contiguous()
+    n, inter = gate_up.shape[0], gate_up.shape[1] // 2
+    out = torch.empty(n, inter, dtype=torch.bfloat16, device=gate_up.device)
+    _lib.call("afd_silu_mul", gate_up.data_ptr(), n, inter, out.data_ptr(),
+              torch.cuda.current_stream(gate_up.device).cuda_stream)
+    return out

@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_functions():
         assert hasattr(L, name), name
-    assert L.afd_abi_version() == _lib.ABI_VERSION == 5
+    assert L.afd_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_status_strings():
@@ -103,6 +103,18 @@ def test_activation_format_checks():
     # bf16 activations are not quantized: afd_quant_act refuses before touching any pointer
     a16 = _lib.AfdMoeCfg(256, 128, 2, 0, 8, _lib.AFD_W_MXFP4, 0, 0.0, 0.0, 0, _lib.AFD_A_BF16)
     assert L.afd_quant_act(ctypes.byref(a16), None, 0, None, None, None) == _lib.AFD_ERR_UNSUPPORTED
+
+
+def test_silu_mul_argument_checks():
+    """afd_silu_mul refuses bad shapes on the host, before any launch."""
+    L = _lib.lib()
+    assert L.afd_silu_mul(None, 0, 1536, None, None) == _lib.AFD_OK  # nothing to do
+    assert L.afd_silu_mul(None, -1, 1536, None, None) == _lib.AFD_ERR_ARG
+    assert L.afd_silu_mul(None, 4, 0, None, None) == _lib.AFD_ERR_ARG
+    assert L.afd_silu_mul(None, 4, 1536, None, None) == _lib.AFD_ERR_ARG
+    assert L.afd_silu_mul(16, 4, 1540, 16, None) == _lib.AFD_ERR_SHAPE  # inter not a multiple of 8
+    assert L.afd_silu_mul(8, 4, 1536, 16, None) == _lib.AFD_ERR_SHAPE  # misaligned rows
+    assert L.afd_silu_mul(16, 1 << 30, 64, 16, None) == _lib.AFD_ERR_SHAPE  # 2^33 vectors
 
 
 def test_python_activation_formats():

@@ -1,4 +1,5 @@
-"""GPU parity: finalize (top-k weighted sum) and the A-side combine are bit-exact."""
+"""GPU parity: finalize (top-k weighted sum) and the A-side combine are bit-exact; the
+shared expert's fused SiLU-and-multiply matches a plain PyTorch fp32 reference."""
 
 import numpy as np
 import pytest
@@ -54,3 +55,28 @@ def test_combine_bitexact(parts_n, with_shared):
         for p in parts[1:]:
             acc += p
         assert np.array_equal(bits16(out), bits16(acc.to(torch.bfloat16)))
+
+
+@pytest.mark.parametrize("n,inter", [(1, 8), (7, 1536), (1000, 1536), (300, 2056)])
+def test_silu_mul_against_torch_fp32(n, inter):
+    """afd_silu_mul = bf16(silu(g) * u) in float, one rounding: against torch fp32 on the CPU,
+    every element within one bf16 step (the kernel's exp and reciprocal are the hardware's
+    approximations, so a value within a few float ulps of a rounding boundary may round the
+    other way) and at most 1% of them off at all; gate and up are told apart."""
+    from sgl_asap_amd.moe.shared import silu_mul
+
+    say(f"silu_mul n={n} inter={inter}")
+    g = torch.Generator().manual_seed(n + inter)
+    gu = (torch.randn(n, 2 * inter, generator=g) * 3).to(torch.bfloat16)
+    gu[0, 0], gu[0, inter] = 0.0, 5.0  # silu(0) * u = 0 exactly
+    got = silu_mul(gu.to(dev()))
+    torch.cuda.synchronize()
+    gate, up = gu.float()[:, :inter], gu.float()[:, inter:]
+    ref = (torch.nn.functional.silu(gate) * up).to(torch.bfloat16)
+    a, b = bits16(got).astype(np.int32), bits16(ref).astype(np.int32)
+    steps = np.abs(a - b)
+    assert steps.max() <= 1, steps.max()
+    assert np.mean(steps != 0) <= 0.01
+    assert bits16(got)[0, 0] == 0
+    swapped = (torch.nn.functional.silu(up) * gate).to(torch.bfloat16)
+    assert np.mean(bits16(swapped) == a) < 0.5
