@@ -411,229 +411,229 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
     // the tile loop of one group (kG0: group 0), instantiated per group so that each loop body
     // holds one form of the stage
     auto run = [&](auto grp) __attribute__((always_inline)) {
-    constexpr bool kG0 = decltype(grp)::value;
-    int rs = 0;  // ring slot of the stage read next
-    int mt_prev = 0, n0_prev = 0;
-    for (bool first = true;; first = false) {
-      walk.at_dense(i, mt, nt);
-      const bool has_next = i_next < walk.tiles;
-      int mt1 = 0, nt1 = 0;
-      if (has_next) walk.at_dense(i_next, mt1, nt1);
-      live_i0 = live_cur > 0;
-      live_i1 = live_cur > 32;
-      auto stage = [&](int kt, auto epi) __attribute__((always_inline)) {
-        constexpr int kSt = decltype(epi)::value ? kEpiStores : 0;
-        if (kt == 0) {
-          if (has_next && w_u < 3) {
-            const int32_t* src = w_u == 2 ? p.tile_expert + mt1
-                                          : p.sorted_pairs + int64_t(mt1) * kBM + 64 * w_u;
-            lds_dma4(meta_lds + w_u * 256, src, w_u == 2 ? 0u : static_cast<uint32_t>(lane) * 4);
+      constexpr bool kG0 = decltype(grp)::value;
+      int rs = 0;  // ring slot of the stage read next
+      int mt_prev = 0, n0_prev = 0;
+      for (bool first = true;; first = false) {
+        walk.at_dense(i, mt, nt);
+        const bool has_next = i_next < walk.tiles;
+        int mt1 = 0, nt1 = 0;
+        if (has_next) walk.at_dense(i_next, mt1, nt1);
+        live_i0 = live_cur > 0;
+        live_i1 = live_cur > 32;
+        auto stage = [&](int kt, auto epi) __attribute__((always_inline)) {
+          constexpr int kSt = decltype(epi)::value ? kEpiStores : 0;
+          if (kt == 0) {
+            if (has_next && w_u < 3) {
+              const int32_t* src = w_u == 2 ? p.tile_expert + mt1
+                                            : p.sorted_pairs + int64_t(mt1) * kBM + 64 * w_u;
+              lds_dma4(meta_lds + w_u * 256, src, w_u == 2 ? 0u : static_cast<uint32_t>(lane) * 4);
+            }
           }
-        }
-        if (kt == last - 1 && has_next) {
-          const int ln = opaque(lane);
-          e_next = meta[kBM];
-          own_next = meta[64 * wm + ln];
-#pragma unroll
-          for (int q = 0; q < T::kQP; ++q) sp_next[q] = meta[8 * (w_u * T::kQP + q) + (ln >> 3)];
-          sp_next[T::kQP] = meta[64 * s_half + ln];
-          decode_next();
-          copy_tile(mt1, nt1, e_cur);
-        }
-        const int ck = kt + 2 <= last ? kt + 2 : has_next ? kt + 2 - KT : last;
-        issue_at(ck, static_cast<uint32_t>((rs == 0 ? 2 : rs - 1) * kStage));
-        if constexpr (decltype(epi)::value) gate_up_epilogue(mt_prev, n0_prev);
-        if (kt == 0) zero_acc();
-        read_stage(rs);
-        if constexpr (kG0) {
-          wait_vmcnt_lds<2 * T::kPieces + kSt>();  // own reads done (copies may be in flight)
-          __syncthreads();
-          __builtin_amdgcn_sched_barrier(0);
-          __builtin_amdgcn_s_setprio(1);
-          mma_stage();
-          __builtin_amdgcn_s_setprio(0);
-          __builtin_amdgcn_sched_barrier(0);
-          wait_vmcnt<T::kPieces + kSt>();  // own pieces of the next stage landed
-          __syncthreads();
-        } else {
-          wait_vmcnt_lds<T::kPieces + kSt>();  // own reads done, own next pieces landed
-          __syncthreads();
-          __builtin_amdgcn_sched_barrier(0);
-          __builtin_amdgcn_s_setprio(1);
-          mma_stage();
-          __builtin_amdgcn_s_setprio(0);
-          __builtin_amdgcn_sched_barrier(0);
-          __syncthreads();
-        }
-        rs = rs == 2 ? 0 : rs + 1;
-      };
-      if (first)
-        stage(0, std::false_type{});
-      else
-        stage(0, std::true_type{});
-      for (int kt = 1; kt < KT; ++kt) stage(kt, std::false_type{});
-      mt_prev = mt;
-      n0_prev = nt * kBN;
-      if (!has_next) break;
-      i = i_next;
-      i_next = min(i_next + walk.stride, walk.tiles);
-    }
-    // the last tile's epilogue: group 0's beside group 1's last MFMAs, then group 1's
-    gate_up_epilogue(mt_prev, n0_prev);
-    if constexpr (kG0) __syncthreads();
+          if (kt == last - 1 && has_next) {
+            const int ln = opaque(lane);
+            e_next = meta[kBM];
+            own_next = meta[64 * wm + ln];
+  #pragma unroll
+            for (int q = 0; q < T::kQP; ++q) sp_next[q] = meta[8 * (w_u * T::kQP + q) + (ln >> 3)];
+            sp_next[T::kQP] = meta[64 * s_half + ln];
+            decode_next();
+            copy_tile(mt1, nt1, e_cur);
+          }
+          const int ck = kt + 2 <= last ? kt + 2 : has_next ? kt + 2 - KT : last;
+          issue_at(ck, static_cast<uint32_t>((rs == 0 ? 2 : rs - 1) * kStage));
+          if constexpr (decltype(epi)::value) gate_up_epilogue(mt_prev, n0_prev);
+          if (kt == 0) zero_acc();
+          read_stage(rs);
+          if constexpr (kG0) {
+            wait_vmcnt_lds<2 * T::kPieces + kSt>();  // own reads done (copies may be in flight)
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+            mma_stage();
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<T::kPieces + kSt>();  // own pieces of the next stage landed
+            __syncthreads();
+          } else {
+            wait_vmcnt_lds<T::kPieces + kSt>();  // own reads done, own next pieces landed
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_setprio(1);
+            mma_stage();
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+          }
+          rs = rs == 2 ? 0 : rs + 1;
+        };
+        if (first)
+          stage(0, std::false_type{});
+        else
+          stage(0, std::true_type{});
+        for (int kt = 1; kt < KT; ++kt) stage(kt, std::false_type{});
+        mt_prev = mt;
+        n0_prev = nt * kBN;
+        if (!has_next) break;
+        i = i_next;
+        i_next = min(i_next + walk.stride, walk.tiles);
+      }
+      // the last tile's epilogue: group 0's beside group 1's last MFMAs, then group 1's
+      gate_up_epilogue(mt_prev, n0_prev);
+      if constexpr (kG0) __syncthreads();
     };
     if (wm == 0)
       run(std::true_type{});
     else
       run(std::false_type{});
   } else {
-  if (i < walk.tiles) {
-    load_next(i);
-    decode_next();
-    if constexpr (kEarlyStart) {
-      int mt, nt;
-      walk.at_dense(i, mt, nt);
-      copy_tile(mt, nt, e_cur);
-      issue(0);
-      issue(min(1, last));
-    }
-  }
-  for (int i_after = walk.tiles; i < walk.tiles; i = i_next, i_next = i_after) {
-    int mt, nt;
-    walk.at_dense(i, mt, nt);
-    const bool has_next = i_next < walk.tiles;
-    const bool claims = dynamic && t == 0 && has_next;  // publishes the tile after next
-    const int m0 = mt * kBM, n0 = nt * kBN;
-    const int64_t e = e_cur;
-    // down: the expert's pairs fill its first rows, padding the rest; rows below row_end are
-    // real (loaded now, used by the epilogue)
-    int row_end = 0;
-    if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
-    live_i0 = live_cur > 0;
-    live_i1 = live_cur > 32;
-    if (has_next) load_next(i_next);
-    if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
-    zero_acc();
-
-    // Ping-pong: the two wavefronts of a SIMD (one per group) alternate between reading a
-    // stage's operands from LDS and running its 16 MFMAs, half a stage apart, so one of them
-    // always feeds the MFMA pipe while the other's reads proceed. All wavefronts meet at a
-    // barrier every half stage; group 1 starts one barrier late and group 0 ends one
-    // barrier later, so both execute 2 KT + 1 barriers per tile. The CU's vector-memory path
-    // takes ~64 B/clk, so the copies are split between the groups, which keeps each read
-    // phase shorter than the other group's MFMA phase. Each group copies its pieces of stage
-    // kt+2 when it starts reading stage kt (copies issued between MFMAs delay them); the target
-    // slot's previous stage was read by both groups before the barrier that started the phase.
-    // Copies are clamped to the last stage (a clamped copy rewrites a slot with its own
-    // bytes). Both groups wait for their own pieces of stage kt+1 in the phase before the
-    // barrier after which group 0 reads stage kt+1: group 0 after its MFMAs of stage kt,
-    // group 1 after its reads of stage kt.
-    // epilogue stores of the previous tile may still be in flight (with kEarlyStart they were
-    // issued after this tile's first copies): they only make the counted waits stricter
-    // (vmcnt counts stores too; loads complete in order among themselves), never early
-    if constexpr (!kEarlyStart) {
-      issue(0);
-      issue(min(1, last));
-    }
-    wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
-    __syncthreads();
-    if (wm == 0) {
-      for (int kt = 0; kt < KT; ++kt) {
-        // the claim rides on the last stage, whose end waits for every copy anyway
-        if (claims && kt == last) ticket = walk.claim_ticket();
-        issue(min(kt + 2, last));
-        read_stage(kt % kStages);
-        wait_vmcnt_lds<2 * T::kPieces>();  // own reads done (copies may be in flight)
-        __syncthreads();
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(1);
-        mma_stage();
-        __builtin_amdgcn_s_setprio(0);
-        __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<T::kPieces>();  // own pieces of stage kt+1 landed
-        __syncthreads();
-      }
-      __syncthreads();
-    } else {
-      __syncthreads();
-      for (int kt = 0; kt < KT; ++kt) {
-        issue(min(kt + 2, last));
-        read_stage(kt % kStages);
-        wait_vmcnt_lds<T::kPieces>();  // own reads done, own pieces of stage kt+1 landed
-        __syncthreads();
-        __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_setprio(1);
-        mma_stage();
-        __builtin_amdgcn_s_setprio(0);
-        __builtin_amdgcn_sched_barrier(0);
-        __syncthreads();
-      }
-    }
-    wait_vmcnt<0>();  // every copy of this tile landed
-    if (claims) claimed[0] = walk.resolve(ticket);
-    __syncthreads();  // and every wavefront is done reading the stages
-    if (has_next) {
-      i_after = dynamic ? __builtin_amdgcn_readfirstlane(claimed[0])
-                        : min(i_next + walk.stride, walk.tiles);
+    if (i < walk.tiles) {
+      load_next(i);
       decode_next();
       if constexpr (kEarlyStart) {
-        int mt2, nt2;
-        walk.at_dense(i_next, mt2, nt2);
-        copy_tile(mt2, nt2, e_cur);
+        int mt, nt;
+        walk.at_dense(i, mt, nt);
+        copy_tile(mt, nt, e_cur);
         issue(0);
         issue(min(1, last));
       }
     }
+    for (int i_after = walk.tiles; i < walk.tiles; i = i_next, i_next = i_after) {
+      int mt, nt;
+      walk.at_dense(i, mt, nt);
+      const bool has_next = i_next < walk.tiles;
+      const bool claims = dynamic && t == 0 && has_next;  // publishes the tile after next
+      const int m0 = mt * kBM, n0 = nt * kBN;
+      const int64_t e = e_cur;
+      // down: the expert's pairs fill its first rows, padding the rest; rows below row_end are
+      // real (loaded now, used by the epilogue)
+      int row_end = 0;
+      if constexpr (MODE == kDown) row_end = p.padded_offsets[e] + p.counts[e];
+      live_i0 = live_cur > 0;
+      live_i1 = live_cur > 32;
+      if (has_next) load_next(i_next);
+      if constexpr (!kEarlyStart) copy_tile(mt, nt, e);
+      zero_acc();
 
-    if constexpr (MODE != kDown) {
-      gate_up_epilogue(mt, n0);
-    } else {
-      // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
-      // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
-      // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile; one exchange with the other
-      // lane half per pair of chunks gives lane half lk whole 16-byte chunks q4 = lk and
-      // 2 + lk, written with one 16-byte LDS write each. Rows [0, nvalid) of this tile are
-      // real. The stores are non-temporal: y (np x H bf16) is read once, by the finalize, and
-      // does not fit in L2 anyway.
-      const int nvalid = min(kBM, row_end - m0);
-      auto y_chunk = [](int r, int c) { return (r * T::kYChunks + (c ^ (r & 15))) * 16; };
-      static_for<2>([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
-        const int row = wm * 64 + i * 32 + lr;
-        static_for<4>([&](auto jc) {
-          constexpr int j = decltype(jc)::value;
-          uint32_t h[4][2];  // the lane's 4 columns of chunk q4, as two bf16 pairs
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4) {
-            h[q4][0] = pk_bf16(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1]);
-            h[q4][1] = pk_bf16(acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
-          }
-#pragma unroll
-          for (int pr = 0; pr < 2; ++pr) {  // chunks 2 pr (lane half 0) and 2 pr + 1 (half 1)
-            // v_permlane32_swap trades the first operand of lanes 32-63 for the second operand
-            // of lanes 0-31: afterwards lane half 0 holds its own columns of chunk 2 pr and its
-            // partner's, lane half 1 its partner's columns of chunk 2 pr + 1 and its own, both
-            // in column order, with no select
-            const auto d0 = __builtin_amdgcn_permlane32_swap(h[2 * pr][0], h[2 * pr + 1][0], false, false);
-            const auto d1 = __builtin_amdgcn_permlane32_swap(h[2 * pr][1], h[2 * pr + 1][1], false, false);
-            const v4i chunk = {static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
-                               static_cast<int>(d1[1])};
-            *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 128 + j * 32) / 8 + 2 * pr + lk)) = chunk;
-          }
-        });
-      });
-      __syncthreads();
-#pragma unroll 4
-      for (int q = 0; q < kBM * T::kYChunks / T::kThreads; ++q) {
-        const int idx = q * T::kThreads + t;
-        const int row = idx / T::kYChunks, c = idx % T::kYChunks;
-        if (row < nvalid)
-          __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
-                                      reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
+      // Ping-pong: the two wavefronts of a SIMD (one per group) alternate between reading a
+      // stage's operands from LDS and running its 16 MFMAs, half a stage apart, so one of them
+      // always feeds the MFMA pipe while the other's reads proceed. All wavefronts meet at a
+      // barrier every half stage; group 1 starts one barrier late and group 0 ends one
+      // barrier later, so both execute 2 KT + 1 barriers per tile. The CU's vector-memory path
+      // takes ~64 B/clk, so the copies are split between the groups, which keeps each read
+      // phase shorter than the other group's MFMA phase. Each group copies its pieces of stage
+      // kt+2 when it starts reading stage kt (copies issued between MFMAs delay them); the target
+      // slot's previous stage was read by both groups before the barrier that started the phase.
+      // Copies are clamped to the last stage (a clamped copy rewrites a slot with its own
+      // bytes). Both groups wait for their own pieces of stage kt+1 in the phase before the
+      // barrier after which group 0 reads stage kt+1: group 0 after its MFMAs of stage kt,
+      // group 1 after its reads of stage kt.
+      // epilogue stores of the previous tile may still be in flight (with kEarlyStart they were
+      // issued after this tile's first copies): they only make the counted waits stricter
+      // (vmcnt counts stores too; loads complete in order among themselves), never early
+      if constexpr (!kEarlyStart) {
+        issue(0);
+        issue(min(1, last));
       }
+      wait_vmcnt<T::kPieces>();  // own pieces of stage 0 landed
       __syncthreads();
+      if (wm == 0) {
+        for (int kt = 0; kt < KT; ++kt) {
+          // the claim rides on the last stage, whose end waits for every copy anyway
+          if (claims && kt == last) ticket = walk.claim_ticket();
+          issue(min(kt + 2, last));
+          read_stage(kt % kStages);
+          wait_vmcnt_lds<2 * T::kPieces>();  // own reads done (copies may be in flight)
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_setprio(1);
+          mma_stage();
+          __builtin_amdgcn_s_setprio(0);
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vmcnt<T::kPieces>();  // own pieces of stage kt+1 landed
+          __syncthreads();
+        }
+        __syncthreads();
+      } else {
+        __syncthreads();
+        for (int kt = 0; kt < KT; ++kt) {
+          issue(min(kt + 2, last));
+          read_stage(kt % kStages);
+          wait_vmcnt_lds<T::kPieces>();  // own reads done, own pieces of stage kt+1 landed
+          __syncthreads();
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_setprio(1);
+          mma_stage();
+          __builtin_amdgcn_s_setprio(0);
+          __builtin_amdgcn_sched_barrier(0);
+          __syncthreads();
+        }
+      }
+      wait_vmcnt<0>();  // every copy of this tile landed
+      if (claims) claimed[0] = walk.resolve(ticket);
+      __syncthreads();  // and every wavefront is done reading the stages
+      if (has_next) {
+        i_after = dynamic ? __builtin_amdgcn_readfirstlane(claimed[0])
+                          : min(i_next + walk.stride, walk.tiles);
+        decode_next();
+        if constexpr (kEarlyStart) {
+          int mt2, nt2;
+          walk.at_dense(i_next, mt2, nt2);
+          copy_tile(mt2, nt2, e_cur);
+          issue(0);
+          issue(min(1, last));
+        }
+      }
+
+      if constexpr (MODE != kDown) {
+        gate_up_epilogue(mt, n0);
+      } else {
+        // bf16 rows through LDS, so the stores write whole rows (a lane holds one row and only
+        // 16-byte pieces of it: stored directly, the down GEMM ran ~4% slower). Lane half lk
+        // holds columns 8 q4 + 4 lk .. + 3 of each 32-column tile; one exchange with the other
+        // lane half per pair of chunks gives lane half lk whole 16-byte chunks q4 = lk and
+        // 2 + lk, written with one 16-byte LDS write each. Rows [0, nvalid) of this tile are
+        // real. The stores are non-temporal: y (np x H bf16) is read once, by the finalize, and
+        // does not fit in L2 anyway.
+        const int nvalid = min(kBM, row_end - m0);
+        auto y_chunk = [](int r, int c) { return (r * T::kYChunks + (c ^ (r & 15))) * 16; };
+        static_for<2>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          const int row = wm * 64 + i * 32 + lr;
+          static_for<4>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
+            uint32_t h[4][2];  // the lane's 4 columns of chunk q4, as two bf16 pairs
+  #pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+              h[q4][0] = pk_bf16(acc[i][j][4 * q4], acc[i][j][4 * q4 + 1]);
+              h[q4][1] = pk_bf16(acc[i][j][4 * q4 + 2], acc[i][j][4 * q4 + 3]);
+            }
+  #pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {  // chunks 2 pr (lane half 0) and 2 pr + 1 (half 1)
+              // v_permlane32_swap trades the first operand of lanes 32-63 for the second operand
+              // of lanes 0-31: afterwards lane half 0 holds its own columns of chunk 2 pr and its
+              // partner's, lane half 1 its partner's columns of chunk 2 pr + 1 and its own, both
+              // in column order, with no select
+              const auto d0 = __builtin_amdgcn_permlane32_swap(h[2 * pr][0], h[2 * pr + 1][0], false, false);
+              const auto d1 = __builtin_amdgcn_permlane32_swap(h[2 * pr][1], h[2 * pr + 1][1], false, false);
+              const v4i chunk = {static_cast<int>(d0[0]), static_cast<int>(d1[0]), static_cast<int>(d0[1]),
+                                 static_cast<int>(d1[1])};
+              *reinterpret_cast<v4i*>(lds + y_chunk(row, (wn * 128 + j * 32) / 8 + 2 * pr + lk)) = chunk;
+            }
+          });
+        });
+        __syncthreads();
+  #pragma unroll 4
+        for (int q = 0; q < kBM * T::kYChunks / T::kThreads; ++q) {
+          const int idx = q * T::kThreads + t;
+          const int row = idx / T::kYChunks, c = idx % T::kYChunks;
+          if (row < nvalid)
+            __builtin_nontemporal_store(*reinterpret_cast<const v4i*>(lds + y_chunk(row, c)),
+                                        reinterpret_cast<v4i*>(p.y + int64_t(m0 + row) * p.N + n0 + c * 8));
+        }
+        __syncthreads();
+      }
     }
-  }
   }
 }
 
