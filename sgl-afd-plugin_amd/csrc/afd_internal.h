@@ -81,13 +81,19 @@ __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   return j;
 }
 
-// Counter words of one call, in the workspace's num_tiles slot (padded to 256 bytes; num_tiles
-// is word 0): the routing launch zeroes words [kCounterWord0, kCounterWord0 + kCounterWords)
-// before any later launch of the call uses them.
+// Counter words of one call, in the workspace's num_tiles slot (num_tiles is word 0): the
+// routing launch zeroes words [kCounterWord0, kCounterWord0 + kCounterWords) and the
+// kArriveGroups group counters before any later launch of the call uses them.
 constexpr int kCounterWord0 = 8, kCounterWords = 32;
 constexpr int kGateUpWalkWord = 8;  // the gate_up GEMM's tile counters, one per XCD
 constexpr int kDownWalkWord = 16;   // the down GEMM's
-constexpr int kArriveWord = 32;     // the reply's arrive counter
+constexpr int kArriveWord = 32;     // the reply's arrive counter (one count per group)
+// The reply's group counters: a finishing workgroup counts itself in its group's counter, and
+// the last of a group in kArriveWord. Returning atomics on one address serialize (~10 ns
+// each, 10 us for the 1024 workgroups of a reply); each group counter has a 256-byte line
+// of its own.
+constexpr int kArriveGroups = 32, kArriveGroupWord0 = 64, kArriveGroupStride = 64;
+constexpr int kCallCounterBytes = (kArriveGroupWord0 + kArriveGroups * kArriveGroupStride) * 4;
 inline uint32_t* call_counters(uint8_t* ws, const afd_ws_layout& L) {
   return reinterpret_cast<uint32_t*>(ws + L.num_tiles);
 }
@@ -100,7 +106,7 @@ struct Reply {
   uint64_t* done[kMaxBatch];
   uint64_t value[kMaxBatch];
   int32_t count;
-  uint32_t* arrive;
+  uint32_t* arrive;  // kArriveWord of the call's counters; the group counters follow it
 };
 
 // Activation quantization as the expert call applies it (MXFP8 with stage-order scales, or

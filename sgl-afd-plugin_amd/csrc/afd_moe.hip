@@ -111,10 +111,10 @@ __device__ __forceinline__ void finalize_item(const uint16_t* __restrict__ y,
 // Workgroups stride over the job's (token, column block) items (one item each when the grid
 // covers them; with a descriptor, items past the job's tokens are skipped). With a reply, the
 // grid is a few workgroups per CU; their output stores write through to memory, and each
-// workgroup, once all its stores are acknowledged, counts itself in reply.arrive (one atomic
-// per workgroup, no cache write-back); the last to arrive stores the reply value (system
-// scope), so a stream waiting on *reply.done (host memory) runs after every output row is in
-// memory.
+// workgroup, once all its stores are acknowledged, counts itself in its group's counter (one
+// atomic per workgroup, no cache write-back), the last of each group counts the group in
+// reply.arrive, and the last group's stores the reply value (system scope), so a stream
+// waiting on *reply.done (host memory) runs after every output row is in memory.
 template <bool kReply>
 __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
     const uint16_t* __restrict__ y, const int32_t* __restrict__ pair_pos, JobIn jin, int k,
@@ -131,9 +131,15 @@ __global__ __launch_bounds__(kFinThreads) void finalize_kernel(
   if constexpr (kReply) {
     wait_vmcnt<0>();  // this lane's output stores are acknowledged (written through)
     __syncthreads();  // and every lane's of the workgroup
+    // workgroup b counts itself in group b % groups; the last of a group counts the group in
+    // the call's arrive word, and the last group stores the reply
+    const uint32_t groups = gridDim.x < kArriveGroups ? gridDim.x : kArriveGroups;
+    const uint32_t g = blockIdx.x % groups, size = (gridDim.x - g + groups - 1) / groups;
+    uint32_t* group = reply.arrive + (kArriveGroupWord0 - kArriveWord) + g * kArriveGroupStride;
     if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == size - 1 &&
         __hip_atomic_fetch_add(reply.arrive, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            gridDim.x - 1) {
+            groups - 1) {
 #pragma unroll
       for (int b = 0; b < kMaxBatch; ++b)
         if (b < reply.count && reply.done[b] != nullptr)
@@ -320,7 +326,7 @@ extern "C" int afd_workspace_layout(const afd_moe_cfg* cfg, int32_t n, afd_ws_la
   L.sorted_pairs = take(uint64_t(np_max) * 4);
   L.pair_pos = take(uint64_t(pairs) * 4);
   L.tile_expert = take(max_tiles * 4);
-  L.num_tiles = take(4);
+  L.num_tiles = take(kCallCounterBytes);  // num_tiles, then the call's counters
   L.hist = take(uint64_t(128) * E * 4);
   L.hq = take(a16  ? max_tiles * (I / kImgK) * kImgA16
                : mx ? max_tiles * (I / kImgK) * kImgA + kImgReadSlack

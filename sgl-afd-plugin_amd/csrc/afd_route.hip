@@ -45,6 +45,8 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
     int32_t* __restrict__ hist, PrepQuant pq, uint32_t* __restrict__ counters) {
   const JobIn job = resolve_job(jin);
   if (blockIdx.x == 0 && threadIdx.x < kCounterWords) counters[kCounterWord0 + threadIdx.x] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x < kArriveGroups)
+    counters[kArriveGroupWord0 + threadIdx.x * kArriveGroupStride] = 0u;
   if (static_cast<int>(blockIdx.x) >= chunks) {
     const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
     const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;
