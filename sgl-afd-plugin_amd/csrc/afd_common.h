@@ -207,6 +207,8 @@ __device__ __forceinline__ uint32_t div_by_magic(uint32_t n, uint32_t magic) {
 // tiles instead of adding a whole round at the end. Everything but the claim itself is host
 // code too, so the walk's coverage is checked on the CPU (tests/walk_model.cpp).
 constexpr int kWalkSplitRows = 32;
+// the dynamic walk's 8 counters (one per XCD) are this many words apart
+constexpr int kWalkCounterStride = 64;
 
 template <int BR>
 struct TileWalk {
@@ -215,8 +217,8 @@ struct TileWalk {
   int mt0, rows_here, ntn, first, stride;
   int tiles;  // rows_here * ntn: the dense positions of at_dense
   uint32_t* ctr;
-  // block / grid: this workgroup's index and the grid size; counters: 8 zeroed words for the
-  // dynamic walk (one per XCD)
+  // block / grid: this workgroup's index and the grid size; counters: for the dynamic walk, 8
+  // zeroed words kWalkCounterStride apart (one per XCD)
   __host__ __device__ __forceinline__ TileWalk(int rows, int ntn_, int block, int grid,
                                                uint32_t* counters = nullptr) {
     ntn = ntn_;
@@ -231,7 +233,7 @@ struct TileWalk {
       rows_here = ((rows * (xcd + 1)) >> 3) - mt0;
       first = block >> 3;
       stride = grid >> 3;
-      if (counters != nullptr) ctr = counters + xcd;
+      if (counters != nullptr) ctr = counters + xcd * kWalkCounterStride;
     }
     tiles = rows_here * ntn;
   }

@@ -81,19 +81,19 @@ __device__ __forceinline__ JobIn resolve_job(JobIn j) {
   return j;
 }
 
-// Counter words of one call, in the workspace's num_tiles slot (num_tiles is word 0): the
-// routing launch zeroes words [kCounterWord0, kCounterWord0 + kCounterWords) and the
-// kArriveGroups group counters before any later launch of the call uses them.
-constexpr int kCounterWord0 = 8, kCounterWords = 32;
-constexpr int kGateUpWalkWord = 8;  // the gate_up GEMM's tile counters, one per XCD
-constexpr int kDownWalkWord = 16;   // the down GEMM's
-constexpr int kArriveWord = 32;     // the reply's arrive counter (one count per group)
-// The reply's group counters: a finishing workgroup counts itself in its group's counter, and
-// the last of a group in kArriveWord. Returning atomics on one address serialize (~10 ns
-// each, 10 us for the 1024 workgroups of a reply); each group counter has a 256-byte line
-// of its own.
-constexpr int kArriveGroups = 32, kArriveGroupWord0 = 64, kArriveGroupStride = 64;
-constexpr int kCallCounterBytes = (kArriveGroupWord0 + kArriveGroups * kArriveGroupStride) * 4;
+// Counter words of one call, in the workspace's num_tiles slot (num_tiles is word 0). Returning
+// atomics on one cache line serialize (~10 ns each), so the counters that many workgroups hit
+// at once each have a 256-byte line of their own: line l (l < kCounterLines) starts at word
+// kLineWord0 + l * kLineStride and holds, in its words 0 / 1 / 2, the reply's group counter l,
+// the gate_up GEMM's tile counter of XCD l and the down GEMM's (l < 8). The routing launch
+// zeroes those words and kArriveWord before any later launch of the call uses them.
+constexpr int kArriveWord = 32;  // the reply's arrive counter (one count per group)
+constexpr int kLineWord0 = 64, kLineStride = 64, kCounterLines = 32;
+constexpr int kArriveGroups = kCounterLines, kArriveGroupWord0 = kLineWord0, kArriveGroupStride = kLineStride;
+constexpr int kGateUpWalkWord = kLineWord0 + 1;  // TileWalk: XCD x's counter x * kWalkCounterStride later
+constexpr int kDownWalkWord = kLineWord0 + 2;
+static_assert(kWalkCounterStride == kLineStride, "one line per XCD's tile counter");
+constexpr int kCallCounterBytes = (kLineWord0 + kCounterLines * kLineStride) * 4;
 inline uint32_t* call_counters(uint8_t* ws, const afd_ws_layout& L) {
   return reinterpret_cast<uint32_t*>(ws + L.num_tiles);
 }

@@ -44,9 +44,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_prep_kernel(
     JobIn jin, int topk, int chunk, int chunks, int e_lo, int num_local,
     int32_t* __restrict__ hist, PrepQuant pq, uint32_t* __restrict__ counters) {
   const JobIn job = resolve_job(jin);
-  if (blockIdx.x == 0 && threadIdx.x < kCounterWords) counters[kCounterWord0 + threadIdx.x] = 0u;
-  if (blockIdx.x == 0 && threadIdx.x < kArriveGroups)
-    counters[kArriveGroupWord0 + threadIdx.x * kArriveGroupStride] = 0u;
+  if (blockIdx.x == 0 && threadIdx.x < kCounterLines) {
+    uint32_t* line = counters + kLineWord0 + threadIdx.x * kLineStride;
+    line[0] = line[1] = line[2] = 0u;
+    if (threadIdx.x == 0) counters[kArriveWord] = 0u;
+  }
   if (static_cast<int>(blockIdx.x) >= chunks) {
     const int64_t first = (int64_t(blockIdx.x) - chunks) * kRouteThreads + threadIdx.x;
     const int64_t stride = (int64_t(gridDim.x) - chunks) * kRouteThreads;

@@ -60,7 +60,7 @@ static bool static_walk(int rows, int ntn, int grid) {
 template <int BR>
 static bool dynamic_walk(int rows, int ntn, int grid, std::mt19937& rng) {
   std::vector<int> hits(rows * ntn, 0);
-  uint32_t counters[8] = {};
+  std::vector<uint32_t> counters(8 * afd::kWalkCounterStride, 0u);
   struct Wg {
     TileWalk<BR> w;
     int i, i_next;
@@ -68,7 +68,7 @@ static bool dynamic_walk(int rows, int ntn, int grid, std::mt19937& rng) {
   };
   std::vector<Wg> wgs;
   for (int b = 0; b < grid; ++b) {
-    TileWalk<BR> w(rows, ntn, b, grid, counters);
+    TileWalk<BR> w(rows, ntn, b, grid, counters.data());
     wgs.push_back({w, 0, 0, false, false});
   }
   // one step of a workgroup = one claim (a counter increment), in random order
