@@ -17,9 +17,8 @@
 //
 // The workgroups are persistent: grid = resident workgroups, and the number of row tiles is
 // read from device memory (the router wrote it), so no host round trip is needed. They walk
-// the tiles XCD by XCD in blocks of 4 row tiles x 8 column tiles (TileWalk; with 8 column
-// tiles, row tile by row tile), so the workgroups of an XCD share activation rows and weight
-// slices in their L2.
+// the tiles XCD by XCD in blocks of 2 row tiles x 16 column tiles (TileWalk), so the
+// workgroups of an XCD share activation rows and weight slices in their L2.
 #include <type_traits>
 
 #include "afd_common.h"
@@ -32,9 +31,12 @@ namespace afd {
 // down
 enum { kGateUp = 0, kDown = 1, kGateUpParam = 2 };
 
-// Tile walk blocks of 4 row tiles x 8 column tiles: a row tile's gathered activation rows are
-// shared 8 ways (measured faster than 8 x 4 blocks, whose lower HBM traffic does not pay).
-constexpr int kMxWalkRows = 4;
+// Tile walk blocks of 2 row tiles x 16 column tiles (all 8 of a 4096-wide GEMM): a row tile's
+// gathered activation rows are shared by all its column tiles, each XCD's 32 workgroups run
+// 2 such blocks at a time (measured ~1% faster than 4 x 8 blocks on the DeepSeek-V4 F-rank
+// layer, the job stream and the loop even; 8 x 4 blocks, whose lower HBM traffic does not
+// pay, no faster than 4 x 8).
+constexpr int kMxWalkRows = 2;
 
 struct MxGemmArgs {
   const uint8_t* a_img;         // down: A images [row tiles][K/128]

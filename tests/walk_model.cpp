@@ -115,10 +115,12 @@ static int run(std::mt19937& rng) {
 
 int main() {
   std::mt19937 rng(12345);
-  const int a = run<4>(rng);  // the MXFP4 GEMMs' 4 x 8 blocks
+  const int a = run<2>(rng);  // the MXFP4 GEMMs' 2 x 16 blocks
   if (a < 0) return 1;
+  const int c = run<4>(rng);  // the bf16-activation GEMMs' 4 x 8 blocks
+  if (c < 0) return 1;
   const int b = run<8>(rng);  // the FP8 GEMMs' 8 x 4 blocks
   if (b < 0) return 1;
-  std::printf("ok: %d walks, every tile taken exactly once\n", a + b);
+  std::printf("ok: %d walks, every tile taken exactly once\n", a + b + c);
   return 0;
 }
