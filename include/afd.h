@@ -127,8 +127,8 @@ enum afd_tile_walk {
 
 /* Shape of one MoE layer on one F rank. Experts [expert_lo, expert_lo + num_local) are
  * local; top-k ids are global expert ids; pairs with other ids are skipped.
- * Limits: hidden a multiple of 256, inter a multiple of 128, num_local <= 256,
- * topk <= 32, n <= 131071. */
+ * Limits: hidden a multiple of 256 up to 16384, inter a multiple of 128 up to 16384,
+ * num_local <= 256, topk <= 32, n <= 131071. */
 typedef struct afd_moe_cfg {
   int32_t hidden;
   int32_t inter;
@@ -379,7 +379,7 @@ int afd_combine(const uint16_t* const* parts, int32_t num_parts, const uint16_t*
  * calls at P/srt/batch_overlap/operations_strategy.py:94, 255): gate_up bf16 [n][2 inter]
  * (gate columns first, then up) -> out bf16 [n][inter], out = bf16(silu(g) * u) computed in
  * float with one rounding, silu(g) = g / (1 + e^-g). inter a multiple of 8, both pointers
- * 16-byte aligned, n * inter / 8 < 2^32. */
+ * 16-byte aligned, n * inter / 8 < 2^31. */
 int afd_silu_mul(const uint16_t* gate_up, int64_t n, int32_t inter, uint16_t* out,
                  afd_stream_t stream);
 

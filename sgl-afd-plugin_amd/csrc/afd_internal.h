@@ -10,6 +10,9 @@ namespace afd {
 
 constexpr int kMaxLocalExperts = 256;
 constexpr int kMaxTopk = 32;
+// Widest hidden and intermediate sizes: the GEMMs gather activation rows with 32-bit offsets
+// (token x row bytes, bf16 rows of up to 16384 values for up to 131071 tokens: < 2^32)
+constexpr int kMaxHidden = 16384, kMaxInter = 16384;
 constexpr int kBlockM = 128;  // row tile of the grouped GEMMs; expert segments pad to it
 constexpr int kFp8BlockM = 256;  // the same for FP8 block weights with fp8 activations (W8A8)
 // the row tile (segment padding) of a configuration's GEMMs

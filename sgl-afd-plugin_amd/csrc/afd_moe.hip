@@ -256,7 +256,8 @@ static int check_cfg(const afd_moe_cfg* cfg) {
   if (cfg->topk < 1 || cfg->topk > kMaxTopk || cfg->num_local < 1 ||
       cfg->num_local > kMaxLocalExperts || cfg->expert_lo < 0)
     return AFD_ERR_ARG;
-  if (cfg->hidden <= 0 || cfg->inter <= 0 || cfg->hidden % 256 || cfg->inter % 128)
+  if (cfg->hidden <= 0 || cfg->inter <= 0 || cfg->hidden % 256 || cfg->inter % 128 ||
+      cfg->hidden > kMaxHidden || cfg->inter > kMaxInter)
     return AFD_ERR_SHAPE;
   if (cfg->weight_fmt != AFD_W_MXFP4 && cfg->weight_fmt != AFD_W_FP8_BLOCK)
     return AFD_ERR_UNSUPPORTED;
@@ -633,8 +634,9 @@ extern "C" int afd_silu_mul(const uint16_t* gate_up, int64_t n, int32_t inter, u
   if (!gate_up || !out) return AFD_ERR_ARG;
   if (inter % 8 || reinterpret_cast<uintptr_t>(gate_up) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
     return AFD_ERR_SHAPE;
+  // the kernel's 32-bit vector index must not wrap when it steps past the end
   const int64_t vecs = n * (inter / 8);
-  if (vecs > 0xffffffffll) return AFD_ERR_SHAPE;
+  if (vecs > 0x7fffffffll) return AFD_ERR_SHAPE;
   int64_t grid = (vecs + 255) / 256;
   if (grid > int64_t(8) * device_cu_count()) grid = int64_t(8) * device_cu_count();
   hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<unsigned>(grid)), dim3(256), 0,

@@ -115,6 +115,7 @@ def test_silu_mul_argument_checks():
     assert L.afd_silu_mul(16, 4, 1540, 16, None) == _lib.AFD_ERR_SHAPE  # inter not a multiple of 8
     assert L.afd_silu_mul(8, 4, 1536, 16, None) == _lib.AFD_ERR_SHAPE  # misaligned rows
     assert L.afd_silu_mul(16, 1 << 30, 64, 16, None) == _lib.AFD_ERR_SHAPE  # 2^33 vectors
+    assert L.afd_silu_mul(16, 1 << 28, 64, 16, None) == _lib.AFD_ERR_SHAPE  # 2^31 vectors
 
 
 def test_python_activation_formats():
@@ -138,6 +139,8 @@ def test_bad_configs_rejected_on_host():
     bad = [
         _lib.AfdMoeCfg(4000, 2048, 8, 0, 64, 1),  # hidden not a multiple of 256
         _lib.AfdMoeCfg(4096, 2000, 8, 0, 64, 1),  # inter not a multiple of 128
+        _lib.AfdMoeCfg(16640, 2048, 8, 0, 64, 1),  # hidden above 16384
+        _lib.AfdMoeCfg(4096, 16512, 8, 0, 64, 1),  # inter above 16384
         _lib.AfdMoeCfg(4096, 2048, 0, 0, 64, 1),  # topk 0
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 512, 1),  # too many local experts
         _lib.AfdMoeCfg(4096, 2048, 8, 0, 64, 7),  # unknown format
@@ -149,6 +152,8 @@ def test_bad_configs_rejected_on_host():
     ]
     for cfg in bad:
         assert _lib.lib().afd_workspace_layout(ctypes.byref(cfg), 16, ctypes.byref(out)) != 0
+    widest = _lib.AfdMoeCfg(16384, 16384, 8, 0, 8, 1)
+    assert _lib.lib().afd_workspace_layout(ctypes.byref(widest), 16, ctypes.byref(out)) == 0
     good = _lib.AfdMoeCfg(256, 128, 2, 0, 8, 1)
     assert _lib.lib().afd_workspace_layout(ctypes.byref(good), 1 << 17, ctypes.byref(out)) != 0
     assert _lib.lib().afd_workspace_layout(ctypes.byref(good), (1 << 17) - 1, ctypes.byref(out)) == 0
