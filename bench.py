@@ -9,7 +9,10 @@ inputs and packed weights resident in HBM.
 Prints one JSON line: value = algorithmic TFLOPS (6 * H * I * Np per step, Np counted from
 the generated ids), plus tokens/s, per-layer latency, per-stage times from HIP events on the
 launch stream, the roofline of the dominant kernel (the gate_up GEMM) and the CPU baseline
-(the fp32 CPU oracle on a bounded sample of the same workload).
+(the fp32 CPU oracle on a bounded sample of the same workload). The default invocation also
+runs the other workloads (the FP8-block layer, the one-GPU loop, the skewed job stream) as
+child processes after its own timed steps and reports their headline numbers under
+"other_workloads".
 """
 
 from __future__ import annotations
@@ -19,6 +22,7 @@ import ctypes
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -68,7 +72,49 @@ def parse():
     ap.add_argument("--stats-summary", metavar="KERNEL_STATS_CSV",
                     help="no GPU: print a rocprofv3 --stats kernel_stats.csv as a markdown table")
     ap.add_argument("--traffic-out", default=None)
+    ap.add_argument("--others", default="auto", choices=["auto", "0", "1"],
+                    help="layer: after the timed steps, run the other workloads (FP8-block layer, "
+                    "loop, job stream) as child processes and report their numbers; auto = only "
+                    "for the default report (the MXFP4 layer with the CPU baseline)")
     return ap.parse_args()
+
+
+# the other workloads of the default report: name, bench.py flags, fields kept from its line
+OTHER_WORKLOADS = (
+    ("ernie_fp8_layer", ["--config", "ernie_fp8", "--cpu-baseline", "0", "--others", "0"],
+     lambda d: {"tflops": d["value"], "ms_per_step": d["ms_per_step"], "stages_ms": d["stages_ms"],
+                "gate_up_tflops": d["roofline"]["achieved"], "gate_up_frac_fp8": d["roofline"]["frac"]}),
+    ("loop", ["--workload", "loop"],
+     lambda d: {"layer_latency_ms": d["layer_latency_ms"], "layer_latency_ms_min": d["layer_latency_ms_min"],
+                "chained_ms_per_layer": d["chained_ms_per_layer"],
+                "tflops_routed_plus_shared": d["tflops_routed_plus_shared"]}),
+    ("stream", ["--workload", "stream"],
+     lambda d: {"batched_tflops": d["value"], "batched_ms": d["batched"]["ms"], "eager_ms": d["eager"]["ms"],
+                "graphs_ms": d["graphs"]["ms"],
+                "small_jobs": [{k: j[k] for k in ("tokens", "ms", "hbm_gbps")} for j in d["small_jobs"]]}),
+)
+
+
+def run_others() -> dict:
+    """Each other workload in a child process of its own (its own warm-up, timing and memory),
+    one after the other; a failed child is reported, not raised."""
+    out = {"note": "each workload run as `python bench.py <flags>` in a child process after this "
+                   "line's timed steps, with its own warm-up and timing"}
+    for name, flags, keep in OTHER_WORKLOADS:
+        t0 = time.monotonic()
+        try:
+            r = subprocess.run([sys.executable, os.path.abspath(__file__)] + flags, capture_output=True,
+                               text=True, timeout=600, cwd=ROOT)
+            lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+            if r.returncode != 0 or not lines:
+                out[name] = {"flags": flags, "error": f"exit {r.returncode}", "stderr_tail": r.stderr[-400:]}
+            else:
+                out[name] = {"flags": flags, **keep(json.loads(lines[-1]))}
+        except subprocess.TimeoutExpired:
+            out[name] = {"flags": flags, "error": "timed out after 600 s"}
+        out[name]["wall_s"] = round(time.monotonic() - t0, 1)
+        print(f"[bench] {name}: {out[name]}", file=sys.stderr, flush=True)
+    return out
 
 
 TRAFFIC_DIR = os.path.join(ROOT, "profiles")
@@ -750,6 +796,13 @@ def main():
     if args.cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(shape, min(args.cpu_sample_tokens, n), min(args.cpu_sample_experts, shape.num_local),
                                               experts.act_format)
+    default_report = (args.cpu_baseline and args.config == "dsv4_rank" and args.act is None and args.tokens is None
+                      and not args.copy_calibration)
+    if args.others == "1" or (args.others == "auto" and default_report):
+        del experts, weights, ws, x, out
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        result["other_workloads"] = run_others()
     print(json.dumps(result), flush=True)
 
 
