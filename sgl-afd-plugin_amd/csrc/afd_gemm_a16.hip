@@ -69,7 +69,7 @@ struct A16GemmArgs {
   const int32_t* num_tiles;     // [1]
   const int32_t* padded_offsets;  // [E + 1]
   const int32_t* counts;          // [E]
-  uint32_t* walk_ctr;             // [8] zeroed tile counters; nullptr: static walk
+  uint32_t* walk_ctr;             // zeroed tile counters, XCD x's at x * kWalkCounterStride; nullptr: static walk
   int K, N;
   uint8_t* h_img;  // gate_up out: the down GEMM's bf16 A images [row tiles][N/2 / stage K]
   ActParams act;   // gate_up: the activation

@@ -62,7 +62,7 @@ struct Fp8GemmArgs {
   const int32_t* num_tiles;       // [1]
   const int32_t* padded_offsets;  // [E + 1]
   const int32_t* counts;          // [E]
-  uint32_t* walk_ctr;             // [8] zeroed tile counters (one per XCD); nullptr: static walk
+  uint32_t* walk_ctr;             // zeroed tile counters, XCD x's at x * kWalkCounterStride; nullptr: static walk
   int K, N;
   ActParams act;  // gate_up: the activation
   uint8_t* hq;    // gate_up out: h images [row tiles][N/2/64]

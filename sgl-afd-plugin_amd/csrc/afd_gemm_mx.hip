@@ -51,7 +51,7 @@ struct MxGemmArgs {
   const int32_t* num_tiles;     // [1]
   const int32_t* padded_offsets;  // [E + 1] first padded row of each expert
   const int32_t* counts;          // [E] pairs of each expert (its first rows)
-  uint32_t* walk_ctr;             // [8] zeroed tile counters (one per XCD); nullptr: static walk
+  uint32_t* walk_ctr;             // zeroed tile counters, XCD x's at x * kWalkCounterStride; nullptr: static walk
   int K, N;
   uint8_t* h_img;  // gate_up out: the down GEMM's A images [row tiles][N/256]
   ActParams act;   // gate_up: the activation
