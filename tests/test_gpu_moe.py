@@ -36,10 +36,11 @@ def deq_weights(w13, w2, fmt):
 
 
 def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=None, situ=None,
-             swiglu_limit=None):
+             swiglu_limit=None, walk="static", act_format=None):
     """situ: None for SwiGLU, else SiTU's (gemm1_alpha, gemm1_clamp_limit); swiglu_limit:
-    SwiGLU with that limit (DeepSeek-V4's FusedMoE argument)."""
-    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed} situ={situ} swiglu_limit={swiglu_limit}")
+    SwiGLU with that limit (DeepSeek-V4's FusedMoE argument); walk: the GEMMs' tile walk;
+    act_format: "bf16" for bf16 activations, None for the weight format's fp8 form."""
+    say(f"moe fmt={fmt} H={hidden} I={inter} E={num_experts} local=[{e_lo},{e_lo + num_local}) k={k} n={n} seed={seed} situ={situ} swiglu_limit={swiglu_limit} walk={walk} act_format={act_format}")
     gen = W.generator("cpu", seed)
     x = W.tokens(n, hidden, gen, "cpu")
     if zipf is None:
@@ -53,11 +54,12 @@ def run_case(hidden, inter, num_experts, e_lo, num_local, k, n, fmt, seed, zipf=
     act_kw = {} if situ is None else dict(activation="situ", gemm1_alpha=situ[0], gemm1_clamp_limit=situ[1])
     if swiglu_limit is not None:
         act_kw = dict(swiglu_limit=swiglu_limit)
-    experts = AfdExperts(num_experts, k, 0, local, weights, n_max=max(n, 1), **act_kw)
+    experts = AfdExperts(num_experts, k, 0, local, weights, n_max=max(n, 1), act_format=act_format, **act_kw)
+    experts.tile_walk = walk
     out = experts(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev())))
     torch.cuda.synchronize()
     w13d, w2d = deq_weights(w13, w2, fmt)
-    act = "mxfp8" if fmt == "mxfp4" else "fp8_1x128"
+    act = "bf16" if act_format == "bf16" else "mxfp8" if fmt == "mxfp4" else "fp8_1x128"
     oact = {} if situ is None else dict(activation="situ", act_alpha=situ[0], act_limit=situ[1])
     if swiglu_limit is not None:
         oact = dict(activation="swiglu_limit", act_limit=swiglu_limit)

@@ -1,6 +1,8 @@
 """GPU: seeded random layer shapes against the oracle, across both weight formats and the
 three activations, with token counts at and around the 128-row tile edge (1, 2, 127, 128,
-129, ...), partial local expert ranges and top-k from 1 to 8. Same bars as test_gpu_moe."""
+129, ...), partial local expert ranges and top-k from 1 to 8; and shapes of 2048-4096 tokens
+where every GEMM workgroup takes several tiles, with both tile walks and bf16 activations.
+Same bars as test_gpu_moe."""
 
 import random
 
@@ -44,4 +46,37 @@ def test_random_layer(case):
     experts, out, ref, parts, (x, ids, w) = run_case(
         s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], s["fmt"],
         9000 + case, zipf=s["zipf"], **extra)
+    assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
+
+
+MANY_TILE_CASES = 12
+
+
+def draw_many_tiles(case: int) -> dict:
+    """Shapes where every GEMM workgroup takes several tiles (hidden of 3 K stages and more
+    runs the continuous-ring gate_up), with both tile walks and bf16 activations."""
+    rng = random.Random(8100 + case)
+    num_experts = rng.choice([16, 32, 64])
+    num_local = rng.randint(num_experts // 4, num_experts)
+    return dict(
+        fmt=rng.choice(["mxfp4", "fp8_block"]),
+        hidden=256 * rng.randint(2, 12),
+        inter=128 * rng.randint(2, 8),
+        num_experts=num_experts,
+        num_local=num_local,
+        e_lo=rng.randint(0, num_experts - num_local),
+        k=rng.randint(2, 8),
+        n=rng.choice([2048, 3000, 4096]),
+        zipf=rng.choice([None, 1.2]),
+        walk=rng.choice(["static", "dynamic"]),
+        act_format=rng.choice([None, None, "bf16"]),
+    )
+
+
+@pytest.mark.parametrize("case", range(MANY_TILE_CASES))
+def test_random_layer_many_tiles(case):
+    s = draw_many_tiles(case)
+    experts, out, ref, parts, (x, ids, w) = run_case(
+        s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], s["fmt"],
+        9500 + case, zipf=s["zipf"], walk=s["walk"], act_format=s["act_format"])
     assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
