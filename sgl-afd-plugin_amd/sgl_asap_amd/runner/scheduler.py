@@ -199,8 +199,9 @@ class FfnScheduler:
         return sizes
 
     def rows_of(self, row):
-        """x, topk_ids and topk_weights of one row: views into the RecvArena. x is a tuple:
-        (bf16 [n, H],) or, with fp8 activations on the wire, (e4m3 codes, scales)."""
+        """The arrived message of one row as tensors over the receive arena, without copying:
+        (activations, ids int32 [n, k], weights fp32 [n, k]); the activations are a tuple,
+        (bf16 [n, H],) or with fp8 on the wire (e4m3 codes, their scales)."""
         g, arena = self.g, self.server.recv
         n, base = row.n_tokens, row.x_ptr - self.server.recv_base
 

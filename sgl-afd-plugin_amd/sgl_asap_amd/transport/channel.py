@@ -211,12 +211,14 @@ class AttnChannel:
         return self
 
     def reconnect(self) -> "AttnChannel":
-        """The only way out of a poisoned channel: new counters, segments and epochs."""
+        """Tear the channel down and connect again with fresh counters, segments and epochs;
+        a channel whose wait was released stays unusable until this is called."""
         self.close()
         return self.connect()
 
     def close(self) -> None:
-        """Release everything (synchronize the streams that used the channel first)."""
+        """Stops the stall watch and frees the host pages and device segments; work still
+        queued on a stream that uses them must have finished (synchronize it first)."""
         if self.watch is not None:
             self.watch.stop()
             self.watch = None
@@ -297,8 +299,9 @@ class AttnChannel:
         return Ticket(slot, seq, layer_id, n_tokens)
 
     def wait(self, ticket: Ticket, stream) -> List[int]:
-        """Enqueue on ``stream`` the waits for every F rank's answer to ``ticket``; returns the
-        device addresses of the partial sums (bf16 [n_tokens, hidden] each, F-rank order)."""
+        """Parks ``stream`` until each F rank's done counter for the ticket's slot reaches the
+        ticket's sequence number, and gives back where those ranks' partial sums lie (one
+        device address per F rank, in rank order, each bf16 [n_tokens, hidden])."""
         self.check()
         g, slot = self.g, ticket.slot
         if self.pump is not None and any(self.flags.load(g.done_off(f, slot)) < ticket.seq for f in range(g.num_f)):
