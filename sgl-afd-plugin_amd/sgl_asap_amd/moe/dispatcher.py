@@ -36,14 +36,19 @@ from .. import _lib
 from .experts import act_scale_shape, quant_act
 from .topk import format_is_standard
 
-# The slot of a whole batch; micro-batch i of two-batch overlap uses slot i.
+# Channel slot used when the batch is not split; with two-batch overlap, micro-batch m
+# travels on slot m.
 SLOT = 0
 
 
 class AsapDispatchOutput(NamedTuple):
-    ticket: Optional[object]  # the pending send, None when ``hidden_states`` is final
+    """What ``dispatch`` hands to ``combine``: either a send still waiting for its answer
+    (``ticket``, with the input tensors its copies read held in ``keepalive``) or, for an empty
+    or chunked batch, the finished output in ``hidden_states``."""
+
+    ticket: Optional[object]
     hidden_states: Optional[torch.Tensor]
-    keepalive: tuple = ()  # the tensors the send's copies read, until the answer
+    keepalive: tuple = ()
 
 
 def combine_parts(parts, shared: Optional[torch.Tensor], n_tokens: int, hidden: int, device) -> torch.Tensor:
