@@ -130,24 +130,6 @@ __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d)
       __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(c), clamp_e4m3(d), lo, true));
 }
 
-// Four fp32 -> four e4m3fn bytes of an MX block with scale code `code`: v / 2^(code - 127),
-// clamped to +-448, rounded to nearest even. v_cvt_scalef32_pk_fp8_f32 divides by the power of
-// two itself (it does not saturate, hence the clamp against 448 * 2^(code - 127) first); the
-// bytes equal pk4_e4m3(v * mx_inv_scale(code), ...) for every code the MX quantizers produce
-// (0-246, code 0 a subnormal scale) and every input, e4m3 rounding midpoints included
-// (checked on the GPU over all block exponents). Used by the gate_up epilogue, where it saves
-// a multiply per value; the activation quantizer keeps the multiply (measured 1.7 us slower
-// with this form).
-__device__ __forceinline__ uint32_t pk4_e4m3_mx(float a, float b, float c, float d, uint32_t code) {
-  typedef short v2s __attribute__((ext_vector_type(2)));
-  const float scale = __uint_as_float(code != 0u ? code << 23 : 0x00400000u);
-  const float lim = kE4m3Max * scale;
-  auto clamp = [lim](float v) { return __builtin_amdgcn_fmed3f(v, -lim, lim); };  // lim >= 0
-  const v2s lo = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(v2s{0, 0}, clamp(a), clamp(b), scale, false);
-  const v2s hi = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(lo, clamp(c), clamp(d), scale, true);
-  return static_cast<uint32_t>(static_cast<uint16_t>(hi[0])) | (static_cast<uint32_t>(static_cast<uint16_t>(hi[1])) << 16);
-}
-
 // f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}): an
 // unrolled loop whose index is a constant expression in the body
 template <int N, int I = 0, typename F>

@@ -349,10 +349,12 @@ __global__ __launch_bounds__(MxTile<WN>::kThreads) void mx_gemm_kernel(MxGemmArg
           }
           amax = fmaxf(amax, xor32(amax, lk));
           const uint32_t code = mx_scale_code(amax, 8);
+          const float inv = mx_inv_scale(code);
           uint32_t d[4];  // h columns 8 q4 + 4 lk .. + 3
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4)
-            d[q4] = pk4_e4m3_mx(h[4 * q4], h[4 * q4 + 1], h[4 * q4 + 2], h[4 * q4 + 3], code);
+            d[q4] = pk4_e4m3(h[4 * q4] * inv, h[4 * q4 + 1] * inv, h[4 * q4 + 2] * inv,
+                             h[4 * q4 + 3] * inv);
           // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
           // 16-31 (the partner's d2, d3 and its own)
           const uint32_t p0 = swap_halves(d[2], d[0], lk);
