@@ -222,3 +222,33 @@ def test_stream_through_the_transport_concurrent_repeated(stream_layer):
                 c.check()
         bad += [(rnd, i) for i, c in enumerate(copies) if not np.array_equal(bits16(c), eager[i % 4])]
     assert not bad, bad
+
+
+def test_direct_calls_on_concurrent_streams(stream_layer):
+    """The four jobs as direct calls of the layer (static walk: the continuous-ring gate_up) on
+    four streams at once, each with its own workspace, three calls per stream per round, five
+    rounds: every output equals the single-stream call's bit for bit."""
+    experts, _, jobs = stream_layer
+    layer = experts[0]
+    say("C3: the four jobs as direct calls on 4 concurrent streams, 5 rounds")
+    dev_jobs = [(x.to(dev()), StandardTopKOutput(w.to(dev()), ids.to(dev()))) for x, ids, w in jobs]
+    ref = [bits16(layer(x, t)) for x, t in dev_jobs]
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream()
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    outs = [torch.empty(x.shape[0], SHAPE.hidden, dtype=torch.bfloat16, device=dev()) for x, _ in dev_jobs]
+    bad = []
+    for rnd in range(5):
+        for o in outs:
+            o.zero_()
+        for s in streams:
+            s.wait_stream(main)
+        for _ in range(3):
+            for (x, t), o, s in zip(dev_jobs, outs, streams):
+                with torch.cuda.stream(s):
+                    layer(x, t, out=o)
+        for s in streams:
+            main.wait_stream(s)
+        torch.cuda.synchronize()
+        bad += [(rnd, j) for j, o in enumerate(outs) if not np.array_equal(bits16(o), ref[j])]
+    assert not bad, bad
