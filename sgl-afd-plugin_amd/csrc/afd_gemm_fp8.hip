@@ -578,13 +578,14 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
           const int row = wm * 64 + i2 * 32 + lr;
           const float amax = fmaxf(amax_l[row], amax_l[kBM + row]);
           const float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
+          const float rsc = 1.0f / sc;  // the quotients below are the IEEE h / sc (div_by)
 #pragma unroll
           for (int jj = 0; jj < 2; ++jj) {
             uint32_t d[4];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4)
-              d[q4] = pk4_e4m3(h[i2][jj][4 * q4] / sc, h[i2][jj][4 * q4 + 1] / sc,
-                               h[i2][jj][4 * q4 + 2] / sc, h[i2][jj][4 * q4 + 3] / sc);
+              d[q4] = pk4_e4m3(div_by(h[i2][jj][4 * q4], sc, rsc), div_by(h[i2][jj][4 * q4 + 1], sc, rsc),
+                               div_by(h[i2][jj][4 * q4 + 2], sc, rsc), div_by(h[i2][jj][4 * q4 + 3], sc, rsc));
             // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
             // 16-31 (the partner's d2, d3 and its own)
             const uint32_t p0 = swap_halves(d[2], d[0], lk);

@@ -91,12 +91,13 @@ __device__ __forceinline__ void quant_fp8_1x128_items(XRow xrow, int64_t quarter
     amax = fmaxf(amax, __shfl_xor(amax, 2));
     float sc = fmaxf(amax, kFp8Eps) / kE4m3Max;
     if (!live) continue;
+    const float rsc = 1.0f / sc;  // the quotients below are the IEEE v / sc (div_by)
     // hardware conversion (v_cvt_pk_fp8_f32): bit-identical to f32_to_e4m3 on the clamped range
     v4i out[2];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(v[i * 4] / sc, v[i * 4 + 1] / sc,
-                                                     v[i * 4 + 2] / sc, v[i * 4 + 3] / sc));
+      out[i / 4][i % 4] = static_cast<int>(pk4_e4m3(div_by(v[i * 4], sc, rsc), div_by(v[i * 4 + 1], sc, rsc),
+                                                     div_by(v[i * 4 + 2], sc, rsc), div_by(v[i * 4 + 3], sc, rsc)));
     v4i* dst = reinterpret_cast<v4i*>(q + row * cols + cq * kMxBlock);
     dst[0] = out[0];
     dst[1] = out[1];
