@@ -1,0 +1,89 @@
+"""CPU: the FP8 quantizers' quotient (``div_by`` in csrc/afd_common.h) against IEEE division.
+
+The kernels compute v / s for every value of a 1x128 group as y = 1 / s (an IEEE division,
+once per group), q0 = RN(v y), r = fma(-q0, s, v), q = fma(r, y, q0), sign of v. Here fma is
+evaluated exactly (rationals) and rounded once to float32, and q is compared bit for bit with
+numpy's float32 division (IEEE round-to-nearest-even) on random operands, operands whose
+quotient lies next to a float32 rounding midpoint, the FP8 quantizers' extreme scales, and
+zeros of both signs. The GPU build was also checked on every pair of fp32 significands."""
+
+from fractions import Fraction
+
+import numpy as np
+
+F32_MIN_NORMAL = Fraction(2) ** -126
+
+
+def rn32(v: Fraction) -> np.float32:
+    """The float32 nearest to the rational v, ties to even (normal range)."""
+    f = np.float32(float(v))  # within one float32 step of the answer
+    best = None
+    for c in (np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))):
+        d = abs(Fraction(float(c)) - v)
+        if best is None or d < best[0] or (d == best[0] and (int(c.view(np.uint32)) & 1) == 0):
+            best = (d, c)
+    return np.float32(best[1])
+
+
+def fma(a, b, c) -> np.float32:
+    return rn32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def div_by(v: np.float32, s: np.float32, y: np.float32) -> np.float32:
+    q0 = np.float32(v * y)
+    r = fma(-q0, s, v)
+    q = fma(r, y, q0)
+    return np.copysign(q, v).astype(np.float32)
+
+
+def check(vs, ss):
+    bad = []
+    for v, s in zip(vs, ss):
+        v, s = np.float32(v), np.float32(s)
+        y = np.float32(np.float32(1.0) / s)
+        got, want = div_by(v, s, y), np.float32(v / s)
+        if got.view(np.uint32) != want.view(np.uint32):
+            bad.append((float(v), float(s), float(got), float(want)))
+    return bad
+
+
+def test_rn32_rounds_to_nearest_even():
+    one = Fraction(1)
+    ulp = Fraction(2) ** -23
+    assert rn32(one + ulp / 2) == np.float32(1.0)  # tie -> even
+    assert rn32(one + 3 * ulp / 2) == np.float32(1.0 + 2 * float(ulp))
+    assert rn32(one + ulp / 2 + Fraction(1, 2**60)) == np.float32(1.0 + float(ulp))
+
+
+def test_random_operands_of_fp8_groups():
+    rng = np.random.default_rng(5)
+    amax = np.exp2(rng.uniform(-20, 20, 3000)).astype(np.float32)
+    s = (np.maximum(amax, np.float32(1e-10)) / np.float32(448.0)).astype(np.float32)
+    v = (amax * rng.uniform(-1, 1, 3000)).astype(np.float32)
+    assert not check(v, s)
+
+
+def test_quotients_next_to_rounding_midpoints():
+    rng = np.random.default_rng(6)
+    vs, ss = [], []
+    for _ in range(1500):
+        s = np.float32(rng.uniform(1, 2))
+        q = np.float32(rng.uniform(1, 2))
+        mid = (Fraction(float(q)) + Fraction(float(np.nextafter(q, np.float32(3))))) / 2
+        for t in (-2, -1, 0, 1, 2):  # v whose exact quotient is at or beside the midpoint
+            v = rn32(mid * Fraction(float(s))) if t == 0 else np.float32(
+                float(rn32(mid * Fraction(float(s)))) * (1 + t * 2.0**-24))
+            vs.append(v)
+            ss.append(s)
+    assert not check(vs, ss)
+
+
+def test_extreme_scales_and_zeros():
+    s_min = np.float32(np.float32(1e-10) / np.float32(448.0))
+    cases = [(0.0, 1.0), (-0.0, 1.0), (0.0, float(s_min)), (-0.0, 3.5), (448.0, 1.0),
+             (-448.0, 1.0), (float(s_min) * 448, float(s_min)), (1e-30, float(s_min)),
+             (3.0e38, 1.0e30), (-1.5, 1.3333334)]
+    bad = check([c[0] for c in cases], [c[1] for c in cases])
+    assert not bad, bad
+    z = div_by(np.float32(-0.0), np.float32(2.0), np.float32(0.5))
+    assert z == 0 and np.signbit(z)
