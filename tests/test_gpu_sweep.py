@@ -54,7 +54,8 @@ MANY_TILE_CASES = 12
 
 def draw_many_tiles(case: int) -> dict:
     """Shapes where every GEMM workgroup takes several tiles (hidden of 3 K stages and more
-    runs the continuous-ring gate_up), with both tile walks and bf16 activations."""
+    runs the continuous-ring gate_up), with both tile walks, bf16 activations and the three
+    activations."""
     rng = random.Random(8100 + case)
     num_experts = rng.choice([16, 32, 64])
     num_local = rng.randint(num_experts // 4, num_experts)
@@ -70,13 +71,15 @@ def draw_many_tiles(case: int) -> dict:
         zipf=rng.choice([None, 1.2]),
         walk=rng.choice(["static", "dynamic"]),
         act_format=rng.choice([None, None, "bf16"]),
+        act=rng.choice(["silu", "silu", "situ", "limit"]),
     )
 
 
 @pytest.mark.parametrize("case", range(MANY_TILE_CASES))
 def test_random_layer_many_tiles(case):
     s = draw_many_tiles(case)
+    extra = {"situ": dict(situ=(1.702, 7.0)), "limit": dict(swiglu_limit=7.0)}.get(s["act"], {})
     experts, out, ref, parts, (x, ids, w) = run_case(
         s["hidden"], s["inter"], s["num_experts"], s["e_lo"], s["num_local"], s["k"], s["n"], s["fmt"],
-        9500 + case, zipf=s["zipf"], walk=s["walk"], act_format=s["act_format"])
+        9500 + case, zipf=s["zipf"], walk=s["walk"], act_format=s["act_format"], **extra)
     assert_close(out, ref, ids.numpy(), range(s["e_lo"], s["e_lo"] + s["num_local"]))
