@@ -10,7 +10,8 @@ the oracle to run the whole job:
 * the job read from a device descriptor equals the by-value call;
 and tokens of a few experts against the oracle on the dequantized weights (rel-L2 1e-2):
 for the MXFP4 layer the tokens of 4 of its experts, for the FP8 block layer (every expert
-local, 8 per token) the tokens whose 8 experts are all among its 16 most used."""
+local, 8 per token) the tokens whose 8 experts are all among its 16 most used; both again
+with each model family's own activation (DeepSeek-V4: SwiGLU with a limit; ERNIE: SiTU)."""
 
 from concurrent.futures import ThreadPoolExecutor
 
@@ -87,8 +88,39 @@ def test_subset_against_oracle(layer):
     expert), against the oracle run with those 4 experts only: the oracle's weight
     quantization of all 64 experts would take minutes on the CPU."""
     shape, experts, (w13, w2), (xc, idsc, wc), _, out = layer
+    subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
+
+
+# the activation each model family runs its experts with: DeepSeek-V4's FusedMoE passes its
+# swiglu_limit (P/srt/models/deepseek_v4.py:63), ERNIE 5.5's SiTU (P/srt/models/ernie55.py:43-55);
+# the limit is lower than a model's so that it clamps a good share of these synthetic gate and
+# up values (N(0, ~1.3)), not only their far tails
+MODEL_ACTIVATION = {
+    "dsv4_rank": (dict(swiglu_limit=1.5), dict(activation="swiglu_limit", act_limit=1.5)),
+    "ernie_fp8": (dict(activation="situ", gemm1_alpha=1.702, gemm1_clamp_limit=7.0),
+                  dict(activation="situ", act_alpha=1.702, act_limit=7.0)),
+}
+
+
+def test_subset_against_oracle_with_model_activation(layer):
+    """The same full-size job through the same packed weights with the model family's own
+    activation (the gate_up kernels' constant-taking form), against the oracle subset."""
+    shape, experts, (w13, w2), (xc, idsc, wc), job, _ = layer
+    kw, oact = MODEL_ACTIVATION[shape.name]
+    say(f"{shape.name}: full-size job with {kw}")
+    act_experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, experts.weights,
+                             n_max=shape.tokens, **kw)
+    out = call(act_experts, *job)
+    assert not torch.equal(out, layer[5])  # the activation took effect
+    subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out, oact)
+
+
+def subset_against_oracle(shape, weights, job, out, oact=None):
+    w13, w2 = weights
+    xc, idsc, wc = job
+    oact = oact or {}
     if shape.fmt != "mxfp4":
-        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
+        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out, oact=oact)
     say(f"{shape.name}: tokens of 4 experts against the oracle")
     lo, keep = shape.local.start, 4
     ids = idsc.numpy()
@@ -101,7 +133,7 @@ def test_subset_against_oracle(layer):
     c13, s13 = F.mx_quantize(w13[:keep].numpy(), "e2m1")
     c2, s2 = F.mx_quantize(w2[:keep].numpy(), "e2m1")
     ref = OX.moe_ffn(xc[sub], ids[sub].astype(np.int32), wc.numpy()[sub].astype(np.float32),
-                     F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1"), lo, act="mxfp8")
+                     F.mx_dequantize(c13, s13, "e2m1"), F.mx_dequantize(c2, s2, "e2m1"), lo, act="mxfp8", **oact)
     got = bits16(out)[sub]
     err = rel_l2(F.bf16_to_f32(got), F.bf16_to_f32(ref))
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
@@ -109,7 +141,7 @@ def test_subset_against_oracle(layer):
     assert not got[~has_kept[sub]].any()  # tokens with no local expert are exactly 0
 
 
-def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
+def fp8_subset_against_oracle(shape, weights, job, out, keep=16, oact=None):
     """The FP8 block layer has every expert local and 8 per token, so no token stays within
     4 experts: take the tokens whose 8 experts are all among the ``keep`` most used, renumber
     those experts 0..keep-1 (a token's result does not depend on the numbering: its pairs,
@@ -137,7 +169,7 @@ def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
     w13d = np.stack([p[0] for p in parts])
     w2d = np.stack([p[1] for p in parts])
     ids = table[rel[sub]].astype(np.int32)
-    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="fp8_1x128")
+    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="fp8_1x128", **(oact or {}))
     err = rel_l2(F.bf16_to_f32(bits16(out)[sub]), F.bf16_to_f32(ref))
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
     assert err <= 1e-2
