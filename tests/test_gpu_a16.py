@@ -316,8 +316,37 @@ def test_dsv4_a16_subset_against_oracle(dsv4_a16):
     token): the tokens whose 8 experts are all among the 16 most used, those experts renumbered
     for the oracle (a token's result does not depend on the numbering)."""
     shape, experts, (w13, w2), (xc, idsc, wc), _, out = dsv4_a16
+    a16_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
+
+
+# each model family's activation (DeepSeek-V4's swiglu_limit, P/srt/models/deepseek_v4.py:63, set
+# low enough to clamp many of these synthetic values; ERNIE 5.5's SiTU, P/srt/models/ernie55.py:43-55)
+MODEL_ACTIVATION = {
+    "dsv4_rank": (dict(swiglu_limit=1.5), dict(activation="swiglu_limit", act_limit=1.5)),
+    "ernie_fp8": (dict(activation="situ", gemm1_alpha=1.702, gemm1_clamp_limit=7.0),
+                  dict(activation="situ", act_alpha=1.702, act_limit=7.0)),
+}
+
+
+def test_a16_full_size_with_model_activation(dsv4_a16):
+    """The full-size job with bf16 activations and the model family's own activation, through
+    the same packed weights, against the oracle subset."""
+    shape, experts, (w13, w2), (xc, idsc, wc), job, base = dsv4_a16
+    kw, oact = MODEL_ACTIVATION[shape.name]
+    say(f"{shape.name} bf16 activations, full size, {kw}")
+    act_experts = AfdExperts(shape.num_experts, shape.top_k, 0, shape.local, experts.weights,
+                             n_max=shape.tokens, act_format="bf16", **kw)
+    out = call(act_experts, *job)
+    assert not torch.equal(out, base)  # the activation took effect
+    a16_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out, oact)
+
+
+def a16_subset_against_oracle(shape, weights, job, out, oact=None):
+    w13, w2 = weights
+    xc, idsc, wc = job
+    oact = oact or {}
     if shape.fmt != "mxfp4":
-        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out)
+        return fp8_subset_against_oracle(shape, (w13, w2), (xc, idsc, wc), out, oact=oact)
     say(f"{shape.name} W4A16: tokens of 4 experts against the oracle")
     lo, keep = shape.local.start, 4
     ids = idsc.numpy()
@@ -329,7 +358,7 @@ def test_dsv4_a16_subset_against_oracle(dsv4_a16):
     assert len(sub) >= 256
     w13d, w2d = mx_deq(w13[:keep], w2[:keep])
     ref = OX.moe_ffn(xc[sub], ids[sub].astype(np.int32), wc.numpy()[sub].astype(np.float32), w13d, w2d, lo,
-                     act="bf16")
+                     act="bf16", **oact)
     got = bits16(out)[sub]
     err = rel_l2(F.bf16_to_f32(got), F.bf16_to_f32(ref))
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
@@ -337,7 +366,7 @@ def test_dsv4_a16_subset_against_oracle(dsv4_a16):
     assert not got[~has_kept[sub]].any()
 
 
-def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
+def fp8_subset_against_oracle(shape, weights, job, out, keep=16, oact=None):
     w13, w2 = weights
     xc, idsc, wc = job
     rel = idsc.numpy() - shape.local.start
@@ -350,7 +379,7 @@ def fp8_subset_against_oracle(shape, weights, job, out, keep=16):
     assert len(sub) >= 128
     w13d, w2d = fp8_deq(w13[chosen], w2[chosen])
     ids = table[rel[sub]].astype(np.int32)
-    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="bf16")
+    ref = OX.moe_ffn(xc[sub], ids, wc.numpy()[sub].astype(np.float32), w13d, w2d, 0, act="bf16", **(oact or {}))
     err = rel_l2(F.bf16_to_f32(bits16(out)[sub]), F.bf16_to_f32(ref))
     say(f"  {len(sub)} tokens, rel_l2 = {err:.2e}")
     assert err <= REL_L2_TOL
