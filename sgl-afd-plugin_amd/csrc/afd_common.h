@@ -125,15 +125,18 @@ __device__ __forceinline__ float xor32(float v, int lk) {
 
 // x / s rounded to nearest even, bit for bit the IEEE quotient, given y = 1 / s (itself the
 // IEEE quotient, computed once per divisor): q0 = x y, then one correction with the exact
-// residual x - q0 s (Markstein's division step), and the sign of x (so -0 / s stays -0).
-// Checked on the GPU for all 2^46 pairs of fp32 significands in [1, 2); scaling x and s by
-// powers of two scales every step exactly, which carries it to every normal operand, and the
-// FP8 quantizers' operands stay normal wherever the e4m3 code is not zero (s >= 1e-10 / 448).
-// Three VALU operations per quotient instead of the ten of a full division.
+// residual x - q0 s (Markstein's division step). The residual is formed negated,
+// t = q0 s - x, and the correction adds -t y: the negations are operand modifiers, and a zero x
+// keeps its sign through both fused steps (-0 / s stays -0; for any other x a zero residual
+// leaves q0 unchanged whatever its sign). Checked on the GPU for all 2^46 pairs of fp32
+// significands in [1, 2); scaling x and s by powers of two scales every step exactly, which
+// carries it to every normal operand, and the FP8 quantizers' operands stay normal wherever the
+// e4m3 code is not zero (s >= 1e-10 / 448). Three VALU operations per quotient instead of the
+// ten of a full division.
 __device__ __forceinline__ float div_by(float x, float s, float y) {
   const float q0 = x * y;
-  const float r = __builtin_fmaf(-q0, s, x);
-  return __builtin_copysignf(__builtin_fmaf(r, y, q0), x);
+  const float t = __builtin_fmaf(q0, s, -x);
+  return __builtin_fmaf(-t, y, q0);
 }
 
 // Four clamped fp32 -> four e4m3fn bytes (element i in byte i).

@@ -1,7 +1,7 @@
 """CPU: the FP8 quantizers' quotient (``div_by`` in csrc/afd_common.h) against IEEE division.
 
 The kernels compute v / s for every value of a 1x128 group as y = 1 / s (an IEEE division,
-once per group), q0 = RN(v y), r = fma(-q0, s, v), q = fma(r, y, q0), sign of v. Here fma is
+once per group), q0 = RN(v y), t = fma(q0, s, -v), q = fma(-t, y, q0). Here fma is
 evaluated exactly (rationals) and rounded once to float32, and q is compared bit for bit with
 numpy's float32 division (IEEE round-to-nearest-even) on random operands, operands whose
 quotient lies next to a float32 rounding midpoint, the FP8 quantizers' extreme scales, and
@@ -26,14 +26,20 @@ def rn32(v: Fraction) -> np.float32:
 
 
 def fma(a, b, c) -> np.float32:
-    return rn32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+    """RN(a b + c) of float32 operands. An exact zero is -0 only when a b and c are both
+    zeros of negative sign (IEEE 754: an exact zero sum of opposite signs is +0 under
+    round-to-nearest, and x + x keeps the sign of x)."""
+    exact = Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c))
+    if exact == 0:
+        prod_is_neg_zero = (a == 0 or b == 0) and bool(np.signbit(a)) != bool(np.signbit(b))
+        return np.float32(-0.0) if prod_is_neg_zero and c == 0 and np.signbit(c) else np.float32(0.0)
+    return rn32(exact)
 
 
 def div_by(v: np.float32, s: np.float32, y: np.float32) -> np.float32:
     q0 = np.float32(v * y)
-    r = fma(-q0, s, v)
-    q = fma(r, y, q0)
-    return np.copysign(q, v).astype(np.float32)
+    t = fma(q0, s, -v)
+    return fma(-t, y, q0)
 
 
 def check(vs, ss):
@@ -53,6 +59,16 @@ def test_rn32_rounds_to_nearest_even():
     assert rn32(one + ulp / 2) == np.float32(1.0)  # tie -> even
     assert rn32(one + 3 * ulp / 2) == np.float32(1.0 + 2 * float(ulp))
     assert rn32(one + ulp / 2 + Fraction(1, 2**60)) == np.float32(1.0 + float(ulp))
+
+
+def test_fma_model_signed_zeros():
+    f32 = np.float32
+    assert np.signbit(fma(f32(-0.0), f32(2.0), f32(-0.0)))  # -0 + -0
+    assert not np.signbit(fma(f32(0.0), f32(2.0), f32(-0.0)))  # +0 + -0
+    assert not np.signbit(fma(f32(-0.0), f32(-2.0), f32(-0.0)))  # +0 + -0
+    assert not np.signbit(fma(f32(1.5), f32(2.0), f32(-3.0)))  # exact cancellation
+    assert not np.signbit(fma(f32(-1.5), f32(2.0), f32(3.0)))
+    assert fma(f32(3.0), f32(1.0 / 3.0), f32(-1.0)) == f32(2.0**-25)  # unrounded product
 
 
 def test_random_operands_of_fp8_groups():
@@ -87,3 +103,5 @@ def test_extreme_scales_and_zeros():
     assert not bad, bad
     z = div_by(np.float32(-0.0), np.float32(2.0), np.float32(0.5))
     assert z == 0 and np.signbit(z)
+    z = div_by(np.float32(0.0), np.float32(2.0), np.float32(0.5))
+    assert z == 0 and not np.signbit(z)
