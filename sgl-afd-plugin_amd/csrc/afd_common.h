@@ -145,6 +145,14 @@ __device__ __forceinline__ uint32_t pk4_e4m3(float a, float b, float c, float d)
   return static_cast<uint32_t>(
       __builtin_amdgcn_cvt_pk_fp8_f32(clamp_e4m3(c), clamp_e4m3(d), lo, true));
 }
+// pk4_e4m3 for values known to lie below 464 in magnitude, without the clamp: round to
+// nearest even already takes (448, 464) to 448. The FP8 1x128 quotients h / s with
+// s = RN(amax / 448) stay below 448 (1 + 2^-23): the FP8 gate_up epilogue converts them so (the
+// activation quantizer keeps the clamp, which measured faster there).
+__device__ __forceinline__ uint32_t pk4_e4m3_near(float a, float b, float c, float d) {
+  int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
+}
 
 // f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}): an
 // unrolled loop whose index is a constant expression in the body

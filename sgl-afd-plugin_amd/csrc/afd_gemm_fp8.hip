@@ -584,7 +584,7 @@ __global__ __launch_bounds__(Tile::kThreads) void fp8_gemm_kernel(Fp8GemmArgs p)
             uint32_t d[4];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4)
-              d[q4] = pk4_e4m3(div_by(h[i2][jj][4 * q4], sc, rsc), div_by(h[i2][jj][4 * q4 + 1], sc, rsc),
+              d[q4] = pk4_e4m3_near(div_by(h[i2][jj][4 * q4], sc, rsc), div_by(h[i2][jj][4 * q4 + 1], sc, rsc),
                                div_by(h[i2][jj][4 * q4 + 2], sc, rsc), div_by(h[i2][jj][4 * q4 + 3], sc, rsc));
             // lane half 0 takes columns 0-15 (its d0, d1 and the partner's), half 1 columns
             // 16-31 (the partner's d2, d3 and its own)
