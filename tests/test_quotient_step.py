@@ -105,3 +105,19 @@ def test_extreme_scales_and_zeros():
     assert z == 0 and np.signbit(z)
     z = div_by(np.float32(0.0), np.float32(2.0), np.float32(0.5))
     assert z == 0 and not np.signbit(z)
+
+
+def test_quotients_stay_below_the_e4m3_rounding_limit():
+    """The FP8 gate_up epilogue converts v / s to e4m3 without a clamp: with s = RN(max(amax,
+    1e-10) / 448) every |v| <= amax gives |v / s| <= 448 (1 + 2^-23), and round to nearest
+    even takes all of (448, 464) to 448 (the codes of both conversions compared bit for bit on
+    the GPU's layer cases)."""
+    rng = np.random.default_rng(7)
+    amax = np.concatenate([np.exp2(rng.uniform(-40, 40, 200000)),
+                           np.float32(448.0) * np.exp2(rng.integers(-30, 30, 2000)).astype(np.float64)])
+    amax = amax.astype(np.float32)
+    s = (np.maximum(amax, np.float32(1e-10)) / np.float32(448.0)).astype(np.float32)
+    q = (amax / s).astype(np.float32)  # numpy float32 division: IEEE round to nearest even
+    limit = np.float32(448.0) * (1 + np.float32(2.0**-23))
+    assert q.max() <= limit < 464
+    assert (q > 448).any()  # the overshoot does occur: the conversion must round it to 448
