@@ -7,6 +7,8 @@
   ones (expert e holds pool member e % 3), so the oracle needs only the pool's weights; an
   offset that wrapped at 2^32 would read the middle of another expert's image.
 * the intermediate size at its limit (16384) with a small hidden size.
+* the largest job (131071 tokens) at hidden 16384: token rows at 32-bit byte offsets up to
+  2^31 (fp8 rows) and 2^32 (bf16 rows) minus a row.
 
 Both weight formats, with fp8 and with bf16 activations; the bars of the other layer tests
 (rel-L2 <= 1e-2, tokens with no local expert exactly zero). The weights are drawn so that
@@ -166,3 +168,30 @@ def test_largest_inter(fmt, act_format):
     ref = OX.moe_ffn(x, ids.numpy(), w.numpy(), w13.cpu().numpy(), w2.cpu().numpy(), 1,
                      act=oracle_act(fmt, act_format))
     assert_close(out, ref, ids.numpy(), range(1, 3))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("act_format", [None, "bf16"])
+@pytest.mark.parametrize("fmt", ["mxfp4", "fp8_block"])
+def test_largest_job_at_the_hidden_limit(fmt, act_format):
+    """131071 tokens (the most a call takes) of hidden 16384: token rows at byte offsets up
+    to 2^31 (fp8 rows) and 2^32 (bf16 rows) minus a row. The first and last 1000 tokens, run
+    as a job of their own, give the same rows bit for bit, and the last 64 match the oracle."""
+    hidden, inter, num, k, n = HIDDEN, 128, 8, 2, 131071
+    say(f"largest job fmt={fmt} act_format={act_format} H={hidden} I={inter} E={num} k={k} n={n}")
+    w13, w2 = exact_weights(fmt, num, hidden, inter, seed=83, device=dev())
+    gen = W.generator(dev(), 84)
+    x = W.tokens(n, hidden, gen, dev())
+    ids, w = W.route_uniform(n, num, k, gen, dev())
+    experts = AfdExperts(num, k, 0, range(num), packed(fmt, w13, w2), n_max=n, act_format=act_format)
+    out = experts(x, StandardTopKOutput(w, ids))
+    ends = torch.cat([torch.arange(1000), torch.arange(n - 1000, n)]).to(dev())
+    sub = experts(x[ends].contiguous(), StandardTopKOutput(w[ends].contiguous(), ids[ends].contiguous()))
+    torch.cuda.synchronize()
+    assert torch.equal(sub.view(torch.int16), out[ends].view(torch.int16))
+    last = slice(n - 64, n)
+    xl, idl, wl = x[last].cpu(), ids[last].cpu().numpy(), w[last].cpu().numpy()
+    got = out[last]
+    del experts, out, sub, x
+    ref = OX.moe_ffn(xl, idl, wl, w13.cpu().numpy(), w2.cpu().numpy(), 0, act=oracle_act(fmt, act_format))
+    assert_close(got, ref, idl, range(num))
